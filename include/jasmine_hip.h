@@ -1,0 +1,250 @@
+/*
+ * jasmine_hip.h -- C ABI of libjasmine_hip.so, the MI355X (gfx950) implementation of
+ * jasmine's transformer inference hot path.
+ *
+ * The reference (a header-only C++20 CPU library) has no FFI of its own: its boundary is
+ * the template API.  These entry points are what that API's evaluation points lower to;
+ * each declaration names the reference code it replaces (file:line into the jasmine
+ * sources).  The C++20 headers under jasmine_amd/include/ (mat_t.hpp, mat_express_t.hpp,
+ * mat_net_t.hpp, mat_mha_t.hpp, ...) are the only intended direct callers besides the
+ * test/bench bindings.
+ *
+ * Conventions
+ *  - plain pointers and sizes; every pointer argument named d_* is device memory;
+ *  - the caller owns every buffer;
+ *  - every call is asynchronous on `stream` (a hipStream_t; NULL = the library stream);
+ *  - every call returns a jas_status; jas_last_error() gives the message.  The C++
+ *    wrapper maps JAS_ERR_INVALID to std::invalid_argument, JAS_ERR_RANGE to
+ *    std::out_of_range and everything else to std::runtime_error, the exception types the
+ *    reference throws (mat_express_t.hpp:711, mat_mha_t.hpp:240, mat_RoPE_t.hpp:57).
+ */
+#ifndef JASMINE_HIP_H
+#define JASMINE_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    JAS_OK = 0,
+    JAS_ERR_INVALID = 1, /* shape / argument mismatch  -> std::invalid_argument */
+    JAS_ERR_RUNTIME = 2, /* state error                 -> std::runtime_error    */
+    JAS_ERR_HIP = 3,     /* HIP runtime failure                                  */
+    JAS_ERR_OOM = 4,     /* device allocation failed                             */
+    JAS_ERR_RANGE = 5    /* index / capacity overflow   -> std::out_of_range     */
+} jas_status;
+
+typedef void *jas_stream_t;
+
+typedef enum { JAS_F32 = 0, JAS_F64 = 1, JAS_I32 = 2, JAS_BF16 = 3 } jas_dtype;
+
+/* ------------------------------------------------------------------ runtime */
+/* Device selection and library stream creation.  Storage behind mat_t<T>
+ * (mat_t.hpp:53-69 new[]/memset, :30-42 delete[]). */
+jas_status jas_init(int device);
+const char *jas_last_error(void);
+const char *jas_version(void);
+jas_stream_t jas_default_stream(void);
+jas_status jas_malloc(void **d_ptr, size_t bytes);          /* mat_t.hpp:67 new[] */
+jas_status jas_free(void *d_ptr);                            /* mat_t.hpp:39 delete[] */
+jas_status jas_memset(void *d_ptr, int value, size_t bytes, jas_stream_t stream); /* mat_t.hpp:68 memset */
+jas_status jas_memcpy_h2d(void *d_dst, const void *src, size_t bytes, jas_stream_t stream);
+jas_status jas_memcpy_d2h(void *dst, const void *d_src, size_t bytes, jas_stream_t stream);
+jas_status jas_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes, jas_stream_t stream);
+jas_status jas_synchronize(jas_stream_t stream);
+
+/* ------------------------------------------------------------------ L1 expressions */
+/* A leaf of an expression tree: a mat_t, or a mat_view_t of one.  Element (i, j) of the
+ * leaf is read exactly as jasmine reads it:
+ *   view (mat_view_t.hpp:28-38):  (a, b) = transposed ? (j + coff, i + roff) : (i + roff, j + coff)
+ *   matrix (mat_t.hpp:312-320):    a %= rows; b %= cols;
+ *                                  addr = row_first ? a * cols + b : b * rows + a
+ * which also gives jasmine's modulo broadcasting of smaller operands. */
+typedef struct {
+    const void *d_data;
+    int32_t dtype;       /* jas_dtype of the stored elements */
+    int32_t rows, cols;  /* dims of the underlying matrix (the modulo bases) */
+    int32_t row_first;   /* storage order of the underlying matrix (mat_t.hpp:27) */
+    int32_t roff, coff;  /* view offsets (0 for a plain mat_t) */
+    int32_t transposed;  /* view transposition flag (mat_view_t.hpp:19) */
+    int32_t vrows, vcols;/* logical dims of the leaf as seen by the expression */
+} jas_leaf;
+
+/* Postfix instructions.  Each instruction's `dtype` is the C++ ele_type of that node
+ * (std::common_type promotion, mat_express_t.hpp:41-44); its result is rounded to that
+ * type before a parent consumes it, as the typed work(lval_base_type, rval_base_type)
+ * parameters do in jasmine. */
+typedef enum {
+    JAS_OP_LEAF = 0,   /* push leaf[arg]                                            */
+    JAS_OP_CONST = 1,  /* push imm (a scalar operand, stored as 1x1 mat_t<T>)        */
+    JAS_OP_ADD = 2,    /* mat_add_t  mat_express_t.hpp:188-223                        */
+    JAS_OP_SUB = 3,    /* mat_sub_t  :253-286                                         */
+    JAS_OP_MUL = 4,    /* mat_mul_t  :288-321                                         */
+    JAS_OP_DIV = 5,    /* mat_div_t  :323-358                                         */
+    JAS_OP_GT = 6,     /* mat_greater_t :119-151 (bool result in node dtype)          */
+    JAS_OP_LT = 7,     /* mat_less_t :153-186                                         */
+    JAS_OP_EXP = 8,    /* mat_exp_t :439-469 (exp in the operand's type)              */
+    JAS_OP_SIGMOID = 9,/* mat_sigmoid_t :479-509 (1.0/(1.0+exp(-x)), exp in operand type) */
+    JAS_OP_TANH = 10,  /* new node: tanh in operand type                              */
+    JAS_OP_GELU = 11,  /* new node: 0.5x(1+tanh(sqrt(2/pi)(x+0.044715x^3)))           */
+    JAS_OP_SILU = 12,  /* new node: x/(1+exp(-x))                                     */
+    JAS_OP_SQRT = 13,  /* sqrt(mat) :804-813                                           */
+    JAS_OP_POW = 14,   /* pow(mat, p) :587-596 (std::pow(x, double p))                */
+    JAS_OP_NEG = 15    /* unary minus                                                  */
+} jas_ew_op;
+
+/* `arg`: leaf index for JAS_OP_LEAF; for binary ops bit 0 set means the right operand
+ * was pushed first (Sethi-Ullman order keeps the stack within JAS_EW_MAX_STACK). */
+typedef struct {
+    int32_t op;
+    int32_t dtype;
+    int32_t arg;
+    int32_t pad;
+    double imm;
+} jas_ew_ins;
+
+#define JAS_EW_MAX_INS 48
+#define JAS_EW_MAX_LEAVES 8
+#define JAS_EW_MAX_STACK 4
+
+/* Materialise an expression tree: mat_express_2_param_stable_t::clone / operator mat_t
+ * (mat_express_t.hpp:96-112, 416-432).  Output is a dense row-major [rows, cols] matrix
+ * of out_dtype (one fused kernel, one HBM pass over the leaves). */
+jas_status jas_ew_eval(const jas_ew_ins *prog, int n_ins, const jas_leaf *leaves, int n_leaves,
+                       void *d_out, int32_t out_dtype, int rows, int cols, jas_stream_t stream);
+
+/* Reductions over a leaf (mat_express_t.hpp:511-628).  op: 0 sum, 1 max, 2 mean.
+ * axis: 0 = per row (hsum/hmax/hmean -> [rows,1]), 1 = per column (vsum/vmean -> [1,cols]),
+ * 2 = whole matrix (sum/max/mean -> one value).  Accumulation in out_dtype. */
+jas_status jas_reduce(const jas_leaf *in, int op, int axis, void *d_out, int32_t out_dtype,
+                      jas_stream_t stream);
+
+/* ------------------------------------------------------------------ L2 row ops */
+/* All row ops act on `n_vec` vectors of length `len`; element e of vector v is read from
+ * x[v * x_vstride + e * estride] and written to y[v * y_vstride + e * estride] (row-wise:
+ * vstride=len, estride=1; column-wise on a row-major [len, n_vec] matrix: vstride=1,
+ * estride=n_vec). */
+
+/* hsoftmax (mat_express_t.hpp:681-694) / hsoftmax_net_t::forward (mat_net_t.hpp:273-279):
+ * y = exp(x - max) / sum, one HBM read + one write per vector. */
+jas_status jas_softmax(const float *d_x, float *d_y, int n_vec, int len, long x_vstride, long y_vstride,
+                       long estride, jas_stream_t stream);
+/* whole-matrix softmax mat_softmax_t (mat_express_t.hpp:630-679), dense n floats */
+jas_status jas_softmax_global(const float *d_x, float *d_y, long n, jas_stream_t stream);
+/* LayerNorm: y = (x - mean) / sqrt(var + eps) * g[e] + b[e]  (population variance).
+ * eps = 0 with column layout is jasmine's layer_norm_net_t::forward (mat_net_t.hpp:209-225).
+ * g / b may be NULL (1 / 0). */
+jas_status jas_layernorm(const float *d_x, float *d_y, int n_vec, int len, long x_vstride, long y_vstride,
+                         long estride, float eps, const float *d_g, const float *d_b, jas_stream_t stream);
+/* RMSNorm (new): y = x / sqrt(mean(x^2) + eps) * g[e] */
+jas_status jas_rmsnorm(const float *d_x, float *d_y, int n_vec, int len, long x_vstride, long y_vstride,
+                       long estride, float eps, const float *d_g, jas_stream_t stream);
+
+/* ------------------------------------------------------------------ GEMM */
+typedef enum {
+    JAS_ACT_NONE = 0,
+    JAS_ACT_RELU = 1,    /* relu_net_t (x>0)*x, mat_net_t.hpp:146-153 */
+    JAS_ACT_GELU = 2,    /* GPT-2 tanh GELU */
+    JAS_ACT_SILU = 3,
+    JAS_ACT_SIGMOID = 4  /* sigmoid_net_t, mat_net_t.hpp:101-106 */
+} jas_act;
+
+/* C(m, n) = act( sum_k A(m, k) B(k, n) + bias ) (+ C(m, n) if accumulate)
+ *   A(m,k) = A[m*as0 + k*as1], B(k,n) = B[k*bs0 + n*bs1], C(m,n) = C[m*cs0 + n*cs1]
+ * bias_mode: 0 none, 1 bias[m] (weight_net_t bias broadcast over tokens, mat_net_t.hpp:41),
+ *            2 bias[n].
+ * Replaces mat_dot_t (mat_express_t.hpp:696-784) and weight_net_t::forward
+ * (mat_net_t.hpp:38-49).  fp32 MFMA (v_mfma_f32_16x16x4_f32), fp32 accumulate.
+ * `batch` independent problems at element offsets *_bstride (0 = shared operand). */
+jas_status jas_gemm(int M, int N, int K,
+                    const float *d_A, long as0, long as1,
+                    const float *d_B, long bs0, long bs1,
+                    float *d_C, long cs0, long cs1,
+                    const float *d_bias, int bias_mode, int act, int accumulate,
+                    int batch, long a_bstride, long b_bstride, long c_bstride, long bias_bstride,
+                    jas_stream_t stream);
+
+/* ------------------------------------------------------------------ attention */
+/* Causal / full flash attention forward, token-major Q[B,H,Sq,D], K,V[B,H,Sk,D] -> O.
+ * Replaces the materialised S = Q'K / sqrt(d) -> mask -> hsoftmax -> V P' sequence of
+ * mat_head_gen_t::forward (mat_mha_t.hpp:45-74) for dense heads.  Causal aligns the last
+ * query with the last key.  dtype JAS_F32 or JAS_BF16 (bf16 inputs, fp32 accumulate).
+ * D in {32, 64, 128}.  Strides (elements) select the [B,H,S,D] layout of each tensor:
+ * x(b,h,s,:) = x[b*sb + h*sh + s*ss]. */
+jas_status jas_attn_prefill(const void *d_Q, const void *d_K, const void *d_V, void *d_O,
+                            int B, int H, int Sq, int Sk, int D,
+                            long q_sb, long q_sh, long q_ss, long k_sb, long k_sh, long k_ss,
+                            long o_sb, long o_sh, long o_ss,
+                            float scale, int causal, int dtype, jas_stream_t stream);
+/* One-query-per-(b,h) decode step over a KV cache (flash-decoding: split over the keys,
+ * log-sum-exp merge).  q[B,H,D], cache K/V[(b,h)] rows of D at k_sb/k_sh strides,
+ * seqlens[B] = number of valid keys per sequence (device int32).  Equivalent to the last
+ * column of a full recompute (transformer_test.hpp:231-238 recomputes the prefix).
+ * d_work must hold jas_attn_decode_workspace(B, H, D, max_len) bytes. */
+size_t jas_attn_decode_workspace(int B, int H, int D, int max_len);
+jas_status jas_attn_decode(const float *d_q, const float *d_K, const float *d_V, float *d_O,
+                           const int32_t *d_seqlens, int B, int H, int D, int max_len,
+                           long k_sb, long k_sh, float scale, void *d_work, jas_stream_t stream);
+
+/* ------------------------------------------------------------------ RoPE, embeddings, argmax */
+/* jasmine RoPE_net_t::forward (mat_RoPE_t.hpp:166-188) with mat_RoPE_t::init angles
+ * (mat_RoPE_t.hpp:107-131); x, y row-major [d, T] feature-major. */
+jas_status jas_rope_jasmine(const float *d_x, float *d_y, int d, int T, jas_stream_t stream);
+/* LLaMA rotary on interleaved pairs, in place: x[(n * nh + h) * hstride ...], n tokens with
+ * positions pos[n] (device int32), nh heads of dh each, token stride tstride elements. */
+jas_status jas_rope_llama(float *d_x, const int32_t *d_pos, int n, int nh, int dh, long tstride,
+                          float theta, jas_stream_t stream);
+/* out[n][d] = wte[ids[n]] (+ wpe[pos[n]] if d_wpe) -- token embedding gather (new) */
+jas_status jas_embed(const float *d_wte, const float *d_wpe, const int32_t *d_ids, const int32_t *d_pos,
+                     float *d_out, int n, int d, jas_stream_t stream);
+/* argmax over each of n rows of length V (first maximum wins) */
+jas_status jas_argmax(const float *d_x, int n, int V, long ld, int32_t *d_out, jas_stream_t stream);
+/* Seeded N(mean, std) fill, same counter-based generator as the host side. */
+jas_status jas_fill_normal(float *d_x, size_t n, uint64_t seed, uint64_t stream_id, float mean, float std,
+                           jas_stream_t stream);
+
+/* ------------------------------------------------------------------ decoder LM runner */
+/* Decoder-only language model (GPT-2 / LLaMA shapes).  The reference has no token
+ * model (its decode loop is test_transformer_t::predict, transformer_test.hpp:194-242,
+ * which recomputes the whole prefix each step); this runner keeps jasmine's decode
+ * semantics (each step's output = last column of a full recompute) with a KV cache. */
+typedef struct {
+    int32_t kind;      /* 0 GPT-2 (pre-LN, GELU, learned positions, tied head), 1 LLaMA */
+    int32_t n_layer, d_model, n_head, d_ff, vocab, max_ctx, max_batch;
+    float eps, rope_theta;
+} jas_lm_config;
+
+typedef struct jas_lm jas_lm;
+
+jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out);
+jas_status jas_lm_destroy(jas_lm *lm);
+/* Fill every weight N(0, std) from `seed` (norm gains 1, biases 0). */
+jas_status jas_lm_init_random(jas_lm *lm, uint64_t seed, float std);
+/* Weight tensor access by name ("wte", "wpe", "ln1_g", "ln1_b", "w_qkv", "b_qkv", "w_o",
+ * "b_o", "ln2_g", "ln2_b", "w_fc", "b_fc", "w_proj", "b_proj", "w_gate", "w_up", "w_down",
+ * "lnf_g", "lnf_b", "w_head"); layer tensors are stacked [n_layer][...], matrices [out][in].
+ * Returns the device pointer and element count (NULL/0 for tensors the kind lacks). */
+jas_status jas_lm_weight(jas_lm *lm, const char *name, float **d_ptr, size_t *count);
+/* Prefill B prompts of length P (host int32 ids [B][P]) and return the greedy next ids
+ * (host [B]); logits of the last position go to h_logits [B][V] if not NULL. */
+jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_t *h_next, float *h_logits);
+/* One decode step for all B sequences: feeds `h_ids` (host [B], or NULL to feed the
+ * previous step's argmax kept on the device), appends to the KV cache, returns argmax
+ * ids (host [B], NULL = keep on device) and optionally logits [B][V]. */
+jas_status jas_lm_decode(jas_lm *lm, const int32_t *h_ids, int32_t *h_next, float *h_logits);
+/* Run `steps` greedy decode steps without host round trips; ids out [steps][B] (host). */
+jas_status jas_lm_generate(jas_lm *lm, int steps, int32_t *h_ids);
+/* Current sequence length (tokens in the KV cache). */
+int jas_lm_position(jas_lm *lm);
+jas_stream_t jas_lm_stream(jas_lm *lm);
+/* Per-kernel-class GPU time (ms) accumulated with HIP events around every launch on the
+ * runner's stream since the last reset; classes: 0 weight GEMM (decode), 1 attention decode,
+ * 2 other. enable=0 turns event recording off. */
+jas_status jas_lm_profile(jas_lm *lm, int enable, double *ms_by_class, long *launches_by_class);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,410 @@
+// fp32 GEMMs on the CDNA4 matrix cores (north-star item 5).
+//
+// Reference: mat_dot_t::operator() (mat_express_t.hpp:730-736) is a scalar triple loop
+// with sequential-k accumulation, reached from weight_net_t::forward (mat_net_t.hpp:38-49)
+// for every projection and from mat_head_gen_t::forward (mat_mha_t.hpp:53,71).
+//
+// Two kernels:
+//  * gemm_tile_kernel: 128x128x16 LDS-tiled MFMA GEMM (v_mfma_f32_16x16x4_f32) for
+//    prefill-sized problems; any operand strides (transposed views included).
+//  * skinny_kernel: N <= 16 tokens (decode).  The weight matrix is streamed from HBM
+//    straight into MFMA A-operand registers (no LDS), one 16-row tile per wave set, the
+//    K range split across the waves of a workgroup and reduced through LDS, with the
+//    layer's elementwise tail fused into the epilogue (bias, GELU, residual add, SwiGLU,
+//    RoPE + KV-cache append).
+//
+// MFMA 16x16x4 f32 operand layout (lane l of 64): A[i = l%16][kslot = l/16],
+// B[kslot = l/16][j = l%16], D rows 4*(l/16)+r (r = 0..3), column l%16.  Each lane loads
+// a float4 along K; sub-step t of 4 feeds element t, so k-slot s of sub-step t is
+// k = 4s + t -- a permutation of K applied identically to A and B.
+#include "gemm.hpp"
+
+namespace jas {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------- tiled GEMM
+constexpr int TBM = 128, TBN = 128, TBK = 16, TLD = 20;  // LDS row stride (floats)
+
+enum LoadMode : int { LM_KC = 0, LM_OC = 1, LM_GEN = 2 };  // K-contig, outer-contig, generic
+
+// Loads a [128 outer x 16 k] tile of X(o, k) = X[o*so + k*sk] into registers, then LDS
+// rows [o][k] (K-contiguous, padded stride TLD).
+template <int MODE>
+struct TileLoader {
+    float r[8];
+    __device__ __forceinline__ void load(const float *__restrict__ X, long so, long sk, int o0, int k0, int O, int K,
+                                         int tid)
+    {
+        if (MODE == LM_KC) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                int idx = tid + q * 256, o = idx >> 2, kq = (idx & 3) * 4;
+                int go = o0 + o, gk = k0 + kq;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (go < O && gk < K) v = *(const float4 *)(X + (long)go * so + gk);
+                r[4 * q] = v.x; r[4 * q + 1] = v.y; r[4 * q + 2] = v.z; r[4 * q + 3] = v.w;
+            }
+        } else if (MODE == LM_OC) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                int idx = tid + q * 256, k = idx >> 5, oq = (idx & 31) * 4;
+                int go = o0 + oq, gk = k0 + k;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (go < O && gk < K) v = *(const float4 *)(X + (long)gk * sk + go);
+                r[4 * q] = v.x; r[4 * q + 1] = v.y; r[4 * q + 2] = v.z; r[4 * q + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                int idx = tid + q * 256, o = idx >> 4, k = idx & 15;
+                int go = o0 + o, gk = k0 + k;
+                r[q] = (go < O && gk < K) ? X[(long)go * so + (long)gk * sk] : 0.f;
+            }
+        }
+    }
+    __device__ __forceinline__ void store(float *lds, int tid) const
+    {
+        if (MODE == LM_KC) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                int idx = tid + q * 256, o = idx >> 2, kq = (idx & 3) * 4;
+                *(float4 *)(lds + o * TLD + kq) = make_float4(r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]);
+            }
+        } else if (MODE == LM_OC) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                int idx = tid + q * 256, k = idx >> 5, oq = (idx & 31) * 4;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) lds[(oq + e) * TLD + k] = r[4 * q + e];
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                int idx = tid + q * 256, o = idx >> 4, k = idx & 15;
+                lds[o * TLD + k] = r[q];
+            }
+        }
+    }
+};
+
+struct TileArgs {
+    const float *A, *B;
+    float *C;
+    const float *bias;
+    long as0, as1, bs0, bs1, cs0, cs1;
+    long abs_, bbs, cbs, biasbs;
+    int M, N, K;
+    int bias_mode, act, accumulate;
+};
+
+template <int AM, int BMODE, bool C4>
+__global__ void __launch_bounds__(256) gemm_tile_kernel(const TileArgs p)
+{
+    __shared__ float As[TBM * TLD];
+    __shared__ float Bs[TBN * TLD];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int wm = w >> 1, wn = w & 1, r16 = lane & 15, g = lane >> 4;
+    const int m0 = blockIdx.y * TBM, n0 = blockIdx.x * TBN;
+    const long bz = blockIdx.z;
+    const float *A = p.A + bz * p.abs_;
+    const float *B = p.B + bz * p.bbs;
+    float *C = p.C + bz * p.cbs;
+    const float *bias = p.bias ? p.bias + bz * p.biasbs : nullptr;
+
+    TileLoader<AM> la;
+    TileLoader<BMODE> lb;
+    // A(m, k) = A[m*as0 + k*as1]: outer = m.  B(k, n) = B[k*bs0 + n*bs1]: outer = n.
+    la.load(A, p.as0, p.as1, m0, 0, p.M, p.K, tid);
+    lb.load(B, p.bs1, p.bs0, n0, 0, p.N, p.K, tid);
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    for (int k0 = 0; k0 < p.K; k0 += TBK) {
+        __syncthreads();
+        la.store(As, tid);
+        lb.store(Bs, tid);
+        __syncthreads();
+        if (k0 + TBK < p.K) {  // prefetch the next K slab while the matrix cores work
+            la.load(A, p.as0, p.as1, m0, k0 + TBK, p.M, p.K, tid);
+            lb.load(B, p.bs1, p.bs0, n0, k0 + TBK, p.N, p.K, tid);
+        }
+        float4 a[4], b[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = *(const float4 *)(As + (wm * 64 + i * 16 + r16) * TLD + 4 * g);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = *(const float4 *)(Bs + (wn * 64 + j * 16 + r16) * TLD + 4 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[i][j] = mfma4(a[i].x, b[j].x, acc[i][j]);
+                acc[i][j] = mfma4(a[i].y, b[j].y, acc[i][j]);
+                acc[i][j] = mfma4(a[i].z, b[j].z, acc[i][j]);
+                acc[i][j] = mfma4(a[i].w, b[j].w, acc[i][j]);
+            }
+    }
+
+    // epilogue: lane holds rows m = 4g + r of each 16x16 block, column n = r16
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int mb = m0 + wm * 64 + i * 16 + 4 * g, n = n0 + wn * 64 + j * 16 + r16;
+            if (n >= p.N) continue;
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                int m = mb + r;
+                float x = acc[i][j][r];
+                if (bias && m < p.M) x = x + (p.bias_mode == 1 ? bias[m] : bias[n]);
+                v[r] = apply_act(x, p.act);
+            }
+            float *cp = C + (long)mb * p.cs0 + (long)n * p.cs1;
+            if (C4 && mb + 3 < p.M) {  // cs0 == 1: four consecutive rows are contiguous
+                float4 o = make_float4(v[0], v[1], v[2], v[3]);
+                if (p.accumulate) {
+                    float4 c = *(float4 *)cp;
+                    o.x += c.x; o.y += c.y; o.z += c.z; o.w += c.w;
+                }
+                *(float4 *)cp = o;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (mb + r < p.M) {
+                        float *q = cp + (long)r * p.cs0;
+                        *q = p.accumulate ? *q + v[r] : v[r];
+                    }
+            }
+        }
+}
+
+template <int AM, int BMODE>
+static void launch_tile_c(const TileArgs &p, bool c4, dim3 grid, hipStream_t s)
+{
+    if (c4) hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, true>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, false>), grid, dim3(256), 0, s, p);
+}
+
+template <int AM>
+static void launch_tile_b(const TileArgs &p, int bm, bool c4, dim3 grid, hipStream_t s)
+{
+    if (bm == LM_KC) launch_tile_c<AM, LM_KC>(p, c4, grid, s);
+    else if (bm == LM_OC) launch_tile_c<AM, LM_OC>(p, c4, grid, s);
+    else launch_tile_c<AM, LM_GEN>(p, c4, grid, s);
+}
+
+static bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// choose a vector load mode for operand X(o, k) = X[o*so + k*sk] over a batch
+static int pick_mode(const float *X, long so, long sk, int O, int K, long bstride)
+{
+    bool base = al16(X) && (bstride % 4 == 0);
+    if (sk == 1 && K % 4 == 0 && so % 4 == 0 && base) return LM_KC;
+    if (so == 1 && O % 4 == 0 && sk % 4 == 0 && base) return LM_OC;
+    return LM_GEN;
+}
+
+jas_status gemm_general(int M, int N, int K, const float *A, long as0, long as1, const float *B, long bs0, long bs1,
+                        float *C, long cs0, long cs1, const float *bias, int bias_mode, int act, int accumulate,
+                        int batch, long abs_, long bbs, long cbs, long biasbs, hipStream_t s)
+{
+    TileArgs p;
+    p.A = A; p.B = B; p.C = C; p.bias = bias_mode ? bias : nullptr;
+    p.as0 = as0; p.as1 = as1; p.bs0 = bs0; p.bs1 = bs1; p.cs0 = cs0; p.cs1 = cs1;
+    p.abs_ = abs_; p.bbs = bbs; p.cbs = cbs; p.biasbs = biasbs;
+    p.M = M; p.N = N; p.K = K;
+    p.bias_mode = bias_mode; p.act = act; p.accumulate = accumulate;
+    int am = pick_mode(A, as0, as1, M, K, abs_);
+    int bm = pick_mode(B, bs1, bs0, N, K, bbs);
+    bool c4 = cs0 == 1 && al16(C) && (cs1 % 4 == 0) && (cbs % 4 == 0);
+    dim3 grid(ceil_div(N, TBN), ceil_div(M, TBM), batch);
+    if (am == LM_KC) launch_tile_b<LM_KC>(p, bm, c4, grid, s);
+    else if (am == LM_OC) launch_tile_b<LM_OC>(p, bm, c4, grid, s);
+    else launch_tile_b<LM_GEN>(p, bm, c4, grid, s);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
+// ---------------------------------------------------------------- skinny (decode) GEMM
+// NT row tiles of 16 per workgroup (DUAL: tile 0 from W, tile 1 from W2 at the same rows),
+// WPB waves split the K chunks of 64 and reduce through LDS.
+template <int NT, int WPB, bool DUAL>
+__global__ void __launch_bounds__(WPB * 64)
+skinny_kernel(const float *__restrict__ W, const float *__restrict__ W2, const float *__restrict__ X, long ldx, int M,
+              int N, int K, const SkinnyEpiArgs epi)
+{
+    __shared__ floatx4 red[WPB][NT][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int rows_per_block = DUAL ? 16 : NT * 16;
+    const int m0 = blockIdx.x * rows_per_block;
+
+    const float *wp[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        int row = m0 + (DUAL ? 0 : t * 16) + r16;
+        row = row < M ? row : M - 1;  // clamped rows are computed and discarded
+        wp[t] = (DUAL && t == 1 ? W2 : W) + (long)row * K + 4 * g;
+    }
+    const bool xvalid = r16 < N;
+    const float *xp = X + (long)(xvalid ? r16 : 0) * ldx + 4 * g;
+
+    floatx4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int nchunk = (K + 63) / 64;
+    const bool ktail = (K & 63) != 0;
+    floatx4 wc[NT][4], wn[NT][4];
+    float4 xc[4], xn[4];
+    auto load = [&](int c, floatx4 (&wv)[NT][4], float4 (&xv)[4]) {
+        const int k = c * 64;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const bool kin = !ktail || (k + 16 * q + 4 * g) < K;
+            xv[q] = (xvalid && kin) ? *(const float4 *)(xp + k + 16 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+                wv[t][q] = kin ? __builtin_nontemporal_load((const floatx4 *)(wp[t] + k + 16 * q))
+                               : floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+    };
+    int c = w;
+    if (c < nchunk) load(c, wc, xc);
+    for (; c < nchunk; c += WPB) {
+        const int cn = c + WPB;
+        if (cn < nchunk) load(cn, wn, xn);  // keep the next chunk's loads in flight
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                acc[t] = mfma4(wc[t][q][0], xc[q].x, acc[t]);
+                acc[t] = mfma4(wc[t][q][1], xc[q].y, acc[t]);
+                acc[t] = mfma4(wc[t][q][2], xc[q].z, acc[t]);
+                acc[t] = mfma4(wc[t][q][3], xc[q].w, acc[t]);
+            }
+        if (cn < nchunk) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                xc[q] = xn[q];
+#pragma unroll
+                for (int t = 0; t < NT; ++t) wc[t][q] = wn[t][q];
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) red[w][t][lane] = acc[t];
+    __syncthreads();
+
+    // epilogue: thread (t, ln) owns rows m..m+3 of tile t for token n = ln % 16
+    const int tid = threadIdx.x;
+    const int n_items = DUAL ? 64 : NT * 64;
+    if (tid >= n_items) return;
+    const int t = DUAL ? 0 : tid / 64, ln = tid % 64;
+    const int n = ln & 15;
+    const int m = m0 + t * 16 + 4 * (ln >> 4);
+    if (n >= N || m >= M) return;
+    floatx4 s0 = red[0][t][ln];
+#pragma unroll
+    for (int ww = 1; ww < WPB; ++ww) s0 += red[ww][t][ln];
+    float v[4] = {s0[0], s0[1], s0[2], s0[3]};
+    const int nv = min(4, M - m);
+
+    if constexpr (DUAL) {  // SwiGLU: silu(gate) * up
+        floatx4 s1 = red[0][1][ln];
+#pragma unroll
+        for (int ww = 1; ww < WPB; ++ww) s1 += red[ww][1][ln];
+        float *o = epi.out + (long)n * epi.ldo + m;
+        for (int r = 0; r < nv; ++r) o[r] = silu_f(v[r]) * s1[r];
+        return;
+    } else {
+    if (epi.bias)
+        for (int r = 0; r < nv; ++r) v[r] = v[r] + epi.bias[m + r];
+    if (epi.mode == EPI_STORE) {
+        float *o = epi.out + (long)n * epi.ldo + m;
+        for (int r = 0; r < nv; ++r) o[r] = apply_act(v[r], epi.act);
+    } else if (epi.mode == EPI_RESID) {
+        float *o = epi.out + (long)n * epi.ldo + m;
+        for (int r = 0; r < nv; ++r) o[r] = o[r] + v[r];
+    } else {  // EPI_QKV (m % 4 == 0, d % 16 == 0, dh even: the 4 rows share a section and head)
+        const int sec = m / epi.d, e = m - sec * epi.d, h = e / epi.dh, ee = e - h * epi.dh;
+        const int pos = epi.pos[n];
+        if (epi.rope && sec < 2) {
+#pragma unroll
+            for (int pr = 0; pr < 2; ++pr) {
+                int i = (ee + 2 * pr) / 2;
+                double inv = pow((double)epi.theta, -2.0 * i / (double)epi.dh);
+                double a = (double)pos * inv, cs = cos(a), sn = sin(a);
+                double x0 = v[2 * pr], x1 = v[2 * pr + 1];
+                v[2 * pr] = (float)(x0 * cs - x1 * sn);
+                v[2 * pr + 1] = (float)(x0 * sn + x1 * cs);
+            }
+        }
+        float *dst;
+        if (sec == 0) dst = epi.q_out + (long)n * epi.d + e;
+        else dst = (sec == 1 ? epi.k_cache : epi.v_cache) + (long)n * epi.kv_sb + (long)h * epi.kv_sh +
+                   (long)pos * epi.dh + ee;
+        *(float4 *)dst = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    }
+}
+
+jas_status skinny_gemm(const float *W, const float *W2, const float *X, long ldx, int M, int N, int K,
+                       const SkinnyEpiArgs &epi, hipStream_t s)
+{
+    JAS_CHECK(N >= 1 && N <= 16 && M > 0 && K > 0 && K % 4 == 0 && ldx % 4 == 0, JAS_ERR_INVALID,
+              "skinny_gemm: unsupported shape");
+    JAS_CHECK(al16(W) && al16(X) && (!W2 || al16(W2)), JAS_ERR_INVALID, "skinny_gemm: operands must be 16B aligned");
+    if (epi.mode == EPI_QKV)
+        JAS_CHECK(epi.d % 16 == 0 && epi.dh % 4 == 0 && M == 3 * epi.d, JAS_ERR_INVALID, "skinny_gemm: bad QKV shape");
+    if (epi.mode == EPI_SWIGLU) {
+        JAS_CHECK(W2 != nullptr, JAS_ERR_INVALID, "skinny_gemm: SwiGLU needs both weights");
+        hipLaunchKernelGGL((skinny_kernel<2, 8, true>), dim3(ceil_div(M, 16)), dim3(512), 0, s, W, W2, X, ldx, M, N, K,
+                           epi);
+    } else {
+        hipLaunchKernelGGL((skinny_kernel<1, 8, false>), dim3(ceil_div(M, 16)), dim3(512), 0, s, W, W2, X, ldx, M, N,
+                           K, epi);
+    }
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
+} // namespace jas
+
+using namespace jas;
+
+extern "C" jas_status jas_gemm(int M, int N, int K, const float *A, long as0, long as1, const float *B, long bs0,
+                               long bs1, float *C, long cs0, long cs1, const float *bias, int bias_mode, int act,
+                               int accumulate, int batch, long abs_, long bbs, long cbs, long biasbs,
+                               jas_stream_t stream)
+{
+    JAS_CHECK(M >= 0 && N >= 0 && K >= 0 && batch >= 1, JAS_ERR_INVALID, "jas_gemm: negative size");
+    JAS_CHECK(A && B && C, JAS_ERR_INVALID, "jas_gemm: null operand");
+    JAS_CHECK(bias_mode >= 0 && bias_mode <= 2 && (bias_mode == 0 || bias), JAS_ERR_INVALID, "jas_gemm: bad bias");
+    JAS_CHECK(act >= JAS_ACT_NONE && act <= JAS_ACT_SIGMOID, JAS_ERR_INVALID, "jas_gemm: bad activation");
+    if (M == 0 || N == 0) return JAS_OK;
+    hipStream_t s = stream_or_default(stream);
+    // decode shape: weights [M][K] row-major, tokens K-contiguous, token-major output
+    if (batch == 1 && N <= 16 && as1 == 1 && bs0 == 1 && cs0 == 1 && K % 4 == 0 && as0 == K && bs1 % 4 == 0 &&
+        al16(A) && al16(B) && bias_mode != 2 && !accumulate && K > 0) {
+        SkinnyEpiArgs e;
+        e.mode = EPI_STORE;
+        e.act = act;
+        e.bias = bias_mode == 1 ? bias : nullptr;
+        e.out = C;
+        e.ldo = cs1;
+        return skinny_gemm(A, nullptr, B, bs1, M, N, K, e, s);
+    }
+    return gemm_general(M, N, K, A, as0, as1, B, bs0, bs1, C, cs0, cs1, bias, bias_mode, act, accumulate, batch, abs_,
+                        bbs, cbs, biasbs, s);
+}

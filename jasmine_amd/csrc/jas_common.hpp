@@ -1,0 +1,121 @@
+// Shared helpers for the gfx950 kernels and the C ABI implementation.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstring>
+#include <cstdio>
+#include <string>
+
+#include "../../include/jasmine_hip.h"
+
+namespace jas {
+
+// thread-local last error message behind jas_last_error()
+void set_error(const std::string &msg);
+jas_status fail(jas_status code, const std::string &msg);
+hipStream_t stream_or_default(jas_stream_t s);
+void *workspace(size_t bytes, hipStream_t s);
+
+#define JAS_HIP(expr)                                                                 \
+    do {                                                                              \
+        hipError_t e_ = (expr);                                                       \
+        if (e_ != hipSuccess)                                                         \
+            return ::jas::fail(JAS_ERR_HIP, std::string(#expr ": ") + hipGetErrorString(e_)); \
+    } while (0)
+
+#define JAS_CHECK(cond, code, msg)                                                    \
+    do {                                                                              \
+        if (!(cond)) return ::jas::fail(code, msg);                                   \
+    } while (0)
+
+#define JAS_LAUNCH_CHECK() JAS_HIP(hipGetLastError())
+
+constexpr int WAVE = 64;
+
+// ---- wave64 reductions (DPP/permute lowered by the compiler from shfl_xor) ----
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+    return v;
+}
+
+// block-wide reduction through LDS; every thread gets the result.  `red` holds >= 16 floats.
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float *red)
+{
+    v = wave_sum(v);
+    constexpr int NW = NT / WAVE;
+    if (NW == 1) return v;
+    int w = threadIdx.x / WAVE, l = threadIdx.x % WAVE;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) s += red[i];
+    return s;
+}
+template <int NT>
+__device__ __forceinline__ float block_max(float v, float *red)
+{
+    v = wave_max(v);
+    constexpr int NW = NT / WAVE;
+    if (NW == 1) return v;
+    int w = threadIdx.x / WAVE, l = threadIdx.x % WAVE;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    float s = red[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) s = fmaxf(s, red[i]);
+    return s;
+}
+
+// GPT-2 tanh GELU and SiLU in fp32
+__device__ __forceinline__ float gelu_f(float x)
+{
+    float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    return 0.5f * x * (1.0f + tanhf(u));
+}
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float apply_act(float v, int act)
+{
+    switch (act) {
+    case JAS_ACT_RELU: return (float)(v > 0.0f) * v;  // (x>0)*x keeps jasmine's -0 / NaN
+    case JAS_ACT_GELU: return gelu_f(v);
+    case JAS_ACT_SILU: return silu_f(v);
+    case JAS_ACT_SIGMOID: return (float)(1.0 / (1.0 + (double)expf(-v)));
+    default: return v;
+    }
+}
+
+inline unsigned ceil_div(long a, long b) { return (unsigned)((a + b - 1) / b); }
+
+// counter-based N(mean,std): splitmix64 + Box-Muller, identical formula on host and device
+__host__ __device__ inline uint64_t splitmix64(uint64_t x)
+{
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+__host__ __device__ inline uint64_t stream_key(uint64_t seed, uint64_t stream)
+{
+    return splitmix64(splitmix64(seed) ^ (stream * 0xD1B54A32D192ED03ull));
+}
+
+} // namespace jas

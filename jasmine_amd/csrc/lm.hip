@@ -1,0 +1,546 @@
+// Decoder-only LM runner: prefill + KV-cache greedy decode on one HIP stream.
+//
+// The reference's only decode loop, test_transformer_t::predict (transformer_test.hpp:
+// 194-242), re-runs the full prefix through the model every step and feeds the last output
+// column back.  This runner computes the same last column incrementally: prefill writes
+// every layer's K/V into a device-resident cache, each decode step appends one column per
+// sequence and attends over the cache.  Per decode step and layer it issues
+//   norm -> QKV GEMM (+bias, +RoPE, K/V appended to the cache in the epilogue)
+//   -> split-K attention -> O GEMM (+residual) -> norm -> FFN GEMM(s) (+GELU / SwiGLU,
+//   +residual)
+// with the decode GEMMs streaming the weights straight from HBM into the matrix cores.
+//
+// HBM layout (all fp32): one weight arena, matrices [out][in] row-major (K-contiguous for
+// both the weight-streaming decode GEMM and the tiled prefill GEMM); activations
+// token-major [token][feature]; KV cache [layer][seq][head][position][head_dim] so a
+// (seq, head) key range is one contiguous stream.
+#include "gemm.hpp"
+
+#include <map>
+#include <string>
+#include <vector>
+
+namespace jas {
+
+struct Tensor {
+    size_t off = 0, count = 0;
+};
+
+__global__ void set_positions_kernel(int32_t *pos, int32_t *seqlens, int B, int p)
+{
+    int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b < B) {
+        pos[b] = p;
+        seqlens[b] = p + 1;
+    }
+}
+
+__global__ void prefill_positions_kernel(int32_t *pos, int B, int P)
+{
+    long n = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (n < (long)B * P) pos[n] = (int32_t)(n % P);
+}
+
+// copy the k and v sections of the prefill QKV rows into the cache:
+// qkv[(b*P + t)*3d + sec*d + h*dh + e] -> cache[b][h][t][e]
+__global__ void kv_scatter_kernel(const float *__restrict__ qkv, float *kc, float *vc, int B, int P, int H, int dh,
+                                  int ctx)
+{
+    long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    int d4 = (H * dh) / 4;
+    long total = (long)B * P * d4;
+    if (g >= total) return;
+    int c4 = (int)(g % d4);
+    long n = g / d4;
+    int b = (int)(n / P), t = (int)(n % P);
+    int e = c4 * 4, h = e / dh, ee = e % dh;
+    int d = H * dh;
+    const float *row = qkv + n * 3L * d;
+    long dst = (((long)b * H + h) * ctx + t) * dh + ee;
+    *(float4 *)(kc + dst) = *(const float4 *)(row + d + e);
+    *(float4 *)(vc + dst) = *(const float4 *)(row + 2 * d + e);
+}
+
+__global__ void swiglu_kernel(const float *__restrict__ gate, const float *__restrict__ up, float *out, long n)
+{
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = silu_f(gate[i]) * up[i];
+}
+
+__global__ void copy_ids_kernel(const int32_t *src, int32_t *dst, int B)
+{
+    int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b < B) dst[b] = src[b];
+}
+
+} // namespace jas
+
+using namespace jas;
+
+struct jas_lm {
+    jas_lm_config cfg{};
+    hipStream_t stream = nullptr;
+    float *arena = nullptr;
+    size_t arena_count = 0;
+    std::map<std::string, Tensor> tensors;
+    // KV cache
+    float *kc = nullptr, *vc = nullptr;
+    long kv_layer = 0, kv_sb = 0, kv_sh = 0;
+    // decode buffers [max_batch][...]
+    float *x = nullptr, *h = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr;
+    int32_t *ids = nullptr, *pos = nullptr, *seqlens = nullptr, *hist = nullptr;
+    int hist_cap = 0;
+    void *attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+    // prefill buffers (grown on demand)
+    float *pX = nullptr, *pH = nullptr, *pQKV = nullptr, *pATT = nullptr, *pG = nullptr, *pU = nullptr, *pFF = nullptr;
+    int32_t *pIds = nullptr, *pPos = nullptr;
+    long p_tokens = 0;
+    int B = 0;         // active batch
+    int position = 0;  // tokens already in the cache
+    // profiling
+    bool prof = false;
+    std::vector<hipEvent_t> ev;
+    std::vector<int> ev_cls;
+    size_t ev_used = 0;
+
+    const float *W(const char *n) const
+    {
+        auto it = tensors.find(n);
+        return it == tensors.end() || it->second.count == 0 ? nullptr : arena + it->second.off;
+    }
+    float *Wm(const char *n) { return const_cast<float *>(W(n)); }
+    int dh() const { return cfg.d_model / cfg.n_head; }
+};
+
+namespace {
+
+void add_tensor(jas_lm *lm, const char *name, size_t count, size_t &cursor)
+{
+    Tensor t;
+    t.off = cursor;
+    t.count = count;
+    lm->tensors[name] = t;
+    cursor += (count + 63) & ~size_t(63);  // 256-byte aligned tensors
+}
+
+jas_status prof_begin(jas_lm *lm, int cls)
+{
+    if (!lm->prof) return JAS_OK;
+    if (lm->ev_used + 2 > lm->ev.size()) {
+        for (int k = 0; k < 256; ++k) {
+            hipEvent_t e;
+            JAS_HIP(hipEventCreate(&e));
+            lm->ev.push_back(e);
+            lm->ev_cls.push_back(0);
+        }
+    }
+    lm->ev_cls[lm->ev_used] = cls;
+    JAS_HIP(hipEventRecord(lm->ev[lm->ev_used++], lm->stream));
+    return JAS_OK;
+}
+
+jas_status prof_end(jas_lm *lm)
+{
+    if (!lm->prof) return JAS_OK;
+    lm->ev_cls[lm->ev_used] = -1;
+    JAS_HIP(hipEventRecord(lm->ev[lm->ev_used++], lm->stream));
+    return JAS_OK;
+}
+
+#define TRY(x)                                   \
+    do {                                         \
+        jas_status s_ = (x);                     \
+        if (s_ != JAS_OK) return s_;             \
+    } while (0)
+
+// y rows are dense [n_vec][d]; x rows are vstride apart
+jas_status norm_rows(jas_lm *lm, const float *x, float *y, int n_vec, long vstride, int l_or_f /* -1 final */,
+                     int which)
+{
+    const jas_lm_config &c = lm->cfg;
+    const int d = c.d_model;
+    const float *g, *b = nullptr;
+    if (l_or_f < 0) {
+        g = lm->W("lnf_g");
+        b = lm->W("lnf_b");
+    } else {
+        g = lm->W(which == 1 ? "ln1_g" : "ln2_g") + (long)l_or_f * d;
+        const float *bb = lm->W(which == 1 ? "ln1_b" : "ln2_b");
+        b = bb ? bb + (long)l_or_f * d : nullptr;
+    }
+    TRY(prof_begin(lm, 2));
+    if (c.kind == 0) TRY(jas_layernorm(x, y, n_vec, d, vstride, d, 1, c.eps, g, b, lm->stream));
+    else TRY(jas_rmsnorm(x, y, n_vec, d, vstride, d, 1, c.eps, g, lm->stream));
+    return prof_end(lm);
+}
+
+// weight GEMM for N tokens whose activations are token-major rows of length K (ld = K)
+jas_status proj(jas_lm *lm, const float *Wt, const float *X, int N, int M, int K, const SkinnyEpiArgs &e)
+{
+    TRY(prof_begin(lm, 0));
+    TRY(skinny_gemm(Wt, nullptr, X, K, M, N, K, e, lm->stream));
+    return prof_end(lm);
+}
+
+jas_status ensure_prefill(jas_lm *lm, long tokens)
+{
+    if (tokens <= lm->p_tokens) return JAS_OK;
+    const jas_lm_config &c = lm->cfg;
+    float **bufs[] = {&lm->pX, &lm->pH, &lm->pQKV, &lm->pATT, &lm->pG, &lm->pU, &lm->pFF};
+    for (auto b : bufs) {
+        if (*b) JAS_HIP(hipFree(*b));
+        *b = nullptr;
+    }
+    if (lm->pIds) JAS_HIP(hipFree(lm->pIds));
+    if (lm->pPos) JAS_HIP(hipFree(lm->pPos));
+    const long d = c.d_model, F = c.d_ff;
+    size_t sz[] = {(size_t)(tokens * d), (size_t)(tokens * d), (size_t)(tokens * 3 * d), (size_t)(tokens * d),
+                   (size_t)(tokens * F), (size_t)(c.kind == 1 ? tokens * F : 4), (size_t)(c.kind == 1 ? tokens * F : 4)};
+    for (int k = 0; k < 7; ++k) TRY(jas_malloc((void **)bufs[k], sz[k] * sizeof(float)));
+    TRY(jas_malloc((void **)&lm->pIds, tokens * sizeof(int32_t)));
+    TRY(jas_malloc((void **)&lm->pPos, tokens * sizeof(int32_t)));
+    lm->p_tokens = tokens;
+    return JAS_OK;
+}
+
+// one decode step for lm->B sequences: d_ids in, argmax written back into d_ids
+jas_status decode_step(jas_lm *lm)
+{
+    const jas_lm_config &c = lm->cfg;
+    const int B = lm->B, d = c.d_model, F = c.d_ff, H = c.n_head, dh = lm->dh(), V = c.vocab;
+    JAS_CHECK(lm->position < c.max_ctx, JAS_ERR_RANGE, "jas_lm_decode: KV cache full (max_ctx reached)");
+    hipStream_t s = lm->stream;
+    hipLaunchKernelGGL(set_positions_kernel, dim3(1), dim3(256), 0, s, lm->pos, lm->seqlens, B, lm->position);
+    TRY(prof_begin(lm, 2));
+    TRY(jas_embed(lm->W("wte"), c.kind == 0 ? lm->W("wpe") : nullptr, lm->ids, lm->pos, lm->x, B, d, s));
+    TRY(prof_end(lm));
+    for (int l = 0; l < c.n_layer; ++l) {
+        TRY(norm_rows(lm, lm->x, lm->h, B, d, l, 1));
+        SkinnyEpiArgs eq;
+        eq.mode = EPI_QKV;
+        eq.bias = lm->W("b_qkv") ? lm->W("b_qkv") + (long)l * 3 * d : nullptr;
+        eq.q_out = lm->q;
+        eq.k_cache = lm->kc + l * lm->kv_layer;
+        eq.v_cache = lm->vc + l * lm->kv_layer;
+        eq.pos = lm->pos;
+        eq.kv_sb = lm->kv_sb;
+        eq.kv_sh = lm->kv_sh;
+        eq.d = d;
+        eq.dh = dh;
+        eq.rope = c.kind == 1;
+        eq.theta = c.rope_theta;
+        TRY(proj(lm, lm->W("w_qkv") + (long)l * 3 * d * d, lm->h, B, 3 * d, d, eq));
+        TRY(prof_begin(lm, 1));
+        TRY(jas_attn_decode(lm->q, lm->kc + l * lm->kv_layer, lm->vc + l * lm->kv_layer, lm->att, lm->seqlens, B, H,
+                            dh, lm->position + 1, lm->kv_sb, lm->kv_sh, 1.0f / sqrtf((float)dh), lm->attn_ws, s));
+        TRY(prof_end(lm));
+        SkinnyEpiArgs eo;
+        eo.mode = EPI_RESID;
+        eo.bias = lm->W("b_o") ? lm->W("b_o") + (long)l * d : nullptr;
+        eo.out = lm->x;
+        eo.ldo = d;
+        TRY(proj(lm, lm->W("w_o") + (long)l * d * d, lm->att, B, d, d, eo));
+        TRY(norm_rows(lm, lm->x, lm->h, B, d, l, 2));
+        if (c.kind == 0) {
+            SkinnyEpiArgs ef;
+            ef.mode = EPI_STORE;
+            ef.act = JAS_ACT_GELU;
+            ef.bias = lm->W("b_fc") + (long)l * F;
+            ef.out = lm->ff;
+            ef.ldo = F;
+            TRY(proj(lm, lm->W("w_fc") + (long)l * F * d, lm->h, B, F, d, ef));
+            SkinnyEpiArgs ep;
+            ep.mode = EPI_RESID;
+            ep.bias = lm->W("b_proj") + (long)l * d;
+            ep.out = lm->x;
+            ep.ldo = d;
+            TRY(proj(lm, lm->W("w_proj") + (long)l * d * F, lm->ff, B, d, F, ep));
+        } else {
+            SkinnyEpiArgs eg;
+            eg.mode = EPI_SWIGLU;
+            eg.out = lm->ff;
+            eg.ldo = F;
+            TRY(prof_begin(lm, 0));
+            TRY(skinny_gemm(lm->W("w_gate") + (long)l * F * d, lm->W("w_up") + (long)l * F * d, lm->h, d, F, B, d, eg,
+                            s));
+            TRY(prof_end(lm));
+            SkinnyEpiArgs ed;
+            ed.mode = EPI_RESID;
+            ed.out = lm->x;
+            ed.ldo = d;
+            TRY(proj(lm, lm->W("w_down") + (long)l * d * F, lm->ff, B, d, F, ed));
+        }
+    }
+    TRY(norm_rows(lm, lm->x, lm->h, B, d, -1, 0));
+    SkinnyEpiArgs eh;
+    eh.mode = EPI_STORE;
+    eh.out = lm->logits;
+    eh.ldo = V;
+    TRY(proj(lm, c.kind == 0 ? lm->W("wte") : lm->W("w_head"), lm->h, B, V, d, eh));
+    TRY(prof_begin(lm, 2));
+    TRY(jas_argmax(lm->logits, B, V, V, lm->ids, s));
+    TRY(prof_end(lm));
+    lm->position += 1;
+    return JAS_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out)
+{
+    JAS_CHECK(cfg && out, JAS_ERR_INVALID, "jas_lm_create: null argument");
+    const jas_lm_config &c = *cfg;
+    JAS_CHECK(c.kind == 0 || c.kind == 1, JAS_ERR_INVALID, "jas_lm_create: kind must be 0 (GPT-2) or 1 (LLaMA)");
+    JAS_CHECK(c.n_layer > 0 && c.d_model > 0 && c.n_head > 0 && c.d_ff > 0 && c.vocab > 0 && c.max_ctx > 0 &&
+                  c.max_batch > 0,
+              JAS_ERR_INVALID, "jas_lm_create: sizes must be positive");
+    // mat_mha_t rejects d_model % heads != 0 (mat_mha_t.hpp:239-240)
+    JAS_CHECK(c.d_model % c.n_head == 0, JAS_ERR_INVALID, "d_model must be divisible by num_heads");
+    const int dh = c.d_model / c.n_head;
+    JAS_CHECK(dh == 32 || dh == 64 || dh == 128, JAS_ERR_INVALID, "jas_lm_create: head dim must be 32, 64 or 128");
+    JAS_CHECK(c.d_model % 64 == 0 && c.d_ff % 16 == 0, JAS_ERR_INVALID,
+              "jas_lm_create: d_model must be a multiple of 64 and d_ff of 16");
+    JAS_CHECK(c.max_batch <= 16, JAS_ERR_INVALID, "jas_lm_create: max_batch above 16 is not supported");
+    TRY(jas_init(-1));
+    jas_lm *lm = new jas_lm();
+    lm->cfg = c;
+    JAS_HIP(hipStreamCreateWithFlags(&lm->stream, hipStreamNonBlocking));
+    const size_t d = c.d_model, F = c.d_ff, L = c.n_layer, V = c.vocab;
+    size_t cur = 0;
+    add_tensor(lm, "wte", V * d, cur);
+    if (c.kind == 0) add_tensor(lm, "wpe", (size_t)c.max_ctx * d, cur);
+    add_tensor(lm, "ln1_g", L * d, cur);
+    if (c.kind == 0) add_tensor(lm, "ln1_b", L * d, cur);
+    add_tensor(lm, "w_qkv", L * 3 * d * d, cur);
+    if (c.kind == 0) add_tensor(lm, "b_qkv", L * 3 * d, cur);
+    add_tensor(lm, "w_o", L * d * d, cur);
+    if (c.kind == 0) add_tensor(lm, "b_o", L * d, cur);
+    add_tensor(lm, "ln2_g", L * d, cur);
+    if (c.kind == 0) add_tensor(lm, "ln2_b", L * d, cur);
+    if (c.kind == 0) {
+        add_tensor(lm, "w_fc", L * F * d, cur);
+        add_tensor(lm, "b_fc", L * F, cur);
+        add_tensor(lm, "w_proj", L * d * F, cur);
+        add_tensor(lm, "b_proj", L * d, cur);
+    } else {
+        add_tensor(lm, "w_gate", L * F * d, cur);
+        add_tensor(lm, "w_up", L * F * d, cur);
+        add_tensor(lm, "w_down", L * d * F, cur);
+    }
+    add_tensor(lm, "lnf_g", d, cur);
+    if (c.kind == 0) add_tensor(lm, "lnf_b", d, cur);
+    if (c.kind == 1) add_tensor(lm, "w_head", V * d, cur);
+    lm->arena_count = cur;
+    jas_status st = jas_malloc((void **)&lm->arena, cur * sizeof(float));
+    if (st != JAS_OK) {
+        jas_lm_destroy(lm);
+        return st;
+    }
+    const int Bm = c.max_batch;
+    lm->kv_sh = (long)c.max_ctx * dh;
+    lm->kv_sb = (long)c.n_head * lm->kv_sh;
+    lm->kv_layer = (long)Bm * lm->kv_sb;
+    size_t kvn = (size_t)L * lm->kv_layer;
+    st = jas_malloc((void **)&lm->kc, kvn * sizeof(float));
+    if (st == JAS_OK) st = jas_malloc((void **)&lm->vc, kvn * sizeof(float));
+    struct { float **p; size_t n; } fb[] = {{&lm->x, Bm * d}, {&lm->h, Bm * d}, {&lm->q, Bm * d}, {&lm->att, Bm * d},
+                                            {&lm->ff, Bm * F}, {&lm->logits, Bm * V}};
+    for (auto &f : fb)
+        if (st == JAS_OK) st = jas_malloc((void **)f.p, f.n * sizeof(float));
+    if (st == JAS_OK) st = jas_malloc((void **)&lm->ids, 64 * sizeof(int32_t));
+    if (st == JAS_OK) st = jas_malloc((void **)&lm->pos, 64 * sizeof(int32_t));
+    if (st == JAS_OK) st = jas_malloc((void **)&lm->seqlens, 64 * sizeof(int32_t));
+    lm->attn_ws_bytes = jas_attn_decode_workspace(Bm, c.n_head, dh, c.max_ctx);
+    for (int b = 1; b < Bm; ++b)  // workspace must cover every batch size actually used
+        lm->attn_ws_bytes = std::max(lm->attn_ws_bytes, jas_attn_decode_workspace(b, c.n_head, dh, c.max_ctx));
+    if (st == JAS_OK && lm->attn_ws_bytes) st = jas_malloc(&lm->attn_ws, lm->attn_ws_bytes);
+    if (st != JAS_OK) {
+        jas_lm_destroy(lm);
+        return st;
+    }
+    *out = lm;
+    return JAS_OK;
+}
+
+jas_status jas_lm_destroy(jas_lm *lm)
+{
+    if (!lm) return JAS_OK;
+    if (lm->stream) (void)hipStreamSynchronize(lm->stream);
+    void *ptrs[] = {lm->arena, lm->kc, lm->vc, lm->x, lm->h, lm->q, lm->att, lm->ff, lm->logits, lm->ids, lm->pos,
+                    lm->seqlens, lm->hist, lm->attn_ws, lm->pX, lm->pH, lm->pQKV, lm->pATT, lm->pG, lm->pU, lm->pFF,
+                    lm->pIds, lm->pPos};
+    for (void *p : ptrs)
+        if (p) (void)hipFree(p);
+    for (auto e : lm->ev) (void)hipEventDestroy(e);
+    if (lm->stream) (void)hipStreamDestroy(lm->stream);
+    delete lm;
+    return JAS_OK;
+}
+
+jas_status jas_lm_init_random(jas_lm *lm, uint64_t seed, float std)
+{
+    JAS_CHECK(lm, JAS_ERR_INVALID, "jas_lm_init_random: null model");
+    uint64_t sid = 0;
+    for (auto &kv : lm->tensors) {  // std::map: deterministic (name) order
+        const std::string &n = kv.first;
+        float *p = lm->arena + kv.second.off;
+        size_t cnt = kv.second.count;
+        ++sid;
+        if (n == "ln1_g" || n == "ln2_g" || n == "lnf_g") {
+            std::vector<float> ones(cnt, 1.0f);
+            TRY(jas_memcpy_h2d(p, ones.data(), cnt * sizeof(float), lm->stream));
+        } else if (n[0] == 'b' || n == "ln1_b" || n == "ln2_b" || n == "lnf_b") {
+            JAS_HIP(hipMemsetAsync(p, 0, cnt * sizeof(float), lm->stream));
+        } else {
+            TRY(jas_fill_normal(p, cnt, seed, sid, 0.0f, std, lm->stream));
+        }
+    }
+    JAS_HIP(hipStreamSynchronize(lm->stream));
+    return JAS_OK;
+}
+
+jas_status jas_lm_weight(jas_lm *lm, const char *name, float **ptr, size_t *count)
+{
+    JAS_CHECK(lm && name && ptr && count, JAS_ERR_INVALID, "jas_lm_weight: null argument");
+    auto it = lm->tensors.find(name);
+    *ptr = nullptr;
+    *count = 0;
+    if (it == lm->tensors.end()) return JAS_OK;
+    *ptr = lm->arena + it->second.off;
+    *count = it->second.count;
+    return JAS_OK;
+}
+
+jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_t *h_next, float *h_logits)
+{
+    JAS_CHECK(lm && h_ids, JAS_ERR_INVALID, "jas_lm_prefill: null argument");
+    const jas_lm_config &c = lm->cfg;
+    JAS_CHECK(B >= 1 && B <= c.max_batch && P >= 1, JAS_ERR_INVALID, "jas_lm_prefill: bad batch/prompt size");
+    JAS_CHECK(P <= c.max_ctx, JAS_ERR_RANGE, "jas_lm_prefill: prompt longer than max_ctx");
+    for (long i = 0; i < (long)B * P; ++i)
+        JAS_CHECK(h_ids[i] >= 0 && h_ids[i] < c.vocab, JAS_ERR_INVALID, "jas_lm_prefill: token id out of range");
+    const long T = (long)B * P;
+    TRY(ensure_prefill(lm, T));
+    hipStream_t s = lm->stream;
+    const int d = c.d_model, F = c.d_ff, H = c.n_head, dh = lm->dh(), V = c.vocab;
+    lm->B = B;
+    lm->position = 0;
+    TRY(jas_memcpy_h2d(lm->pIds, h_ids, T * sizeof(int32_t), s));
+    hipLaunchKernelGGL(prefill_positions_kernel, dim3(ceil_div(T, 256)), dim3(256), 0, s, lm->pPos, B, P);
+    TRY(jas_embed(lm->W("wte"), c.kind == 0 ? lm->W("wpe") : nullptr, lm->pIds, lm->pPos, lm->pX, (int)T, d, s));
+    for (int l = 0; l < c.n_layer; ++l) {
+        TRY(norm_rows(lm, lm->pX, lm->pH, (int)T, d, l, 1));
+        const float *bq = lm->W("b_qkv") ? lm->W("b_qkv") + (long)l * 3 * d : nullptr;
+        // QKV[n][m] = sum_k w_qkv[m][k] H[n][k] (+ b[m])
+        TRY(gemm_general(3 * d, (int)T, d, lm->W("w_qkv") + (long)l * 3 * d * d, d, 1, lm->pH, 1, d, lm->pQKV, 1,
+                         3L * d, bq, bq ? 1 : 0, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s));
+        if (c.kind == 1)  // q and k sections are 2H consecutive heads of each row
+            TRY(jas_rope_llama(lm->pQKV, lm->pPos, (int)T, 2 * H, dh, 3L * d, c.rope_theta, s));
+        float *kcl = lm->kc + l * lm->kv_layer, *vcl = lm->vc + l * lm->kv_layer;
+        hipLaunchKernelGGL(kv_scatter_kernel, dim3(ceil_div(T * (d / 4), 256)), dim3(256), 0, s, lm->pQKV, kcl, vcl,
+                           B, P, H, dh, c.max_ctx);
+        TRY(jas_attn_prefill(lm->pQKV, kcl, vcl, lm->pATT, B, H, P, P, dh, (long)P * 3 * d, dh, 3L * d, lm->kv_sb,
+                             lm->kv_sh, dh, (long)P * d, dh, d, 1.0f / sqrtf((float)dh), 1, JAS_F32, s));
+        const float *bo = lm->W("b_o") ? lm->W("b_o") + (long)l * d : nullptr;
+        TRY(gemm_general(d, (int)T, d, lm->W("w_o") + (long)l * d * d, d, 1, lm->pATT, 1, d, lm->pX, 1, d, bo,
+                         bo ? 1 : 0, JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s));
+        TRY(norm_rows(lm, lm->pX, lm->pH, (int)T, d, l, 2));
+        if (c.kind == 0) {
+            TRY(gemm_general(F, (int)T, d, lm->W("w_fc") + (long)l * F * d, d, 1, lm->pH, 1, d, lm->pG, 1, F,
+                             lm->W("b_fc") + (long)l * F, 1, JAS_ACT_GELU, 0, 1, 0, 0, 0, 0, s));
+            TRY(gemm_general(d, (int)T, F, lm->W("w_proj") + (long)l * d * F, F, 1, lm->pG, 1, F, lm->pX, 1, d,
+                             lm->W("b_proj") + (long)l * d, 1, JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s));
+        } else {
+            TRY(gemm_general(F, (int)T, d, lm->W("w_gate") + (long)l * F * d, d, 1, lm->pH, 1, d, lm->pG, 1, F,
+                             nullptr, 0, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s));
+            TRY(gemm_general(F, (int)T, d, lm->W("w_up") + (long)l * F * d, d, 1, lm->pH, 1, d, lm->pU, 1, F, nullptr,
+                             0, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s));
+            hipLaunchKernelGGL(swiglu_kernel, dim3(ceil_div(T * F, 256)), dim3(256), 0, s, lm->pG, lm->pU, lm->pFF,
+                               T * F);
+            TRY(gemm_general(d, (int)T, F, lm->W("w_down") + (long)l * d * F, F, 1, lm->pFF, 1, F, lm->pX, 1, d,
+                             nullptr, 0, JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s));
+        }
+    }
+    // final norm and LM head on the last position of every sequence
+    TRY(norm_rows(lm, lm->pX + (long)(P - 1) * d, lm->h, B, (long)P * d, -1, 0));
+    SkinnyEpiArgs eh;
+    eh.mode = EPI_STORE;
+    eh.out = lm->logits;
+    eh.ldo = V;
+    TRY(skinny_gemm(c.kind == 0 ? lm->W("wte") : lm->W("w_head"), nullptr, lm->h, d, V, B, d, eh, s));
+    TRY(jas_argmax(lm->logits, B, V, V, lm->ids, s));
+    lm->position = P;
+    if (h_next) TRY(jas_memcpy_d2h(h_next, lm->ids, B * sizeof(int32_t), s));
+    if (h_logits) TRY(jas_memcpy_d2h(h_logits, lm->logits, (size_t)B * V * sizeof(float), s));
+    JAS_HIP(hipStreamSynchronize(s));
+    return JAS_OK;
+}
+
+jas_status jas_lm_decode(jas_lm *lm, const int32_t *h_ids, int32_t *h_next, float *h_logits)
+{
+    JAS_CHECK(lm && lm->B > 0, JAS_ERR_RUNTIME, "jas_lm_decode: call jas_lm_prefill first");
+    if (h_ids) {
+        for (int b = 0; b < lm->B; ++b)
+            JAS_CHECK(h_ids[b] >= 0 && h_ids[b] < lm->cfg.vocab, JAS_ERR_INVALID, "jas_lm_decode: token id out of range");
+        TRY(jas_memcpy_h2d(lm->ids, h_ids, lm->B * sizeof(int32_t), lm->stream));
+    }
+    TRY(decode_step(lm));
+    if (h_next) TRY(jas_memcpy_d2h(h_next, lm->ids, lm->B * sizeof(int32_t), lm->stream));
+    if (h_logits) TRY(jas_memcpy_d2h(h_logits, lm->logits, (size_t)lm->B * lm->cfg.vocab * sizeof(float), lm->stream));
+    return JAS_OK;
+}
+
+jas_status jas_lm_generate(jas_lm *lm, int steps, int32_t *h_ids)
+{
+    JAS_CHECK(lm && lm->B > 0, JAS_ERR_RUNTIME, "jas_lm_generate: call jas_lm_prefill first");
+    JAS_CHECK(steps >= 0, JAS_ERR_INVALID, "jas_lm_generate: negative steps");
+    JAS_CHECK(lm->position + steps <= lm->cfg.max_ctx, JAS_ERR_RANGE, "jas_lm_generate: would overflow max_ctx");
+    if (steps > lm->hist_cap) {
+        if (lm->hist) JAS_HIP(hipFree(lm->hist));
+        lm->hist = nullptr;
+        TRY(jas_malloc((void **)&lm->hist, (size_t)steps * 16 * sizeof(int32_t)));
+        lm->hist_cap = steps;
+    }
+    for (int st = 0; st < steps; ++st) {
+        TRY(decode_step(lm));
+        hipLaunchKernelGGL(copy_ids_kernel, dim3(1), dim3(64), 0, lm->stream, lm->ids, lm->hist + (long)st * lm->B,
+                           lm->B);
+    }
+    if (h_ids && steps) TRY(jas_memcpy_d2h(h_ids, lm->hist, (size_t)steps * lm->B * sizeof(int32_t), lm->stream));
+    JAS_HIP(hipStreamSynchronize(lm->stream));
+    return JAS_OK;
+}
+
+int jas_lm_position(jas_lm *lm) { return lm ? lm->position : -1; }
+jas_stream_t jas_lm_stream(jas_lm *lm) { return lm ? (jas_stream_t)lm->stream : nullptr; }
+
+jas_status jas_lm_profile(jas_lm *lm, int enable, double *ms_by_class, long *launches_by_class)
+{
+    JAS_CHECK(lm, JAS_ERR_INVALID, "jas_lm_profile: null model");
+    JAS_HIP(hipStreamSynchronize(lm->stream));
+    if (ms_by_class || launches_by_class) {
+        double ms[3] = {0, 0, 0};
+        long cnt[3] = {0, 0, 0};
+        for (size_t i = 0; i + 1 < lm->ev_used; i += 2) {
+            float t = 0.f;
+            JAS_HIP(hipEventElapsedTime(&t, lm->ev[i], lm->ev[i + 1]));
+            int k = lm->ev_cls[i];
+            if (k >= 0 && k < 3) {
+                ms[k] += t;
+                cnt[k] += 1;
+            }
+        }
+        for (int k = 0; k < 3; ++k) {
+            if (ms_by_class) ms_by_class[k] = ms[k];
+            if (launches_by_class) launches_by_class[k] = cnt[k];
+        }
+    }
+    lm->ev_used = 0;
+    lm->prof = enable != 0;
+    return JAS_OK;
+}
+
+} // extern "C"

@@ -1,0 +1,178 @@
+// Rotary embeddings, token embedding gather, argmax, seeded normal fill.
+#include "jas_common.hpp"
+
+#include <cfloat>
+
+namespace jas {
+
+// mat_RoPE_t::init cache entry (mat_RoPE_t.hpp:107-131) for val_type float:
+// angle = (float)(c / pow(10000.0, (float)(r/2) / (float)d)); cos where r, c have equal
+// parity, -sin at (even, odd), sin at (odd, even).
+__device__ __forceinline__ float rope_jas_entry(int r, int c, int d)
+{
+    float e = (float)(r / 2) / (float)d;
+    float angle = (float)((double)c / pow(10000.0, (double)e));
+    if ((r & 1) == (c & 1)) return cosf(angle);
+    return (r & 1) ? sinf(angle) : -sinf(angle);
+}
+
+// RoPE_net_t::forward (mat_RoPE_t.hpp:166-188): y[2i+r, m] = sum_c block(r, c) x[2i+c, m],
+// a float dot of two terms accumulated from 0 (no fused multiply-add).
+__global__ void rope_jas_kernel(const float *__restrict__ x, float *__restrict__ y, int d, int T)
+{
+#pragma clang fp contract(off)
+    long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    int half = d / 2;
+    if (g >= (long)half * T) return;
+    int i = (int)(g / T), m = (int)(g % T);
+    float x0 = x[(long)(2 * i) * T + m], x1 = x[(long)(2 * i + 1) * T + m];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        float s = 0.0f;
+        s = s + rope_jas_entry(2 * i + r, 2 * m, d) * x0;
+        s = s + rope_jas_entry(2 * i + r, 2 * m + 1, d) * x1;
+        y[(long)(2 * i + r) * T + m] = s;
+    }
+}
+
+__global__ void zero_row_kernel(float *y, int T)
+{
+    int m = blockIdx.x * blockDim.x + threadIdx.x;
+    if (m < T) y[m] = 0.0f;
+}
+
+// LLaMA rotary, interleaved pairs, angles in double (positions reach thousands of radians)
+__global__ void rope_llama_kernel(float *x, const int32_t *__restrict__ pos, int n, int nh, int dh, long tstride,
+                                  float theta)
+{
+    long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    int hp = dh / 2;
+    long total = (long)n * nh * hp;
+    if (g >= total) return;
+    int i = (int)(g % hp);
+    long r = g / hp;
+    int h = (int)(r % nh);
+    int t = (int)(r / nh);
+    double inv = pow((double)theta, -2.0 * i / (double)dh);
+    double a = (double)pos[t] * inv;
+    double c = cos(a), s = sin(a);
+    float *p = x + (long)t * tstride + (long)h * dh + 2 * i;
+    double x0 = p[0], x1 = p[1];
+    p[0] = (float)(x0 * c - x1 * s);
+    p[1] = (float)(x0 * s + x1 * c);
+}
+
+__global__ void embed_kernel(const float *__restrict__ wte, const float *__restrict__ wpe, const int32_t *__restrict__ ids,
+                             const int32_t *__restrict__ pos, float *__restrict__ out, int n, int d)
+{
+    long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= (long)n * d) return;
+    int t = (int)(g / d), e = (int)(g % d);
+    float v = wte[(long)ids[t] * d + e];
+    if (wpe) v = v + wpe[(long)pos[t] * d + e];
+    out[g] = v;
+}
+
+// argmax of each row; ties go to the lowest index (the first maximum, like a forward scan)
+__global__ void __launch_bounds__(256) argmax_kernel(const float *__restrict__ x, int V, long ld, int32_t *out)
+{
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const float *row = x + (long)blockIdx.x * ld;
+    float bv = -FLT_MAX;
+    int bi = 0x7fffffff;
+    for (int e = threadIdx.x; e < V; e += 256) {
+        float v = row[e];
+        if (v > bv) { bv = v; bi = e; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        float ov = __shfl_xor(bv, o, WAVE);
+        int oi = __shfl_xor(bi, o, WAVE);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    int w = threadIdx.x / WAVE;
+    if (threadIdx.x % WAVE == 0) { sv[w] = bv; si[w] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; ++k)
+            if (sv[k] > bv || (sv[k] == bv && si[k] < bi)) { bv = sv[k]; bi = si[k]; }
+        out[blockIdx.x] = bi == 0x7fffffff ? 0 : bi;
+    }
+}
+
+__global__ void fill_normal_kernel(float *x, size_t n, uint64_t key, float mean, float std)
+{
+    size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        uint64_t a = splitmix64(key + 2 * i), b = splitmix64(key + 2 * i + 1);
+        double u1 = ((double)(a >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+        double u2 = (double)(b >> 11) * (1.0 / 9007199254740992.0);
+        double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+        x[i] = (float)((double)mean + (double)std * z);
+    }
+}
+
+} // namespace jas
+
+using namespace jas;
+
+extern "C" {
+
+jas_status jas_rope_jasmine(const float *x, float *y, int d, int T, jas_stream_t stream)
+{
+    JAS_CHECK(x && y && d > 0 && T > 0, JAS_ERR_INVALID, "jas_rope_jasmine: bad arguments");
+    hipStream_t s = stream_or_default(stream);
+    long n = (long)(d / 2) * T;
+    if (n) hipLaunchKernelGGL(rope_jas_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, s, x, y, d, T);
+    if (d & 1)  // the odd trailing row of the zero-initialised result stays 0 (mat_RoPE_t.hpp:176-186)
+        hipLaunchKernelGGL(zero_row_kernel, dim3(ceil_div(T, 256)), dim3(256), 0, s, y + (long)(d - 1) * T, T);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
+jas_status jas_rope_llama(float *x, const int32_t *pos, int n, int nh, int dh, long tstride, float theta,
+                          jas_stream_t stream)
+{
+    JAS_CHECK(x && pos && n >= 0 && nh > 0 && dh > 0 && dh % 2 == 0, JAS_ERR_INVALID, "jas_rope_llama: bad arguments");
+    long total = (long)n * nh * (dh / 2);
+    if (total)
+        hipLaunchKernelGGL(rope_llama_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream_or_default(stream), x,
+                           pos, n, nh, dh, tstride, theta);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
+jas_status jas_embed(const float *wte, const float *wpe, const int32_t *ids, const int32_t *pos, float *out, int n,
+                     int d, jas_stream_t stream)
+{
+    JAS_CHECK(wte && ids && out && n >= 0 && d > 0 && (!wpe || pos), JAS_ERR_INVALID, "jas_embed: bad arguments");
+    long total = (long)n * d;
+    if (total)
+        hipLaunchKernelGGL(embed_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream_or_default(stream), wte, wpe,
+                           ids, pos, out, n, d);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
+jas_status jas_argmax(const float *x, int n, int V, long ld, int32_t *out, jas_stream_t stream)
+{
+    JAS_CHECK(x && out && n >= 0 && V > 0 && ld >= V, JAS_ERR_INVALID, "jas_argmax: bad arguments");
+    if (n) hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(256), 0, stream_or_default(stream), x, V, ld, out);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
+jas_status jas_fill_normal(float *x, size_t n, uint64_t seed, uint64_t stream_id, float mean, float std,
+                           jas_stream_t stream)
+{
+    JAS_CHECK(x || n == 0, JAS_ERR_INVALID, "jas_fill_normal: null pointer");
+    if (!n) return JAS_OK;
+    unsigned nb = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
+    hipLaunchKernelGGL(fill_normal_kernel, dim3(nb), dim3(256), 0, stream_or_default(stream), x, n,
+                       stream_key(seed, stream_id), mean, std);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
+} // extern "C"

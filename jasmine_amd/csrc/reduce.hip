@@ -1,0 +1,363 @@
+// Row reductions (north-star item 2): softmax, LayerNorm, RMSNorm, and jasmine's generic
+// sum/max/mean reductions.
+//
+// Reference: hsoftmax (mat_express_t.hpp:681-694) makes four materialised passes (hmax,
+// exp, hsum, divide); layer_norm_net_t::forward (mat_net_t.hpp:209-225) five (vmean, sub,
+// pow, vmean+sqrt, divide).  Here a row that fits the workgroup's registers is read from
+// HBM once and written once: wave64 shuffles (DPP) reduce inside a wave, LDS across waves.
+// Column-wise forms (jasmine's feature-major [d, T] LayerNorm normalises each column) map
+// one thread per column so the loads stay coalesced across columns.
+#include "jas_leaf.hpp"
+
+#include <cfloat>
+
+namespace jas {
+
+enum RowMode : int { RM_SOFTMAX = 0, RM_LN = 1, RM_RMS = 2 };
+
+template <int NT, int PER, int MODE, bool V4>
+__global__ void __launch_bounds__(NT)
+rowop_reg_kernel(const float *__restrict__ x, float *__restrict__ y, int len, long vstride, long ystride, float eps,
+                 const float *__restrict__ g, const float *__restrict__ bta)
+{
+    __shared__ float red[NT / WAVE];
+    const float *xr = x + (long)blockIdx.x * vstride;
+    float *yr = y + (long)blockIdx.x * ystride;
+    const int t = threadIdx.x;
+    float v[PER];
+    if (V4) {
+#pragma unroll
+        for (int k = 0; k < PER / 4; ++k) {
+            int e = (k * NT + t) * 4;
+            float4 q = e < len ? *(const float4 *)(xr + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+            v[4 * k] = q.x; v[4 * k + 1] = q.y; v[4 * k + 2] = q.z; v[4 * k + 3] = q.w;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            int e = k * NT + t;
+            v[k] = e < len ? xr[e] : 0.f;
+        }
+    }
+    auto idx = [&](int k) { return V4 ? ((k / 4) * NT + t) * 4 + (k % 4) : k * NT + t; };
+
+    if (MODE == RM_SOFTMAX) {
+        float m = -FLT_MAX;  // hmax starts from numeric_limits::lowest() (mat_express_t.hpp:619)
+#pragma unroll
+        for (int k = 0; k < PER; ++k)
+            if (idx(k) < len && v[k] > m) m = v[k];
+        m = block_max<NT>(m, red);
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            v[k] = idx(k) < len ? expf(v[k] - m) : 0.f;
+            s += v[k];
+        }
+        s = block_sum<NT>(s, red);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) v[k] = v[k] / s;
+    } else if (MODE == RM_LN) {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) s += v[k];  // padding is 0
+        float mean = block_sum<NT>(s, red) / (float)len;
+        float s2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            float d = idx(k) < len ? v[k] - mean : 0.f;
+            s2 += d * d;
+        }
+        float den = sqrtf(block_sum<NT>(s2, red) / (float)len + eps);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            int e = idx(k) < len ? idx(k) : 0;
+            v[k] = (v[k] - mean) / den * (g ? g[e] : 1.f) + (bta ? bta[e] : 0.f);
+        }
+    } else {
+        float s2 = 0.f;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) s2 += v[k] * v[k];
+        float den = sqrtf(block_sum<NT>(s2, red) / (float)len + eps);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            int e = idx(k) < len ? idx(k) : 0;
+            v[k] = v[k] / den * (g ? g[e] : 1.f);
+        }
+    }
+
+    if (V4) {
+#pragma unroll
+        for (int k = 0; k < PER / 4; ++k) {
+            int e = (k * NT + t) * 4;
+            if (e < len) *(float4 *)(yr + e) = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            int e = k * NT + t;
+            if (e < len) yr[e] = v[k];
+        }
+    }
+}
+
+// rows too long for registers: three passes over the row (later passes hit L2)
+template <int NT, int MODE>
+__global__ void __launch_bounds__(NT)
+rowop_loop_kernel(const float *__restrict__ x, float *__restrict__ y, int len, long vstride, long ystride, float eps,
+                  const float *__restrict__ g, const float *__restrict__ bta)
+{
+    __shared__ float red[NT / WAVE];
+    const float *xr = x + (long)blockIdx.x * vstride;
+    float *yr = y + (long)blockIdx.x * ystride;
+    const int t = threadIdx.x;
+    if (MODE == RM_SOFTMAX) {
+        float m = -FLT_MAX;
+        for (int e = t; e < len; e += NT) m = xr[e] > m ? xr[e] : m;
+        m = block_max<NT>(m, red);
+        float s = 0.f;
+        for (int e = t; e < len; e += NT) s += expf(xr[e] - m);
+        s = block_sum<NT>(s, red);
+        for (int e = t; e < len; e += NT) yr[e] = expf(xr[e] - m) / s;
+    } else if (MODE == RM_LN) {
+        float s = 0.f;
+        for (int e = t; e < len; e += NT) s += xr[e];
+        float mean = block_sum<NT>(s, red) / (float)len;
+        float s2 = 0.f;
+        for (int e = t; e < len; e += NT) { float d = xr[e] - mean; s2 += d * d; }
+        float den = sqrtf(block_sum<NT>(s2, red) / (float)len + eps);
+        for (int e = t; e < len; e += NT)
+            yr[e] = (xr[e] - mean) / den * (g ? g[e] : 1.f) + (bta ? bta[e] : 0.f);
+    } else {
+        float s2 = 0.f;
+        for (int e = t; e < len; e += NT) s2 += xr[e] * xr[e];
+        float den = sqrtf(block_sum<NT>(s2, red) / (float)len + eps);
+        for (int e = t; e < len; e += NT) yr[e] = xr[e] / den * (g ? g[e] : 1.f);
+    }
+}
+
+// column form: one thread per vector, sequential over the elements (coalesced when the
+// vectors are adjacent columns of a row-major matrix, vstride == 1)
+template <int MODE>
+__global__ void __launch_bounds__(256)
+rowop_col_kernel(const float *__restrict__ x, float *__restrict__ y, int n_vec, int len, long vstride, long ystride, long estride,
+                 float eps, const float *__restrict__ g, const float *__restrict__ bta)
+{
+    int v = blockIdx.x * blockDim.x + threadIdx.x;
+    if (v >= n_vec) return;
+    const float *xr = x + (long)v * vstride;
+    float *yr = y + (long)v * ystride;
+    if (MODE == RM_SOFTMAX) {
+        float m = -FLT_MAX;
+        for (int e = 0; e < len; ++e) m = xr[e * estride] > m ? xr[e * estride] : m;
+        float s = 0.f;
+        for (int e = 0; e < len; ++e) s += expf(xr[e * estride] - m);
+        for (int e = 0; e < len; ++e) yr[e * estride] = expf(xr[e * estride] - m) / s;
+    } else if (MODE == RM_LN) {
+        float s = 0.f;
+        for (int e = 0; e < len; ++e) s += xr[e * estride];
+        float mean = s / (float)len;
+        float s2 = 0.f;
+        for (int e = 0; e < len; ++e) { float d = xr[e * estride] - mean; s2 += d * d; }
+        float den = sqrtf(s2 / (float)len + eps);
+        for (int e = 0; e < len; ++e)
+            yr[e * estride] = (xr[e * estride] - mean) / den * (g ? g[e] : 1.f) + (bta ? bta[e] : 0.f);
+    } else {
+        float s2 = 0.f;
+        for (int e = 0; e < len; ++e) s2 += xr[e * estride] * xr[e * estride];
+        float den = sqrtf(s2 / (float)len + eps);
+        for (int e = 0; e < len; ++e) yr[e * estride] = xr[e * estride] / den * (g ? g[e] : 1.f);
+    }
+}
+
+template <int NT, int PER, int MODE>
+static void launch_reg(const float *x, float *y, int n_vec, int len, long vstride, long ystride, float eps,
+                       const float *g, const float *b, bool v4, hipStream_t s)
+{
+    if (v4)
+        hipLaunchKernelGGL((rowop_reg_kernel<NT, PER, MODE, true>), dim3(n_vec), dim3(NT), 0, s, x, y, len, vstride,
+                           ystride, eps, g, b);
+    else
+        hipLaunchKernelGGL((rowop_reg_kernel<NT, PER, MODE, false>), dim3(n_vec), dim3(NT), 0, s, x, y, len, vstride,
+                           ystride, eps, g, b);
+}
+
+template <int MODE>
+static jas_status rowop(const float *x, float *y, int n_vec, int len, long vstride, long ystride, long estride,
+                        float eps, const float *g, const float *b, jas_stream_t stream)
+{
+    JAS_CHECK(x && y, JAS_ERR_INVALID, "row op: null pointer");
+    JAS_CHECK(n_vec >= 0 && len > 0, JAS_ERR_INVALID, "row op: bad shape");
+    if (n_vec == 0) return JAS_OK;
+    JAS_CHECK(n_vec < (1 << 30), JAS_ERR_INVALID, "row op: too many vectors");
+    hipStream_t s = stream_or_default(stream);
+    if (estride != 1) {
+        hipLaunchKernelGGL((rowop_col_kernel<MODE>), dim3(ceil_div(n_vec, 256)), dim3(256), 0, s, x, y, n_vec, len,
+                           vstride, ystride, estride, eps, g, b);
+        JAS_LAUNCH_CHECK();
+        return JAS_OK;
+    }
+    bool v4 = (len % 4 == 0) && (vstride % 4 == 0) && (ystride % 4 == 0) && ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0);
+    if (len <= 256) launch_reg<64, 4, MODE>(x, y, n_vec, len, vstride, ystride, eps, g, b, v4, s);
+    else if (len <= 512) launch_reg<64, 8, MODE>(x, y, n_vec, len, vstride, ystride, eps, g, b, v4, s);
+    else if (len <= 1024) launch_reg<128, 8, MODE>(x, y, n_vec, len, vstride, ystride, eps, g, b, v4, s);
+    else if (len <= 2048) launch_reg<256, 8, MODE>(x, y, n_vec, len, vstride, ystride, eps, g, b, v4, s);
+    else if (len <= 4096) launch_reg<256, 16, MODE>(x, y, n_vec, len, vstride, ystride, eps, g, b, v4, s);
+    else if (len <= 8192) launch_reg<256, 32, MODE>(x, y, n_vec, len, vstride, ystride, eps, g, b, v4, s);
+    else if (len <= 16384) launch_reg<512, 32, MODE>(x, y, n_vec, len, vstride, ystride, eps, g, b, v4, s);
+    else hipLaunchKernelGGL((rowop_loop_kernel<512, MODE>), dim3(n_vec), dim3(512), 0, s, x, y, len, vstride, ystride, eps, g, b);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
+// ---------------- whole-matrix softmax (mat_softmax_t, mat_express_t.hpp:642-659) ----------------
+// pass 1: per block (max, sum exp(x - local max)); pass 2: one block combines; pass 3: write.
+__global__ void __launch_bounds__(256) gsm_partial_kernel(const float *__restrict__ x, long n, float2 *part)
+{
+    __shared__ float red[4];
+    float m = -FLT_MAX;
+    long stride = (long)gridDim.x * 256;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) m = x[i] > m ? x[i] : m;
+    m = block_max<256>(m, red);
+    float s = 0.f;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) s += expf(x[i] - m);
+    s = block_sum<256>(s, red);
+    if (threadIdx.x == 0) part[blockIdx.x] = make_float2(m, s);
+}
+
+__global__ void __launch_bounds__(256) gsm_combine_kernel(float2 *part, int nb)
+{
+    __shared__ float red[4];
+    float m = -FLT_MAX;
+    for (int i = threadIdx.x; i < nb; i += 256) m = part[i].x > m ? part[i].x : m;
+    m = block_max<256>(m, red);
+    float s = 0.f;
+    for (int i = threadIdx.x; i < nb; i += 256) s += part[i].y * expf(part[i].x - m);
+    s = block_sum<256>(s, red);
+    __syncthreads();
+    if (threadIdx.x == 0) part[nb] = make_float2(m, s);
+}
+
+__global__ void __launch_bounds__(256) gsm_write_kernel(const float *__restrict__ x, float *y, long n, const float2 *ms)
+{
+    float2 r = *ms;
+    long stride = (long)gridDim.x * 256;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) y[i] = expf(x[i] - r.x) / r.y;
+}
+
+// ---------------- generic reductions over a leaf (mat_express_t.hpp:511-628) ----------------
+// Per-row and per-column forms use one thread per output and accumulate sequentially in
+// the output type, exactly the order jasmine's loops use (hsum :548-564, vsum :530-546).
+template <typename T>
+__device__ __forceinline__ T leaf_get(const LeafDev &L, int i, int j)
+{
+    return (T)load_elem(L.p, leaf_index(L, i, j), L.dtype);
+}
+
+template <typename T>
+__global__ void reduce_line_kernel(LeafDev L, int rows, int cols, int op, int axis, T *out)
+{
+    int o = blockIdx.x * blockDim.x + threadIdx.x;
+    int n_out = axis == 0 ? rows : cols;
+    if (o >= n_out) return;
+    int len = axis == 0 ? cols : rows;
+    T acc = op == 1 ? -std::numeric_limits<T>::max() : (T)0;
+    for (int k = 0; k < len; ++k) {
+        T v = axis == 0 ? leaf_get<T>(L, o, k) : leaf_get<T>(L, k, o);
+        if (op == 1) acc = v > acc ? v : acc;
+        else acc += v;
+    }
+    if (op == 2) acc = acc / (T)len;  // vmean / hmean: ele / int (mat_express_t.hpp:566-578)
+    out[o] = acc;
+}
+
+// whole-matrix: per-row sequential partials, then a sequential pass over the partials
+template <typename T>
+__global__ void reduce_all_kernel(const T *rowpart, int rows, int cols, int op, T *out)
+{
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    T acc = op == 1 ? -std::numeric_limits<T>::max() : (T)0;
+    for (int r = 0; r < rows; ++r) {
+        if (op == 1) acc = rowpart[r] > acc ? rowpart[r] : acc;
+        else acc += rowpart[r];
+    }
+    if (op == 2) acc = acc / (T)((long)rows * cols);  // mean (mat_express_t.hpp:580-585)
+    out[0] = acc;
+}
+
+template <typename T>
+static jas_status reduce_t(const jas_leaf *in, int op, int axis, void *d_out, hipStream_t s)
+{
+    int rows = in->vrows, cols = in->vcols;
+    LeafDev L = classify(*in, rows, cols);
+    if (L.kind == LK_CONTIG) {  // contiguous row-major: strided form of the same address
+        L.kind = LK_STRIDED;
+        L.rs = cols;
+        L.cs = 1;
+    }
+    if (axis == 0 || axis == 1) {
+        int n_out = axis == 0 ? rows : cols;
+        hipLaunchKernelGGL(reduce_line_kernel<T>, dim3(ceil_div(n_out, 128)), dim3(128), 0, s, L, rows, cols, op,
+                           axis, (T *)d_out);
+        JAS_LAUNCH_CHECK();
+        return JAS_OK;
+    }
+    T *part = (T *)workspace(sizeof(T) * (size_t)rows, s);
+    JAS_CHECK(part, JAS_ERR_OOM, "jas_reduce: workspace allocation failed");
+    hipLaunchKernelGGL(reduce_line_kernel<T>, dim3(ceil_div(rows, 128)), dim3(128), 0, s, L, rows, cols,
+                       op == 2 ? 0 : op, 0, part);
+    hipLaunchKernelGGL(reduce_all_kernel<T>, dim3(1), dim3(64), 0, s, part, rows, cols, op, (T *)d_out);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
+} // namespace jas
+
+using namespace jas;
+
+extern "C" {
+
+jas_status jas_softmax(const float *x, float *y, int n_vec, int len, long vstride, long ystride, long estride,
+                       jas_stream_t s)
+{
+    return rowop<RM_SOFTMAX>(x, y, n_vec, len, vstride, ystride, estride, 0.f, nullptr, nullptr, s);
+}
+
+jas_status jas_layernorm(const float *x, float *y, int n_vec, int len, long vstride, long ystride, long estride,
+                         float eps, const float *g, const float *b, jas_stream_t s)
+{
+    return rowop<RM_LN>(x, y, n_vec, len, vstride, ystride, estride, eps, g, b, s);
+}
+
+jas_status jas_rmsnorm(const float *x, float *y, int n_vec, int len, long vstride, long ystride, long estride,
+                       float eps, const float *g, jas_stream_t s)
+{
+    return rowop<RM_RMS>(x, y, n_vec, len, vstride, ystride, estride, eps, g, nullptr, s);
+}
+
+jas_status jas_softmax_global(const float *x, float *y, long n, jas_stream_t stream)
+{
+    JAS_CHECK(x && y && n > 0, JAS_ERR_INVALID, "jas_softmax_global: bad arguments");
+    hipStream_t s = stream_or_default(stream);
+    int nb = (int)std::min<long>(1024, (n + 255) / 256);
+    float2 *part = (float2 *)workspace(sizeof(float2) * (nb + 1), s);
+    JAS_CHECK(part, JAS_ERR_OOM, "jas_softmax_global: workspace allocation failed");
+    hipLaunchKernelGGL(gsm_partial_kernel, dim3(nb), dim3(256), 0, s, x, n, part);
+    hipLaunchKernelGGL(gsm_combine_kernel, dim3(1), dim3(256), 0, s, part, nb);
+    hipLaunchKernelGGL(gsm_write_kernel, dim3(nb), dim3(256), 0, s, x, y, n, (const float2 *)(part + nb));
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
+jas_status jas_reduce(const jas_leaf *in, int op, int axis, void *d_out, int32_t out_dtype, jas_stream_t stream)
+{
+    JAS_CHECK(in && d_out, JAS_ERR_INVALID, "jas_reduce: null argument");
+    JAS_CHECK(op >= 0 && op <= 2 && axis >= 0 && axis <= 2, JAS_ERR_INVALID, "jas_reduce: bad op/axis");
+    JAS_CHECK(in->vrows > 0 && in->vcols > 0 && in->rows > 0 && in->cols > 0, JAS_ERR_INVALID,
+              "jas_reduce: empty input");
+    hipStream_t s = stream_or_default(stream);
+    if (out_dtype == JAS_F64) return reduce_t<double>(in, op, axis, d_out, s);
+    JAS_CHECK(out_dtype == JAS_F32, JAS_ERR_INVALID, "jas_reduce: out dtype must be f32 or f64");
+    return reduce_t<float>(in, op, axis, d_out, s);
+}
+
+} // extern "C"

@@ -1,0 +1,320 @@
+// ref_driver.cpp -- TEST INFRASTRUCTURE ONLY.
+//
+// Builds the jasmine reference itself (its headers are included by path from the
+// reference checkout, nothing is copied) into oracle/_ref/libjasref.so, with plain
+// C entry points so tests can (a) pin the C restatement in oracle.c against the real
+// reference and (b) write the golden fixtures under tests/golden/, and bench.py can
+// time the reference CPU path as its cpu_baseline ("kind": "reference").
+//
+// Weights are injected through jasmine's own initialiser hook: init_matrix<I>(m)
+// dispatches to init_t<I>::cal (mat_init_t.hpp:10-18,113-118), and every net's
+// init_weight<I>() visits its matrices in a fixed order (mat_net_t.hpp:51-56,
+// mat_mha_t.hpp:141-147,384-392, mat_transformer_kernel_t.hpp:166-176,340-352).
+// fixture_init_t fills each visited matrix row-major from a caller buffer.
+#include <chrono>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+
+#include "mat_t.hpp"
+#include "mat_express_t.hpp"
+#include "mat_view_t.hpp"
+#include "mat_net_t.hpp"
+#include "mat_init_t.hpp"
+#include "mat_mha_t.hpp"
+#include "mat_transformer_kernel_t.hpp"
+#include "mat_RoPE_t.hpp"
+#include "mat_transformer_t.hpp"
+
+struct fixture_init_t;
+static const float *g_fixture = nullptr;
+static size_t g_fixture_pos = 0;
+
+template <>
+struct init_t<fixture_init_t>
+{
+    template <typename mat_type>
+    requires is_matrix<mat_type>
+    static void cal(mat_type &m)
+    {
+        for (int i = 0; i < m.row_num(); ++i)
+            for (int j = 0; j < m.col_num(); ++j)
+                m(i, j) = g_fixture[g_fixture_pos++];
+    }
+};
+
+// tanh as a jasmine unary node, built on the reference's own CRTP base
+// (mat_express_t.hpp:360-436) exactly like mat_exp_t (:439-469).
+template <typename val_type>
+class ref_tanh_t : public mat_express_1_param_stable_t<val_type, ref_tanh_t>
+{
+public:
+    using base_type = mat_express_1_param_stable_t<val_type, ref_tanh_t>;
+    using ele_type = typename val_type::ele_type;
+    using val_base_type = typename base_type::val_base_type;
+    ref_tanh_t(val_type const &v) : base_type(v) {}
+    auto work(val_base_type i) const { return std::tanh(i); }
+    static std::string type_name() { return "ref_tanh_t"; }
+};
+template <typename val_type>
+auto ref_tanh(val_type const &v) { return ref_tanh_t<val_type>(v); }
+
+static mat_t<float> to_mat(const float *p, int R, int C)
+{
+    mat_t<float> m(R, C);
+    for (int i = 0; i < R; ++i)
+        for (int j = 0; j < C; ++j) m(i, j) = p[(long)i * C + j];
+    return m;
+}
+
+template <typename M>
+static void from_mat(const M &m, float *out)
+{
+    int R = m.row_num(), C = m.col_num();
+    for (int i = 0; i < R; ++i)
+        for (int j = 0; j < C; ++j) out[(long)i * C + j] = static_cast<float>(m(i, j));
+}
+
+template <typename T>
+using upd_t = sgd_t<T>;
+
+extern "C" {
+
+// mat_t::dot -> mat_dot_t clone (mat_express_t.hpp:730-776)
+void ref_gemm(int M, int N, int K, const float *A, const float *B, float *C)
+{
+    auto a = to_mat(A, M, K), b = to_mat(B, K, N);
+    mat_t<float> c = a.dot(b).clone();
+    from_mat(c, C);
+}
+
+// A.t().dot(B) through mat_view_t transposition (mat_view_t.hpp:97-102)
+void ref_gemm_tn(int M, int N, int K, const float *A /*[K,M]*/, const float *B, float *C)
+{
+    auto a = to_mat(A, K, M), b = to_mat(B, K, N);
+    mat_t<float> c = a.t().dot(b).clone();
+    from_mat(c, C);
+}
+
+void ref_cfg2_expr(const float *A, const float *B, const float *C, float *D, int R, int Cc)
+{
+    auto a = to_mat(A, R, Cc), b = to_mat(B, R, Cc), c = to_mat(C, R, Cc);
+    mat_t<float> d = (a * b + 0.5 * c - ref_tanh(a)).clone();
+    from_mat(d, D);
+}
+
+// generic small expressions used to pin the ew interpreter: id selects the tree.
+void ref_expr(int id, const float *A, int ar, int ac, const float *B, int br, int bc,
+              float *out, int *out_r, int *out_c)
+{
+    auto a = to_mat(A, ar, ac), b = to_mat(B, br, bc);
+    mat_t<float> r;
+    switch (id) {
+    case 0: r = (a + b).clone(); break;
+    case 1: r = (a - b * 2).clone(); break;
+    case 2: r = (a * b / (b + 3.0)).clone(); break;
+    case 3: r = exp(a - b).clone(); break;
+    case 4: r = sigmoid(a * b).clone(); break;
+    case 5: r = ((a > b) * a + (a < b) * b).clone(); break;
+    case 6: r = ((a + b - a) * b / a).clone(); break;
+    case 7: r = (a - 1.5f).clone(); break;
+    case 8: r = (2 - a).clone(); break;
+    case 9: r = (a.t() * 0.25 + b).clone(); break;
+    default: throw std::invalid_argument("ref_expr id");
+    }
+    *out_r = r.row_num();
+    *out_c = r.col_num();
+    if (out) from_mat(r, out);
+}
+
+void ref_hsoftmax(const float *X, int R, int C, float *Y)
+{
+    auto x = to_mat(X, R, C);
+    mat_t<float> y = hsoftmax(x);
+    from_mat(y, Y);
+}
+
+void ref_softmax_global(const float *X, int R, int C, float *Y)
+{
+    auto x = to_mat(X, R, C);
+    mat_t<float> y = softmax(x).clone();
+    from_mat(y, Y);
+}
+
+void ref_reductions(const float *X, int R, int C, float *hs, float *vs, float *hm,
+                    float *vmn, float *hmn, float *scalars /*sum,max,mean*/)
+{
+    auto x = to_mat(X, R, C);
+    from_mat(hsum(x), hs);
+    from_mat(vsum(x), vs);
+    from_mat(hmax(x), hm);
+    from_mat(vmean(x), vmn);
+    from_mat(hmean(x), hmn);
+    scalars[0] = sum(x);
+    scalars[1] = max(x);
+    scalars[2] = mean(x);
+}
+
+void ref_linear(const float *W, const float *b, const float *X, int out, int in, int T, float *Y)
+{
+    weight_net_t<mat_t<float>, upd_t> net(in, out);
+    std::vector<float> buf((size_t)out * in + out);
+    memcpy(buf.data(), W, sizeof(float) * out * in);
+    memcpy(buf.data() + (size_t)out * in, b, sizeof(float) * out);
+    g_fixture = buf.data(); g_fixture_pos = 0;
+    net.init_weight<fixture_init_t>();
+    auto x = to_mat(X, in, T);
+    from_mat(net.forward(x), Y);
+}
+
+void ref_relu(const float *X, int R, int C, float *Y)
+{
+    relu_net_t<mat_t<float>> n;
+    from_mat(n.forward(to_mat(X, R, C)), Y);
+}
+
+void ref_sigmoid(const float *X, int R, int C, float *Y)
+{
+    sigmoid_net_t<mat_t<float>> n;
+    from_mat(n.forward(to_mat(X, R, C)), Y);
+}
+
+void ref_layernorm_cols(const float *X, int R, int C, float *Y)
+{
+    layer_norm_net_t<mat_t<float>, upd_t> n;
+    from_mat(n.forward(to_mat(X, R, C)), Y);
+}
+
+// mat_head_gen_t self (Xkv == NULL) or cross attention
+void ref_head(const float *Xq, const float *Xkv, int dh, int Tq, int Tk, const float *W, int mask, float *Y)
+{
+    mat_head_gen_t<mat_t<float>, upd_t> head(dh, mask != 0, Tq);
+    g_fixture = W; g_fixture_pos = 0;
+    head.init_weight<fixture_init_t>();
+    auto xq = to_mat(Xq, dh, Tq);
+    if (!Xkv) {
+        from_mat(head.forward(xq.view()), Y);
+    } else {
+        auto xk = to_mat(Xkv, dh, Tk);
+        from_mat(head.forward(xq.view(), xk.view()), Y);
+    }
+}
+
+void ref_mha(const float *Xq, const float *Xkv, int d, int H, int Tq, int Tk, const float *W, int mask, float *Y)
+{
+    mat_mha_t<mat_t<float>, upd_t> mha(H, d, mask != 0, Tq);
+    g_fixture = W; g_fixture_pos = 0;
+    mha.init_weight<fixture_init_t>();
+    auto xq = to_mat(Xq, d, Tq);
+    if (!Xkv) {
+        from_mat(mha.forward(xq), Y);
+    } else {
+        auto xk = to_mat(Xkv, d, Tk);
+        from_mat(mha.forward(xq, xk), Y);
+    }
+}
+
+void ref_rope(const float *X, int d, int T, float *Y)
+{
+    RoPE_net_t<mat_t<float>> r(d);
+    from_mat(r.forward(to_mat(X, d, T)), Y);
+}
+
+// transformer_base_t: encoder_forward then forward (mat_transformer_t.hpp:36-44)
+void ref_transformer(const float *en, int Te, const float *de, int Td, int d, int H,
+                     int n_enc, int n_dec, const float *W, float *Y)
+{
+    transformer_base_t<mat_t<float>, upd_t> tf(n_enc, n_dec, H, d);
+    g_fixture = W; g_fixture_pos = 0;
+    tf.init_weight<fixture_init_t>();
+    tf.encoder_forward(to_mat(en, d, Te));
+    from_mat(tf.forward(to_mat(de, d, Td)), Y);
+}
+
+// number of parameters transformer_base_t::init_weight visits (for buffer sizing)
+long ref_transformer_nparams(int d, int H, int n_enc, int n_dec)
+{
+    transformer_base_t<mat_t<float>, upd_t> tf(n_enc, n_dec, H, d);
+    static std::vector<float> zeros;
+    zeros.assign(1 << 24, 0.0f);
+    g_fixture = zeros.data(); g_fixture_pos = 0;
+    tf.init_weight<fixture_init_t>();
+    return (long)g_fixture_pos;
+}
+
+// ---- CPU-baseline timers (seconds per call of the reference code path) ----
+// weight_net_t::forward at a real projection shape (mat_net_t.hpp:38-49)
+double ref_time_linear(int out, int in, int T, int reps)
+{
+    weight_net_t<mat_t<float>, upd_t> net(in, out);
+    std::vector<float> buf((size_t)out * in + out);
+    for (size_t i = 0; i < buf.size(); ++i) buf[i] = (float)((i * 2654435761u) % 1000) * 1e-5f;
+    g_fixture = buf.data(); g_fixture_pos = 0;
+    net.init_weight<fixture_init_t>();
+    mat_t<float> x(in, T);
+    for (int i = 0; i < in; ++i)
+        for (int j = 0; j < T; ++j) x(i, j) = 0.001f * (float)((i + j) % 7);
+    volatile float sink = 0.0f;
+    auto t0 = std::chrono::steady_clock::now();
+    for (int r = 0; r < reps; ++r) {
+        auto y = net.forward(x);
+        sink = sink + y(0, 0);
+    }
+    auto t1 = std::chrono::steady_clock::now();
+    return std::chrono::duration<double>(t1 - t0).count() / reps;
+}
+
+// the config-2 fused expression, R x C (mat_express_t.hpp:96-107 clone loop)
+double ref_time_cfg2(int R, int C, int reps)
+{
+    mat_t<float> a(R, C), b(R, C), c(R, C);
+    for (int i = 0; i < R; ++i)
+        for (int j = 0; j < C; ++j) { a(i, j) = 0.1f * (float)((i + j) % 13); b(i, j) = 0.5f; c(i, j) = 1.0f; }
+    volatile double sink = 0;
+    auto t0 = std::chrono::steady_clock::now();
+    for (int r = 0; r < reps; ++r) {
+        mat_t<float> d = (a * b + 0.5 * c - ref_tanh(a)).clone();
+        sink = sink + d(0, 0);
+    }
+    auto t1 = std::chrono::steady_clock::now();
+    return std::chrono::duration<double>(t1 - t0).count() / reps;
+}
+
+// hsoftmax at R x C (mat_express_t.hpp:681-694)
+double ref_time_hsoftmax(int R, int C, int reps)
+{
+    mat_t<float> a(R, C);
+    for (int i = 0; i < R; ++i)
+        for (int j = 0; j < C; ++j) a(i, j) = 0.1f * (float)((i * 7 + j) % 13);
+    volatile float sink = 0;
+    auto t0 = std::chrono::steady_clock::now();
+    for (int r = 0; r < reps; ++r) {
+        mat_t<float> y = hsoftmax(a);
+        sink = sink + y(0, 0);
+    }
+    auto t1 = std::chrono::steady_clock::now();
+    return std::chrono::duration<double>(t1 - t0).count() / reps;
+}
+
+// one masked mat_head_gen_t forward of T tokens at head dim dh (mat_mha_t.hpp:45-74)
+double ref_time_head(int dh, int T, int reps)
+{
+    mat_head_gen_t<mat_t<float>, upd_t> head(dh, true, T);
+    std::vector<float> buf(3 * ((size_t)dh * dh + dh), 0.01f);
+    g_fixture = buf.data(); g_fixture_pos = 0;
+    head.init_weight<fixture_init_t>();
+    mat_t<float> x(dh, T);
+    for (int i = 0; i < dh; ++i)
+        for (int j = 0; j < T; ++j) x(i, j) = 0.01f * (float)((i + 3 * j) % 11);
+    volatile float sink = 0;
+    auto t0 = std::chrono::steady_clock::now();
+    for (int r = 0; r < reps; ++r) {
+        auto y = head.forward(x.view());
+        sink = sink + y(0, 0);
+    }
+    auto t1 = std::chrono::steady_clock::now();
+    return std::chrono::duration<double>(t1 - t0).count() / reps;
+}
+
+} // extern "C"

@@ -1,0 +1,116 @@
+"""GPU decoder-LM parity (configs 1, 4-shape, 5-architecture) against the CPU oracle.
+
+The GPU model is initialised on the device from the shared counter-based generator; its
+weights are copied back and handed to the oracle, so both sides run the same numbers.
+Logits: |gpu - cpu| <= 1e-3 + 1e-4 |cpu| at every step, with teacher forcing on the CPU's
+greedy ids so one near-tie cannot cascade.  Greedy ids must match wherever the CPU top-2
+margin exceeds that tolerance (near-ties are counted and reported, not failed).
+"""
+import numpy as np
+import pytest
+
+from oracle_lib import orc, fp, ip, randint, LmCfg, LmWeights, LM_WEIGHT_FIELDS
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 1e-3, 1e-4
+
+
+def close(a, b, atol=ATOL, rtol=RTOL):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    err = np.abs(a - b)
+    assert np.all(err <= atol + rtol * np.abs(b)), f"max abs err {err.max():.3g}"
+
+
+def oracle_for(jas, lm, cfg):
+    w = {n: lm.weight(n) for n in LM_WEIGHT_FIELDS}
+    ocfg = LmCfg(cfg.kind, cfg.n_layer, cfg.d_model, cfg.n_head, cfg.d_ff, cfg.vocab, cfg.max_ctx, cfg.eps,
+                 cfg.rope_theta)
+    ow = LmWeights(*[fp(w[n]) if w[n] is not None else None for n in LM_WEIGHT_FIELDS])
+    return ocfg, ow, w
+
+
+def run_parity(jas, cfg, seed, B, P, steps, prompt_seed):
+    lm = jas.Lm(cfg)
+    lm.init_random(seed, 0.02)
+    ocfg, ow, keep = oracle_for(jas, lm, cfg)
+    prompt = randint((B, P), cfg.vocab, prompt_seed)
+    cpu_ids = np.zeros((B, steps), np.int32)
+    cpu_logits = np.zeros((steps, B, cfg.vocab), np.float32)
+    orc.orc_lm_generate(ocfg, ow, B, P, ip(prompt), steps, None, ip(cpu_ids), fp(cpu_logits), 16)
+
+    nxt, lg = lm.prefill(prompt, want_logits=True)
+    gpu_logits = [lg]
+    gpu_ids = [nxt]
+    for s in range(1, steps):
+        nxt, lg = lm.decode(cpu_ids[:, s - 1], want_logits=True)  # teacher forcing
+        gpu_logits.append(lg)
+        gpu_ids.append(nxt)
+    gpu_logits = np.stack(gpu_logits)
+    gpu_ids = np.stack(gpu_ids, 1)
+    close(gpu_logits, cpu_logits)
+    srt = np.sort(cpu_logits, -1)
+    margin = (srt[..., -1] - srt[..., -2]).T  # [B, steps]
+    decisive = margin > ATOL + RTOL * np.abs(srt[..., -1]).T
+    assert np.all(gpu_ids[decisive] == cpu_ids[decisive])
+    return lm, prompt, cpu_ids, int((~decisive).sum())
+
+
+def test_config1_tiny_gpt2(jas):
+    # config 1: 2 layers, d 128, 4 heads, FFN 512 GELU, pre-LN eps 1e-5, learned positions,
+    # vocab 256, context 64; weights N(0, 0.02) from seed 0; 32-token prompt (seed 0); 32 steps
+    cfg = jas.LmConfig(0, 2, 128, 4, 512, 256, 64, 1, 1e-5, 10000.0)
+    lm, prompt, cpu_ids, ties = run_parity(jas, cfg, seed=0, B=1, P=32, steps=32, prompt_seed=0)
+    # free-running greedy generation on the device reproduces the CPU ids exactly
+    first, _ = lm.prefill(prompt)
+    ids = np.concatenate([first[:, None], lm.generate(31, 1).T], 1)
+    if ties == 0:
+        assert np.array_equal(ids, cpu_ids)
+
+
+def test_llama_architecture_small(jas):
+    # LLaMA block (RMSNorm eps 1e-6, RoPE theta 1e4 on q/k, SwiGLU, untied head), head dim 128
+    cfg = jas.LmConfig(1, 2, 256, 2, 512, 320, 48, 3, 1e-6, 10000.0)
+    run_parity(jas, cfg, seed=4, B=3, P=20, steps=8, prompt_seed=4)
+
+
+def test_gpt2_small_shape(jas):
+    # config 4 shape (12 layers, d 768, 12 heads, FFN 3072, vocab 50257, ctx 1024, seed 3),
+    # 2 sequences x 24-token prompts x 3 steps (the oracle is the bound here, not the GPU)
+    cfg = jas.LmConfig(0, 12, 768, 12, 3072, 50257, 1024, 2, 1e-5, 10000.0)
+    run_parity(jas, cfg, seed=3, B=2, P=24, steps=3, prompt_seed=3)
+
+
+def test_kv_cache_equals_recompute(jas):
+    # jasmine's decode (transformer_test.hpp:231-238) recomputes the whole prefix each step;
+    # the KV-cache step must give the last column of that recompute.
+    cfg = jas.LmConfig(1, 2, 128, 2, 256, 200, 40, 2, 1e-6, 10000.0)
+    lm = jas.Lm(cfg)
+    lm.init_random(7, 0.02)
+    prompt = randint((2, 9), 200, 7)
+    nxt, _ = lm.prefill(prompt)
+    seq = [prompt, nxt[:, None]]
+    lg = None
+    for _ in range(5):
+        nxt, lg = lm.decode(nxt, want_logits=True)
+        seq.append(nxt[:, None])
+    full = np.concatenate(seq[:-1], 1)
+    lm2 = jas.Lm(cfg)
+    lm2.init_random(7, 0.02)
+    _, lg_full = lm2.prefill(full, want_logits=True)
+    close(lg, lg_full, atol=1e-4, rtol=1e-4)
+
+
+def test_lm_errors(jas):
+    from jasmine_amd import JasError
+    with pytest.raises(JasError, match="divisible"):
+        jas.Lm(jas.LmConfig(0, 1, 128, 3, 256, 10, 8, 1, 1e-5, 1e4))
+    cfg = jas.LmConfig(0, 1, 64, 2, 128, 50, 8, 1, 1e-5, 1e4)
+    lm = jas.Lm(cfg)
+    lm.init_random(1)
+    with pytest.raises(JasError):
+        lm.prefill(np.array([[1, 2, 99]], np.int32))  # id out of vocab
+    lm.prefill(np.array([[1, 2, 3, 4, 5, 6, 7]], np.int32))
+    lm.decode(np.array([1], np.int32))
+    with pytest.raises(JasError, match="max_ctx"):  # KV cache capacity (8)
+        lm.decode(np.array([1], np.int32))

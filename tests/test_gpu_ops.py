@@ -1,0 +1,346 @@
+"""GPU parity of every kernel behind the C ABI against the CPU oracle / golden vectors.
+
+Tolerance (fp32): |gpu - ref| <= 1e-3 + 1e-4 * |ref| (max-abs 1e-3, rel 1e-4), the
+north-star bound.  Paths whose arithmetic order matches jasmine exactly (per-column
+reductions, elementwise trees) are additionally checked for bit-exactness.  bf16
+attention: |gpu - fp32 ref| <= 2e-2 + 2e-2 * |ref|.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import ewexpr as E
+from oracle_lib import orc, fp, normal
+
+pytestmark = pytest.mark.gpu
+
+
+def close(a, b, atol=1e-3, rtol=1e-4):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    err = np.abs(a - b) - (atol + rtol * np.abs(b))
+    assert a.shape == b.shape, (a.shape, b.shape)
+    assert np.all(np.isfinite(a) == np.isfinite(b)), "non-finite mismatch"
+    fin = np.isfinite(b)
+    assert np.all(err[fin] <= 0), f"max abs err {np.max(np.abs(a - b)[fin]):.3g}"
+
+
+def bitfrac(a, b):
+    return float(np.mean(np.asarray(a, np.float32).view(np.uint32) == np.asarray(b, np.float32).view(np.uint32)))
+
+
+# ---------------------------------------------------------------- expressions
+GOLD_TREES = {
+    0: lambda a, b: a + b,
+    1: lambda a, b: a - b * 2,
+    2: lambda a, b: a * b / (b + 3.0),
+    3: lambda a, b: E.un("exp", a - b),
+    4: lambda a, b: E.un("sigmoid", a * b),
+    5: lambda a, b: (a > b) * a + (a < b) * b,
+    6: lambda a, b: (a + b - a) * b / a,
+    7: lambda a, b: a - E.const(1.5, E.F32),
+    8: lambda a, b: 2 - a,
+}
+
+
+def test_ew_golden(jas):
+    g = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "jasmine_golden.npz"))
+    n = 0
+    while f"expr{n}_id" in g:
+        eid = int(g[f"expr{n}_id"])
+        a_h, b_h, want = g[f"expr{n}_a"], g[f"expr{n}_b"], g[f"expr{n}_out"]
+        da, db = jas.to_device(a_h), jas.to_device(b_h)
+        if eid == 9:  # a.t() * 0.25 + b : transposed view of a
+            tree = E.leaf(da, transposed=1) * 0.25 + E.leaf(db)
+        else:
+            tree = GOLD_TREES[eid](E.leaf(da), E.leaf(db))
+        got = E.evaluate(jas, tree).astype(np.float32)
+        close(got, want)
+        if eid not in (3, 4):  # pure +-*/ and compares are bit-exact with jasmine
+            assert bitfrac(got, want) == 1.0, (n, eid)
+        n += 1
+    assert n >= 13
+
+
+@pytest.mark.parametrize("shape", [(64, 64), (33, 65), (1024, 1024), (8192, 1024)])
+def test_ew_cfg2(jas, shape):
+    R, Cc = shape
+    a, b, c = normal(shape, 1, 0), normal(shape, 1, 1), normal(shape, 1, 2)
+    want = np.zeros_like(a)
+    orc.orc_cfg2_expr(fp(a), fp(b), fp(c), fp(want), a.size)
+    da, db, dc = jas.to_device(a), jas.to_device(b), jas.to_device(c)
+    A, B, C = E.leaf(da), E.leaf(db), E.leaf(dc)
+    tree = A * B + 0.5 * C - E.un("tanh", A)
+    assert tree.dtype == E.F64  # jasmine promotion through the double scalar
+    got = E.evaluate(jas, tree, out_dtype=E.F32)
+    close(got, want)
+    # the +,-,* part follows jasmine's typed evaluation bit for bit; tanh's last ulp is the
+    # platform libm's (glibc tanhf is not correctly rounded), so it is held to tolerance only
+    part = E.evaluate(jas, A * B + 0.5 * C, out_dtype=E.F32)
+    want_part = ((a * b).astype(np.float64) + 0.5 * c.astype(np.float64)).astype(np.float32)
+    assert bitfrac(part, want_part) == 1.0
+
+
+def test_ew_jasmine_view_and_modulo_semantics(jas):
+    # jasmine views add offsets then the underlying mat_t wraps indices modulo its dims
+    # (mat_view_t.hpp:28-38, mat_t.hpp:312-320), including the swapped offsets of a
+    # transposed view with offsets.
+    base = normal((5, 7), 2, 0)
+    small = normal((2, 7), 2, 1)
+    db, ds = __import__("jasmine_amd").to_device(base), __import__("jasmine_amd").to_device(small)
+
+    def jas_get(m, r, c, roff, coff, t):
+        a, bb = (c + coff, r + roff) if t else (r + roff, c + coff)
+        return m[a % m.shape[0], bb % m.shape[1]]
+
+    for (roff, coff, t, vr, vc) in [(1, 2, 0, 3, 4), (0, 0, 1, 7, 5), (1, 1, 1, 4, 3), (2, 3, 0, 6, 6)]:
+        tree = E.leaf(db, roff=roff, coff=coff, transposed=t, vrows=vr, vcols=vc) + E.leaf(ds)
+        out_r, out_c = max(vr, 2), max(vc, 7)
+        want = np.array([[jas_get(base, i, j, roff, coff, t) + small[i % 2, j % 7] for j in range(out_c)]
+                         for i in range(out_r)], np.float32)
+        got = E.evaluate(jas, tree)
+        assert got.shape == want.shape
+        assert bitfrac(got, want) == 1.0, (roff, coff, t)
+
+
+def test_ew_unary_and_pow(jas):
+    x = normal((37, 41), 3, 0)
+    dx = jas.to_device(x)
+    X = E.leaf(dx)
+    for op, fn in (("tanh", np.tanh), ("gelu", lambda v: 0.5 * v * (1 + np.tanh(0.7978845608028654 * (v + 0.044715 * v ** 3)))),
+                   ("silu", lambda v: v / (1 + np.exp(-v))), ("neg", lambda v: -v)):
+        close(E.evaluate(jas, E.un(op, X)), fn(x.astype(np.float64)).astype(np.float32), atol=2e-6, rtol=2e-6)
+    sq = E.evaluate(jas, E.un("sqrt", E.un("pow", X, imm=2.0)))
+    close(sq, np.abs(x), atol=1e-6, rtol=1e-6)
+
+
+def test_ew_rejects_bad_programs(jas):
+    import ctypes as C
+    from jasmine_amd.capi import Ins, Leaf, DeviceArray, lib
+    out = DeviceArray((4, 4))
+    prog = (Ins * 2)(Ins(1, 0, 0, 0, 1.0), Ins(2, 0, 0, 0, 0.0))  # const then ADD: stack underflow
+    assert lib.jas_ew_eval(prog, 2, (Leaf * 1)(), 0, out.p, 0, 4, 4, None) == 1
+    assert b"underflow" in lib.jas_last_error()
+
+
+# ---------------------------------------------------------------- reductions
+def test_reductions_bitexact(jas):
+    g = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "jasmine_golden.npz"))
+    x = g["x"]
+    R, Cc = x.shape
+    dx = jas.to_device(x)
+    lf = jas.leaf(dx)
+    import ctypes as C
+    for op, axis, name, n in ((0, 0, "hsum", R), (0, 1, "vsum", Cc), (1, 0, "hmax", R), (2, 1, "vmean", Cc),
+                              (2, 0, "hmean", R)):
+        out = jas.DeviceArray(n)
+        jas.check(jas.lib.jas_reduce(C.byref(lf), op, axis, out.p, 0, None))
+        assert bitfrac(out.numpy(), g[name]) == 1.0, name  # same sequential order as jasmine
+    for op, k in ((0, 0), (1, 1), (2, 2)):
+        out = jas.DeviceArray(1)
+        jas.check(jas.lib.jas_reduce(C.byref(lf), op, 2, out.p, 0, None))
+        close(out.numpy()[0], g["sum_max_mean"][k], atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("n_vec,length", [(3, 7), (5, 64), (4, 300), (2, 1000), (3, 2048), (2, 4099), (2, 8192),
+                                          (1, 16384), (2, 20000)])
+def test_row_ops(jas, n_vec, length):
+    x = normal((n_vec, length), 4, length, std=2.0)
+    dx, dy = jas.to_device(x), jas.DeviceArray((n_vec, length))
+    want = np.zeros_like(x)
+    jas.check(jas.lib.jas_softmax(dx.p, dy.p, n_vec, length, length, length, 1, None))
+    orc.orc_hsoftmax(fp(x), n_vec, length, fp(want))
+    close(dy.numpy(), want, atol=1e-6, rtol=1e-4)
+    gam = normal(length, 4, 1, mean=1.0, std=0.1)
+    bet = normal(length, 4, 2, std=0.1)
+    dg, dbt = jas.to_device(gam), jas.to_device(bet)
+    jas.check(jas.lib.jas_layernorm(dx.p, dy.p, n_vec, length, length, length, 1, 1e-5, dg.p, dbt.p, None))
+    orc.orc_layernorm_rows(fp(x), n_vec, length, 1e-5, fp(gam), fp(bet), fp(want))
+    close(dy.numpy(), want)
+    jas.check(jas.lib.jas_rmsnorm(dx.p, dy.p, n_vec, length, length, length, 1, 1e-6, dg.p, None))
+    orc.orc_rmsnorm_rows(fp(x), n_vec, length, 1e-6, fp(gam), fp(want))
+    close(dy.numpy(), want)
+
+
+def test_column_layernorm_jasmine(jas):
+    # jasmine's layer_norm_net_t normalises each column of a feature-major [d, T] matrix, eps 0
+    g = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "jasmine_golden.npz"))
+    x = g["x"]
+    R, Cc = x.shape
+    dx, dy = jas.to_device(x), jas.DeviceArray((R, Cc))
+    jas.check(jas.lib.jas_layernorm(dx.p, dy.p, Cc, R, 1, 1, Cc, 0.0, None, None, None))
+    close(dy.numpy(), g["layernorm_cols"], atol=1e-5, rtol=1e-5)
+    jas.check(jas.lib.jas_softmax(dx.p, dy.p, R, Cc, Cc, Cc, 1, None))
+    close(dy.numpy(), g["hsoftmax"], atol=1e-6, rtol=1e-5)
+
+
+def test_softmax_global(jas):
+    x = normal((300, 517), 5, 0)
+    dx, dy = jas.to_device(x), jas.DeviceArray(x.shape)
+    jas.check(jas.lib.jas_softmax_global(dx.p, dy.p, x.size, None))
+    want = np.zeros_like(x)
+    orc.orc_softmax_global(fp(x), 300, 517, fp(want))
+    close(dy.numpy(), want, atol=1e-9, rtol=1e-4)
+
+
+# ---------------------------------------------------------------- GEMM
+def _gemm_case(jas, M, N, K, ta=False, tb=False, col_c=False, bias_mode=0, act=0, acc=False, batch=1, seed=0):
+    A = normal((batch, K, M) if ta else (batch, M, K), 10 + seed, 0)
+    B = normal((batch, N, K) if tb else (batch, K, N), 10 + seed, 1)
+    C0 = normal((batch, N, M) if col_c else (batch, M, N), 10 + seed, 2)
+    bias = normal((batch, M if bias_mode == 1 else N), 10 + seed, 3)
+    An = np.swapaxes(A, 1, 2) if ta else A
+    Bn = np.swapaxes(B, 1, 2) if tb else B
+    ref = np.einsum("bmk,bkn->bmn", An.astype(np.float64), Bn.astype(np.float64))
+    if bias_mode == 1:
+        ref += bias[:, :, None]
+    elif bias_mode == 2:
+        ref += bias[:, None, :]
+    if act == 1:
+        ref = np.where(ref > 0, ref, 0.0)
+    elif act == 2:
+        ref = 0.5 * ref * (1 + np.tanh(0.7978845608028654 * (ref + 0.044715 * ref ** 3)))
+    if acc:
+        ref += np.swapaxes(C0, 1, 2) if col_c else C0
+    dA, dB, dC, dbias = jas.to_device(A), jas.to_device(B), jas.to_device(C0), jas.to_device(bias)
+    as0, as1 = (1, M) if ta else (K, 1)
+    bs0, bs1 = (1, K) if tb else (N, 1)
+    cs0, cs1 = (1, M) if col_c else (N, 1)
+    jas.check(jas.lib.jas_gemm(M, N, K, dA.p, as0, as1, dB.p, bs0, bs1, dC.p, cs0, cs1, dbias.p, bias_mode, act,
+                               int(acc), batch, M * K, K * N, M * N, bias.shape[1], None))
+    got = dC.numpy()
+    if col_c:
+        got = np.swapaxes(got, 1, 2)
+    # fp32 accumulation of K products: scale the tolerance with sqrt(K) * |a||b|
+    scale = np.sqrt(K) * 1.0
+    close(got, ref.astype(np.float32), atol=1e-5 * scale + 1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (7, 5, 13), (128, 128, 16), (130, 257, 65), (512, 384, 1024),
+                                   (256, 200, 4096)])
+def test_gemm_shapes(jas, M, N, K):
+    _gemm_case(jas, M, N, K)
+
+
+@pytest.mark.parametrize("ta,tb,col_c", [(1, 0, 0), (0, 1, 0), (1, 1, 1), (0, 0, 1)])
+def test_gemm_layouts(jas, ta, tb, col_c):
+    _gemm_case(jas, 136, 72, 40, ta=bool(ta), tb=bool(tb), col_c=bool(col_c))
+    _gemm_case(jas, 33, 17, 7, ta=bool(ta), tb=bool(tb), col_c=bool(col_c))
+
+
+@pytest.mark.parametrize("bias_mode,act,acc,batch", [(1, 0, 0, 1), (2, 1, 0, 2), (1, 2, 1, 3), (0, 0, 1, 1)])
+def test_gemm_epilogues(jas, bias_mode, act, acc, batch):
+    _gemm_case(jas, 150, 90, 70, bias_mode=bias_mode, act=act, acc=bool(acc), batch=batch)
+
+
+@pytest.mark.parametrize("N", [1, 2, 5, 8, 16])
+@pytest.mark.parametrize("M,K", [(300, 64), (64, 100), (1000, 4096), (4096, 1024)])
+def test_gemm_skinny(jas, M, N, K):
+    # decode shape: W [M][K], tokens X [N][K] -> out [N][M] (token-major), via jas_gemm's skinny path
+    W, X, b = normal((M, K), 20, 0), normal((N, K), 20, 1), normal(M, 20, 2)
+    dW, dX, db, dO = jas.to_device(W), jas.to_device(X), jas.to_device(b), jas.DeviceArray((N, M))
+    jas.check(jas.lib.jas_gemm(M, N, K, dW.p, K, 1, dX.p, 1, K, dO.p, 1, M, db.p, 1, 0, 0, 1, 0, 0, 0, 0, None))
+    ref = X.astype(np.float64) @ W.astype(np.float64).T + b
+    close(dO.numpy(), ref.astype(np.float32), atol=1e-5 * np.sqrt(K) + 1e-5, rtol=1e-5)
+
+
+# ---------------------------------------------------------------- attention
+@pytest.mark.parametrize("B,H,Sq,Sk,D,causal", [(2, 3, 100, 100, 64, 1), (1, 2, 64, 64, 32, 0), (2, 2, 70, 130, 128, 1),
+                                                (1, 4, 200, 200, 128, 1), (1, 1, 1, 1, 64, 1), (2, 2, 37, 90, 64, 0)])
+def test_attn_prefill(jas, B, H, Sq, Sk, D, causal):
+    Q, K, V = normal((B, H, Sq, D), 30, 0), normal((B, H, Sk, D), 30, 1), normal((B, H, Sk, D), 30, 2)
+    want = np.zeros((B, H, Sq, D), np.float32)
+    sc = 1 / math.sqrt(D)
+    orc.orc_attention(fp(Q), fp(K), fp(V), fp(want), B, H, Sq, Sk, D, sc, causal)
+    dq, dk, dv, do = jas.to_device(Q), jas.to_device(K), jas.to_device(V), jas.DeviceArray(Q.shape)
+    jas.check(jas.lib.jas_attn_prefill(dq.p, dk.p, dv.p, do.p, B, H, Sq, Sk, D, H * Sq * D, Sq * D, D, H * Sk * D,
+                                       Sk * D, D, H * Sq * D, Sq * D, D, sc, causal, 0, None))
+    close(do.numpy(), want, atol=1e-5, rtol=1e-4)
+
+
+def test_attn_prefill_bf16(jas):
+    B, H, S, D = 2, 2, 96, 64
+    Q, K, V = normal((B, H, S, D), 31, 0), normal((B, H, S, D), 31, 1), normal((B, H, S, D), 31, 2)
+
+    def bf(x):  # round to nearest even bf16, as uint16
+        u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    want = np.zeros((B, H, S, D), np.float32)
+    orc.orc_attention(fp(Q), fp(K), fp(V), fp(want), B, H, S, S, D, 0.125, 1)
+    dq, dk, dv = jas.to_device(bf(Q)), jas.to_device(bf(K)), jas.to_device(bf(V))
+    do = jas.DeviceArray((B, H, S, D), np.uint16)
+    jas.check(jas.lib.jas_attn_prefill(dq.p, dk.p, dv.p, do.p, B, H, S, S, D, H * S * D, S * D, D, H * S * D, S * D, D,
+                                       H * S * D, S * D, D, 0.125, 1, 3, None))
+    got = (do.numpy().astype(np.uint32) << 16).view(np.float32)
+    close(got, want, atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("B,H,D,lens", [(2, 3, 64, (1, 37)), (3, 2, 128, (1000, 513, 64)), (1, 4, 32, (2049,)),
+                                        (8, 12, 64, (1024,) * 8)])
+def test_attn_decode(jas, B, H, D, lens):
+    ctx = max(lens) + 5
+    K, V = normal((B, H, ctx, D), 32, 0), normal((B, H, ctx, D), 32, 1)
+    q = normal((B, H, 1, D), 32, 2)
+    sc = 1 / math.sqrt(D)
+    want = np.zeros((B, H, 1, D), np.float32)
+    for b in range(B):
+        L = lens[b]
+        Kb, Vb = np.ascontiguousarray(K[b:b + 1, :, :L]), np.ascontiguousarray(V[b:b + 1, :, :L])
+        o = np.zeros((1, H, 1, D), np.float32)
+        orc.orc_attention(fp(np.ascontiguousarray(q[b:b + 1])), fp(Kb), fp(Vb), fp(o), 1, H, 1, L, D, sc, 1)
+        want[b] = o[0]
+    dq, dk, dv, do = jas.to_device(q), jas.to_device(K), jas.to_device(V), jas.DeviceArray((B, H, D))
+    dl = jas.to_device(np.array(lens, np.int32))
+    ws_bytes = jas.lib.jas_attn_decode_workspace(B, H, D, max(lens))
+    ws = jas.DeviceArray(max(ws_bytes // 4, 1))
+    jas.check(jas.lib.jas_attn_decode(dq.p, dk.p, dv.p, do.p, dl.p, B, H, D, max(lens), H * ctx * D, ctx * D, sc,
+                                      ws.p, None))
+    close(do.numpy(), want[:, :, 0], atol=1e-5, rtol=1e-4)
+
+
+# ---------------------------------------------------------------- RoPE / embed / argmax / rng
+def test_rope_jasmine(jas):
+    for d, T in ((16, 6), (64, 33), (7, 5)):
+        X = normal((d, T), 40, d)
+        want = np.zeros_like(X)
+        orc.orc_rope_jas(fp(X), d, T, fp(want))
+        dx, dy = jas.to_device(X), jas.DeviceArray((d, T))
+        jas.check(jas.lib.jas_rope_jasmine(dx.p, dy.p, d, T, None))
+        close(dy.numpy(), want, atol=1e-6, rtol=1e-5)
+    g = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "jasmine_golden.npz"))
+    dx, dy = jas.to_device(g["rope_x"]), jas.DeviceArray(g["rope_x"].shape)
+    jas.check(jas.lib.jas_rope_jasmine(dx.p, dy.p, 16, 6, None))
+    close(dy.numpy(), g["rope_y"], atol=1e-6, rtol=1e-5)
+
+
+def test_rope_llama(jas):
+    n, nh, dh = 5, 3, 128
+    X = normal((n, nh * dh), 41, 0)
+    pos = np.array([0, 1, 7, 1000, 2175], np.int32)
+    want = X.copy()
+    for t in range(n):
+        for h in range(nh):
+            seg = np.ascontiguousarray(want[t, h * dh:(h + 1) * dh])
+            orc.orc_rope_llama(fp(seg), dh, int(pos[t]), 10000.0)
+            want[t, h * dh:(h + 1) * dh] = seg
+    dx, dp = jas.to_device(X), jas.to_device(pos)
+    jas.check(jas.lib.jas_rope_llama(dx.p, dp.p, n, nh, dh, nh * dh, 10000.0, None))
+    close(dx.numpy(), want, atol=1e-6, rtol=1e-6)
+
+
+def test_embed_argmax_fill(jas):
+    V, d, n = 50, 16, 7
+    wte, wpe = normal((V, d), 42, 0), normal((20, d), 42, 1)
+    ids, pos = np.array([3, 0, 49, 7, 7, 12, 1], np.int32), np.arange(7, dtype=np.int32)
+    dw, dp, di, dpo, do = jas.to_device(wte), jas.to_device(wpe), jas.to_device(ids), jas.to_device(pos), jas.DeviceArray((n, d))
+    jas.check(jas.lib.jas_embed(dw.p, dp.p, di.p, dpo.p, do.p, n, d, None))
+    assert bitfrac(do.numpy(), wte[ids] + wpe[pos]) == 1.0
+    x = normal((4, 50257), 42, 2)
+    x[1, 100] = x[1, 30000] = 50.0  # tie -> first index
+    dx, da = jas.to_device(x), jas.DeviceArray(4, np.int32)
+    jas.check(jas.lib.jas_argmax(dx.p, 4, 50257, 50257, da.p, None))
+    assert list(da.numpy()) == [int(np.argmax(r)) for r in x]
+    dn = jas.DeviceArray(100003)
+    jas.check(jas.lib.jas_fill_normal(dn.p, 100003, 9, 3, 0.0, 0.02, None))
+    close(dn.numpy(), normal(100003, 9, 3, std=0.02), atol=1e-7, rtol=1e-6)
