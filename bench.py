@@ -1,0 +1,211 @@
+"""Decode throughput of the LLaMA-7B-shaped fp32 decoder on one MI355X (config 5).
+
+    python bench.py [--steps K] [--warmup W] [--batch 16] [--prompt 2048] [--no-gpt2] [--no-cpu]
+
+Workload (the north-star target): 32 layers, d_model 4096, 32
+heads (head dim 128), SwiGLU FFN 11008, RMSNorm eps 1e-6, RoPE theta 1e4, vocab 32000,
+weights N(0, 0.02) from seed 4 (generated on the device), batch 16, prompts of 2048 token
+ids uniform over the vocab (seed 4).  The prompt is prefilled (untimed, reported), W
+greedy decode steps warm up, then K steps are timed; W + K <= 128 (the config's decode
+length).  One step = one token for each of the 16 sequences through the whole model
+(embedding, 32 layers, final norm, LM head, argmax) with the KV cache appended in place.
+
+The roofline object is for the dominant kernel class, timed with HIP events around every
+launch on the runner's stream inside the timed region.  cpu_baseline times the jasmine
+reference itself (oracle/_ref, its weight_net_t::forward at the real 4096x4096 projection
+shape, 16 columns) on one host core and extrapolates by FLOPs to a whole decode step.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, datasheet
+FP32_MFMA_TFLOPS = 157.3   # MI355X dense fp32 matrix, datasheet
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def llama_cfg(jas, B, ctx):
+    return jas.LmConfig(1, 32, 4096, 32, 11008, 32000, ctx, B, 1e-6, 10000.0)
+
+
+def weight_bytes_per_step(L, d, F, V):
+    # every weight matrix is streamed once per decode step (embedding rows are gathered)
+    return 4 * (L * (3 * d * d + d * d + 3 * d * F) + V * d)
+
+
+def cpu_baseline(step_flops, B):
+    """Time the reference CPU path (jasmine compiled from its sources) on a bounded sample."""
+    try:
+        from oracle_lib import ref, orc
+    except Exception as e:  # pragma: no cover
+        log("cpu baseline unavailable:", e)
+        return None
+    out, inn, T = 4096, 4096, B
+    flops_one = 2.0 * out * inn * T
+    if ref is not None:
+        kind, fn = "reference", lambda: ref.ref_time_linear(out, inn, T, 1)
+        what = "jasmine weight_net_t::forward (oracle/_ref, -O2, 1 thread)"
+    else:
+        import ctypes
+        import numpy as np
+        W = np.full((out, inn), 0.01, np.float32)
+        X = np.full((inn, T), 0.02, np.float32)
+        Y = np.zeros((out, T), np.float32)
+        from oracle_lib import fp
+
+        def fn():
+            t0 = time.perf_counter()
+            orc.orc_linear(fp(W), None, fp(X), out, inn, T, fp(Y))
+            return time.perf_counter() - t0
+        kind, what = "port", "oracle orc_linear (C restatement, 1 thread)"
+    t_total, reps = 0.0, 0
+    while t_total < 8.0 and reps < 8:
+        t_total += fn()
+        reps += 1
+    per = t_total / reps
+    rate = flops_one / per
+    step_s = step_flops / rate
+    return {"value": B / step_s, "unit": "tok/s", "cores": 1, "kind": kind,
+            "sample": f"{what} at W[4096x4096] x X[4096x{T}] ({reps} reps, {t_total:.1f} s, "
+                      f"{rate / 1e9:.3f} GFLOP/s), extrapolated by FLOPs to one decode step "
+                      f"({step_flops / 1e9:.1f} GFLOP: all projections + attention + LM head)"}
+
+
+def run_gpt2(jas, steps=32, warmup=4):
+    """Config 4 shape: GPT-2-small, batch 8, 512-token prompts; returns decode tok/s."""
+    from oracle_lib import randint
+    B, P = 8, 512
+    cfg = jas.LmConfig(0, 12, 768, 12, 3072, 50257, 1024, B, 1e-5, 10000.0)
+    lm = jas.Lm(cfg)
+    lm.init_random(3, 0.02)
+    lm.prefill(randint((B, P), 50257, 3))
+    lm.generate(warmup, B)
+    t0 = time.perf_counter()
+    lm.generate(steps, B)
+    dt = time.perf_counter() - t0
+    lm.close()
+    return B * steps / dt, 1e3 * dt / steps
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=120)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=2048)
+    ap.add_argument("--no-gpt2", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.warmup + args.steps > 128:
+        args.steps = max(1, 128 - args.warmup)
+
+    import numpy as np
+    import jasmine_amd as jas
+    from oracle_lib import randint
+
+    os.environ.setdefault("JAS_VERBOSE", "1")
+    jas.check(jas.lib.jas_init(0))
+    B, P = args.batch, args.prompt
+    L, d, H, F, V = 32, 4096, 32, 11008, 32000
+    dh = d // H
+    ctx = P + 128
+    cfg = llama_cfg(jas, B, ctx)
+    log(f"[bench] creating LLaMA-7B-shape fp32 model, batch {B}, ctx {ctx}")
+    lm = jas.Lm(cfg)
+    t0 = time.perf_counter()
+    lm.init_random(4, 0.02)
+    log(f"[bench] weights initialised in {time.perf_counter() - t0:.1f} s")
+    prompt = randint((B, P), V, 4)
+    t0 = time.perf_counter()
+    lm.prefill(prompt)
+    prefill_s = time.perf_counter() - t0
+    log(f"[bench] prefill {B}x{P} tokens: {prefill_s:.2f} s ({B * P / prefill_s:.0f} tok/s)")
+
+    lm.generate(args.warmup, B)
+    pos0 = lm.position
+    lm.profile(True)
+    jas.check(jas.lib.jas_synchronize(lm.stream))
+    t0 = time.perf_counter()
+    lm.generate(args.steps, B)  # synchronises at the end
+    dt = time.perf_counter() - t0
+    ms, cnt = lm.profile(False)
+    tok_s = B * args.steps / dt
+    log(f"[bench] decode: {args.steps} steps in {dt:.3f} s -> {tok_s:.1f} tok/s")
+
+    # algorithmic bytes over the timed region
+    w_bytes = weight_bytes_per_step(L, d, F, V) * args.steps
+    kv_bytes = sum(B * L * H * (pos0 + s + 1) * dh * 4 * 2 for s in range(args.steps))
+    gemm_gbs = w_bytes / (ms[0] * 1e-3) / 1e9
+    attn_gbs = kv_bytes / (ms[1] * 1e-3) / 1e9
+    step_bytes = (w_bytes + kv_bytes) / args.steps
+    classes = [
+        {"kernel": "skinny_kernel (decode weight GEMMs: QKV+RoPE+KV append, O+residual, SwiGLU, down+residual, LM head)",
+         "achieved": gemm_gbs, "launches": cnt[0], "gpu_ms": ms[0], "bytes": w_bytes},
+        {"kernel": "attn_decode_kernel (split-K KV-cache attention + merge)",
+         "achieved": attn_gbs, "launches": cnt[1], "gpu_ms": ms[1], "bytes": kv_bytes},
+    ]
+    dom = max(classes, key=lambda c: c["gpu_ms"])
+    other = min(classes, key=lambda c: c["gpu_ms"])
+    roof = {"bound": "hbm", "achieved": round(dom["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom["kernel"],
+            "bytes_per_launch": dom["bytes"] / max(dom["launches"], 1),
+            "avg_launch_us": 1e3 * dom["gpu_ms"] / max(dom["launches"], 1)}
+    step_roofline_frac = (step_bytes / (dt / args.steps)) / 1e9 / HBM_PEAK_GBS
+
+    step_flops = 2.0 * B * (L * (3 * d * d + d * d + 3 * d * F) + V * d) + 4.0 * B * L * H * (P + 64) * dh
+    cpu = None if args.no_cpu else cpu_baseline(step_flops, B)
+
+    gpt2 = None
+    if not args.no_gpt2:
+        lm.close()
+        try:
+            g_tok, g_ms = run_gpt2(jas)
+            gpt2 = {"decode_tok_s": round(g_tok, 1), "ms_per_step": round(g_ms, 3),
+                    "workload": "config4: GPT-2-small fp32, batch 8, 512-token prompts, greedy decode"}
+        except Exception as e:  # the headline number stands on its own
+            log("[bench] gpt2 leg failed:", e)
+
+    line = {
+        "metric": "decode tok/s (GPT-2-small, LLaMA-7B shape); kernel % of HBM/MFMA peak",
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * dt / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (random-init N(0,0.02) weights, uniform random prompt ids)",
+        "config": {"workload": f"config5: LLaMA-7B-shape decoder fp32, batch {B}, {P}-token prompts, "
+                               f"greedy KV-cache decode (positions {pos0}..{pos0 + args.steps - 1})",
+                   "batch": B, "prompt": P, "parallelism": "single GPU"},
+        "roofline": roof,
+        "roofline_other": {"kernel": other["kernel"], "achieved": round(other["achieved"], 1), "unit": "GB/s",
+                           "frac": round(other["achieved"] / HBM_PEAK_GBS, 4)},
+        "step_hbm_frac": round(step_roofline_frac, 4),
+        "step_bytes": step_bytes,
+        "prefill_tok_s": round(B * P / prefill_s, 1),
+        "cpu_baseline": cpu,
+        "gpt2_small": gpt2,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

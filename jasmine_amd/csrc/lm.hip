@@ -16,6 +16,7 @@
 // (seq, head) key range is one contiguous stream.
 #include "gemm.hpp"
 
+#include <cstdlib>
 #include <map>
 #include <string>
 #include <vector>
@@ -431,7 +432,13 @@ jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_
     TRY(jas_memcpy_h2d(lm->pIds, h_ids, T * sizeof(int32_t), s));
     hipLaunchKernelGGL(prefill_positions_kernel, dim3(ceil_div(T, 256)), dim3(256), 0, s, lm->pPos, B, P);
     TRY(jas_embed(lm->W("wte"), c.kind == 0 ? lm->W("wpe") : nullptr, lm->pIds, lm->pPos, lm->pX, (int)T, d, s));
+    const bool verbose = getenv("JAS_VERBOSE") != nullptr;
     for (int l = 0; l < c.n_layer; ++l) {
+        if (verbose && l % 4 == 0) {  // progress for long prefills (synchronises, diagnostics only)
+            JAS_HIP(hipStreamSynchronize(s));
+            fprintf(stderr, "[jas] prefill layer %d/%d\n", l, c.n_layer);
+            fflush(stderr);
+        }
         TRY(norm_rows(lm, lm->pX, lm->pH, (int)T, d, l, 1));
         const float *bq = lm->W("b_qkv") ? lm->W("b_qkv") + (long)l * 3 * d : nullptr;
         // QKV[n][m] = sum_k w_qkv[m][k] H[n][k] (+ b[m])
