@@ -222,11 +222,16 @@ jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out);
 jas_status jas_lm_destroy(jas_lm *lm);
 /* Fill every weight N(0, std) from `seed` (norm gains 1, biases 0). */
 jas_status jas_lm_init_random(jas_lm *lm, uint64_t seed, float std);
-/* Weight tensor access by name ("wte", "wpe", "ln1_g", "ln1_b", "w_qkv", "b_qkv", "w_o",
- * "b_o", "ln2_g", "ln2_b", "w_fc", "b_fc", "w_proj", "b_proj", "w_gate", "w_up", "w_down",
- * "lnf_g", "lnf_b", "w_head"); layer tensors are stacked [n_layer][...], matrices [out][in].
- * Returns the device pointer and element count (NULL/0 for tensors the kind lacks). */
-jas_status jas_lm_weight(jas_lm *lm, const char *name, float **d_ptr, size_t *count);
+/* Weight tensors by name ("wte", "wpe", "ln1_g", "ln1_b", "w_qkv", "b_qkv", "w_o", "b_o",
+ * "ln2_g", "ln2_b", "w_fc", "b_fc", "w_proj", "b_proj", "w_gate", "w_up", "w_down", "lnf_g",
+ * "lnf_b", "w_head"); a tensor is `layers` stacked [rows][cols] matrices ([out][in] for
+ * projections).  Host copies use that logical row-major order whatever the device layout
+ * (projection matrices are stored in the MFMA-native packed layout).  weight_shape reports
+ * 0/0/0 for a tensor the model kind lacks.  Stands in for jasmine's init_weight<I>()
+ * traversal hook (mat_init_t.hpp:113-118) as the way to load trained weights. */
+jas_status jas_lm_weight_shape(jas_lm *lm, const char *name, int *layers, int *rows, int *cols);
+jas_status jas_lm_get_weight(jas_lm *lm, const char *name, float *h_dst, size_t count);
+jas_status jas_lm_set_weight(jas_lm *lm, const char *name, const float *h_src, size_t count);
 /* Prefill B prompts of length P (host int32 ids [B][P]) and return the greedy next ids
  * (host [B]); logits of the last position go to h_logits [B][V] if not NULL. */
 jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_t *h_next, float *h_logits);

@@ -68,7 +68,9 @@ _sigs = {
     "jas_lm_create": [C.POINTER(LmConfig), C.POINTER(VP)],
     "jas_lm_destroy": [VP],
     "jas_lm_init_random": [VP, C.c_uint64, C.c_float],
-    "jas_lm_weight": [VP, C.c_char_p, C.POINTER(VP), C.POINTER(C.c_size_t)],
+    "jas_lm_weight_shape": [VP, C.c_char_p, C.POINTER(I), C.POINTER(I), C.POINTER(I)],
+    "jas_lm_get_weight": [VP, C.c_char_p, FP, C.c_size_t],
+    "jas_lm_set_weight": [VP, C.c_char_p, FP, C.c_size_t],
     "jas_lm_prefill": [VP, I, I, IP, IP, FP],
     "jas_lm_decode": [VP, IP, IP, FP],
     "jas_lm_generate": [VP, I, IP],
@@ -171,25 +173,25 @@ class Lm:
     def init_random(self, seed, std=0.02):
         check(lib.jas_lm_init_random(self.h, seed, std))
 
-    def weight_ptr(self, name):
-        p, n = VP(), C.c_size_t()
-        check(lib.jas_lm_weight(self.h, name.encode(), C.byref(p), C.byref(n)))
-        return p.value, n.value
+    def weight_shape(self, name):
+        l, r, c = I(), I(), I()
+        check(lib.jas_lm_weight_shape(self.h, name.encode(), C.byref(l), C.byref(r), C.byref(c)))
+        return l.value, r.value, c.value
 
     def weight(self, name):
-        p, n = self.weight_ptr(name)
-        if not p:
+        """Host copy of a weight tensor, flat in logical [layers][rows][cols] order (None if absent)."""
+        l, r, c = self.weight_shape(name)
+        if l == 0:
             return None
-        out = np.empty(n, np.float32)
-        check(lib.jas_synchronize(None))
-        check(lib.jas_memcpy_d2h(out.ctypes.data_as(VP), VP(p), n * 4, self.stream))
+        out = np.empty(l * r * c, np.float32)
+        check(lib.jas_lm_get_weight(self.h, name.encode(), out.ctypes.data_as(FP), out.size))
         return out
 
     def set_weight(self, name, a):
-        p, n = self.weight_ptr(name)
+        l, r, c = self.weight_shape(name)
         a = np.ascontiguousarray(a, np.float32).ravel()
-        assert p and a.size == n, (name, a.size, n)
-        check(lib.jas_memcpy_h2d(VP(p), a.ctypes.data_as(VP), n * 4, self.stream))
+        assert l and a.size == l * r * c, (name, a.size, (l, r, c))
+        check(lib.jas_lm_set_weight(self.h, name.encode(), a.ctypes.data_as(FP), a.size))
 
     @property
     def stream(self):

@@ -205,7 +205,15 @@ struct DecodeArgs {
     long k_sb, k_sh;
     int B, H, nsplit, chunk;
     float scale_log2;
+    int o_packed_d;  // > 0: write O in the packed B-operand layout over o_packed_d features
 };
+
+__device__ __forceinline__ long decode_out_index(const DecodeArgs &p, int bh, int D, int e)
+{
+    if (p.o_packed_d <= 0) return (long)bh * D + e;
+    const int b = bh / p.H, k = (bh % p.H) * D + e;  // token b, feature k
+    return ((long)(k >> 4) * 64 + b + 16 * ((k & 15) >> 2)) * 4 + (k & 3);
+}
 
 // TPK lanes per key (D/4 floats each); each group of TPK lanes walks its own keys.
 template <int D>
@@ -278,7 +286,7 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(const DecodeArgs p)
             A += sacc[k][tid] * f;
         }
         if (p.nsplit == 1) {
-            p.O[(long)bh * D + tid] = L > 0.f ? A / L : 0.f;
+            p.O[decode_out_index(p, bh, D, tid)] = L > 0.f ? A / L : 0.f;
         } else {
             float *pp = p.part + ((long)bh * p.nsplit + split) * (D + 2);
             pp[2 + tid] = A;
@@ -301,7 +309,7 @@ __global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p
         L += pp[s * (D + 2) + 1] * f;
         A += pp[s * (D + 2) + 2 + tid] * f;
     }
-    p.O[(long)bh * D + tid] = L > 0.f ? A / L : 0.f;
+    p.O[decode_out_index(p, bh, D, tid)] = L > 0.f ? A / L : 0.f;
 }
 
 static int decode_nsplit(int B, int H, int D, int max_len, int *chunk)
@@ -317,6 +325,33 @@ static int decode_nsplit(int B, int H, int D, int max_len, int *chunk)
     *chunk = ch;
     return ns;
 }
+
+jas_status attn_decode_impl(const float *q, const float *K, const float *V, float *O, const int32_t *seqlens, int B,
+                            int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, hipStream_t s,
+                            int o_packed_d)
+{
+    JAS_CHECK(q && K && V && O && seqlens, JAS_ERR_INVALID, "jas_attn_decode: null tensor");
+    JAS_CHECK(B > 0 && H > 0 && max_len > 0, JAS_ERR_INVALID, "jas_attn_decode: empty shape");
+    JAS_CHECK(D == 32 || D == 64 || D == 128, JAS_ERR_INVALID, "jas_attn_decode: head dim must be 32, 64 or 128");
+    JAS_CHECK(k_sb % 4 == 0 && k_sh % 4 == 0, JAS_ERR_INVALID, "jas_attn_decode: strides must be multiples of 4");
+    int chunk;
+    int ns = decode_nsplit(B, H, D, max_len, &chunk);
+    JAS_CHECK(ns == 1 || work, JAS_ERR_INVALID, "jas_attn_decode: workspace required");
+    JAS_CHECK(o_packed_d <= 0 || (B <= 16 && o_packed_d == H * D), JAS_ERR_INVALID, "attn_decode: bad packed output");
+    DecodeArgs p{q, K, V, O, seqlens, (float *)work, k_sb, k_sh, B, H, ns, chunk, scale * 1.4426950408889634f,
+                 o_packed_d};
+    dim3 grid(ns, B * H);
+#define JAS_DEC(DD)                                                                                  \
+    if (D == DD) {                                                                                   \
+        hipLaunchKernelGGL((attn_decode_kernel<DD>), grid, dim3(256), 0, s, p);                      \
+        if (ns > 1) hipLaunchKernelGGL((attn_decode_merge_kernel<DD>), dim3(B * H), dim3(DD), 0, s, p); \
+    }
+    JAS_DEC(32) JAS_DEC(64) JAS_DEC(128)
+#undef JAS_DEC
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
 
 } // namespace jas
 
@@ -364,25 +399,7 @@ jas_status jas_attn_decode(const float *q, const float *K, const float *V, float
                            int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work,
                            jas_stream_t stream)
 {
-    JAS_CHECK(q && K && V && O && seqlens, JAS_ERR_INVALID, "jas_attn_decode: null tensor");
-    JAS_CHECK(B > 0 && H > 0 && max_len > 0, JAS_ERR_INVALID, "jas_attn_decode: empty shape");
-    JAS_CHECK(D == 32 || D == 64 || D == 128, JAS_ERR_INVALID, "jas_attn_decode: head dim must be 32, 64 or 128");
-    JAS_CHECK(k_sb % 4 == 0 && k_sh % 4 == 0, JAS_ERR_INVALID, "jas_attn_decode: strides must be multiples of 4");
-    int chunk;
-    int ns = decode_nsplit(B, H, D, max_len, &chunk);
-    JAS_CHECK(ns == 1 || work, JAS_ERR_INVALID, "jas_attn_decode: workspace required");
-    DecodeArgs p{q, K, V, O, seqlens, (float *)work, k_sb, k_sh, B, H, ns, chunk, scale * 1.4426950408889634f};
-    hipStream_t s = stream_or_default(stream);
-    dim3 grid(ns, B * H);
-#define JAS_DEC(DD)                                                                                  \
-    if (D == DD) {                                                                                   \
-        hipLaunchKernelGGL((attn_decode_kernel<DD>), grid, dim3(256), 0, s, p);                      \
-        if (ns > 1) hipLaunchKernelGGL((attn_decode_merge_kernel<DD>), dim3(B * H), dim3(DD), 0, s, p); \
-    }
-    JAS_DEC(32) JAS_DEC(64) JAS_DEC(128)
-#undef JAS_DEC
-    JAS_LAUNCH_CHECK();
-    return JAS_OK;
+    return attn_decode_impl(q, K, V, O, seqlens, B, H, D, max_len, k_sb, k_sh, scale, work, stream_or_default(stream), 0);
 }
 
 } // extern "C"

@@ -31,7 +31,8 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c)
 // ---------------------------------------------------------------- tiled GEMM
 constexpr int TBM = 128, TBN = 128, TBK = 16, TLD = 20;  // LDS row stride (floats)
 
-enum LoadMode : int { LM_KC = 0, LM_OC = 1, LM_GEN = 2 };  // K-contig, outer-contig, generic
+// K-contiguous, outer-contiguous, generic strides, packed weights (weight_pack_offset)
+enum LoadMode : int { LM_KC = 0, LM_OC = 1, LM_GEN = 2, LM_PK = 3 };
 
 // Loads a [128 outer x 16 k] tile of X(o, k) = X[o*so + k*sk] into registers, then LDS
 // rows [o][k] (K-contiguous, padded stride TLD).
@@ -48,6 +49,15 @@ struct TileLoader {
                 int go = o0 + o, gk = k0 + kq;
                 float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (go < O && gk < K) v = *(const float4 *)(X + (long)go * so + gk);
+                r[4 * q] = v.x; r[4 * q + 1] = v.y; r[4 * q + 2] = v.z; r[4 * q + 3] = v.w;
+            }
+        } else if (MODE == LM_PK) {  // 8 row tiles x one 16-wide K block: 8 contiguous 1 KB blocks
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                int idx = tid + q * 256, i = idx >> 6, ln = idx & 63;
+                long rt = o0 / 16 + i;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (rt * 16 < O) v = *(const float4 *)(X + ((rt * (K >> 4) + (k0 >> 4)) * 64 + ln) * 4);
                 r[4 * q] = v.x; r[4 * q + 1] = v.y; r[4 * q + 2] = v.z; r[4 * q + 3] = v.w;
             }
         } else if (MODE == LM_OC) {
@@ -75,6 +85,13 @@ struct TileLoader {
             for (int q = 0; q < 2; ++q) {
                 int idx = tid + q * 256, o = idx >> 2, kq = (idx & 3) * 4;
                 *(float4 *)(lds + o * TLD + kq) = make_float4(r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]);
+            }
+        } else if (MODE == LM_PK) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                int idx = tid + q * 256, i = idx >> 6, ln = idx & 63;
+                *(float4 *)(lds + (i * 16 + (ln & 15)) * TLD + 4 * (ln >> 4)) =
+                    make_float4(r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]);
             }
         } else if (MODE == LM_OC) {
 #pragma unroll
@@ -216,7 +233,7 @@ static int pick_mode(const float *X, long so, long sk, int O, int K, long bstrid
 
 jas_status gemm_general(int M, int N, int K, const float *A, long as0, long as1, const float *B, long bs0, long bs1,
                         float *C, long cs0, long cs1, const float *bias, int bias_mode, int act, int accumulate,
-                        int batch, long abs_, long bbs, long cbs, long biasbs, hipStream_t s)
+                        int batch, long abs_, long bbs, long cbs, long biasbs, hipStream_t s, bool a_packed)
 {
     TileArgs p;
     p.A = A; p.B = B; p.C = C; p.bias = bias_mode ? bias : nullptr;
@@ -224,11 +241,13 @@ jas_status gemm_general(int M, int N, int K, const float *A, long as0, long as1,
     p.abs_ = abs_; p.bbs = bbs; p.cbs = cbs; p.biasbs = biasbs;
     p.M = M; p.N = N; p.K = K;
     p.bias_mode = bias_mode; p.act = act; p.accumulate = accumulate;
-    int am = pick_mode(A, as0, as1, M, K, abs_);
+    JAS_CHECK(!a_packed || (K % 16 == 0 && batch == 1), JAS_ERR_INVALID, "gemm: packed A needs K % 16 == 0");
+    int am = a_packed ? LM_PK : pick_mode(A, as0, as1, M, K, abs_);
     int bm = pick_mode(B, bs1, bs0, N, K, bbs);
     bool c4 = cs0 == 1 && al16(C) && (cs1 % 4 == 0) && (cbs % 4 == 0);
     dim3 grid(ceil_div(N, TBN), ceil_div(M, TBM), batch);
-    if (am == LM_KC) launch_tile_b<LM_KC>(p, bm, c4, grid, s);
+    if (am == LM_PK) launch_tile_b<LM_PK>(p, bm, c4, grid, s);
+    else if (am == LM_KC) launch_tile_b<LM_KC>(p, bm, c4, grid, s);
     else if (am == LM_OC) launch_tile_b<LM_OC>(p, bm, c4, grid, s);
     else launch_tile_b<LM_GEN>(p, bm, c4, grid, s);
     JAS_LAUNCH_CHECK();
@@ -236,70 +255,96 @@ jas_status gemm_general(int M, int N, int K, const float *A, long as0, long as1,
 }
 
 // ---------------------------------------------------------------- skinny (decode) GEMM
-// NT row tiles of 16 per workgroup (DUAL: tile 0 from W, tile 1 from W2 at the same rows),
-// WPB waves split the K chunks of 64 and reduce through LDS.
-template <int NT, int WPB, bool DUAL>
+// One workgroup per row group of 16 rows (NT tiles of 16 rows for NT > 1; DUAL: tile 0 from
+// W, tile 1 from W2 at the same 16 rows).  Its WPB waves interleave over the K chunks of 64
+// and are reduced through LDS, then the fused epilogue runs.  No cross-workgroup reduction:
+// on MI355X each XCD has its own L2, so a device-scope release/acquire inside the kernel
+// would write back and invalidate L2 -- far costlier than the parallelism it buys.
+//
+// PACKED weights (weight_pack_offset): each wave-wide load is one contiguous 1 KB block
+// holding exactly the A-operand float4s of 64 lanes, so a workgroup streams its rows as
+// long contiguous runs instead of 16 rows x 64 B scattered 4*K bytes apart.
+template <int NT, int WPB, int DEPTH, bool DUAL, bool PACKED>
 __global__ void __launch_bounds__(WPB * 64)
 skinny_kernel(const float *__restrict__ W, const float *__restrict__ W2, const float *__restrict__ X, long ldx, int M,
               int N, int K, const SkinnyEpiArgs epi)
 {
+    constexpr int ITEMS = NT * 64;
     __shared__ floatx4 red[WPB][NT][64];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r16 = lane & 15, g = lane >> 4;
-    const int rows_per_block = DUAL ? 16 : NT * 16;
-    const int m0 = blockIdx.x * rows_per_block;
+    const int m0 = blockIdx.x * (DUAL ? 16 : NT * 16);
+    const int K16 = K >> 4;
 
     const float *wp[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        int row = m0 + (DUAL ? 0 : t * 16) + r16;
-        row = row < M ? row : M - 1;  // clamped rows are computed and discarded
-        wp[t] = (DUAL && t == 1 ? W2 : W) + (long)row * K + 4 * g;
+        const float *base = (DUAL && t == 1) ? W2 : W;
+        if (PACKED) {
+            const long rt = m0 / 16 + (DUAL ? 0 : t);
+            wp[t] = base + (rt * K16 * 64 + lane) * 4;
+        } else {
+            int row = m0 + (DUAL ? 0 : t * 16) + r16;
+            row = row < M ? row : M - 1;  // clamped rows are computed and discarded
+            wp[t] = base + (long)row * K + 4 * g;
+        }
     }
     const bool xvalid = r16 < N;
-    const float *xp = X + (long)(xvalid ? r16 : 0) * ldx + 4 * g;
+    const float *xp = PACKED ? X + (long)lane * 4 : X + (long)(xvalid ? r16 : 0) * ldx + 4 * g;
 
     floatx4 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    const int nchunk = (K + 63) / 64;
+    const int nchunk_all = (K + 63) / 64;
+    // K split (PARTIAL mode): this workgroup streams chunks [c_begin, nchunk)
+    const int c_begin = blockIdx.y * epi.cpb;
+    const int nchunk = min(nchunk_all, c_begin + epi.cpb);
     const bool ktail = (K & 63) != 0;
-    floatx4 wc[NT][4], wn[NT][4];
-    float4 xc[4], xn[4];
+    // DEPTH-deep ring of chunk buffers: chunk c+j*WPB is loading while chunk c computes
+    floatx4 wb[DEPTH][NT][4];
+    float4 xb[DEPTH][4];
     auto load = [&](int c, floatx4 (&wv)[NT][4], float4 (&xv)[4]) {
         const int k = c * 64;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const bool kin = !ktail || (k + 16 * q + 4 * g) < K;
-            xv[q] = (xvalid && kin) ? *(const float4 *)(xp + k + 16 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const bool cin = !ktail || (4 * c + q) < K16;  // packed: whole 16-wide block valid
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
-                wv[t][q] = kin ? __builtin_nontemporal_load((const floatx4 *)(wp[t] + k + 16 * q))
-                               : floatx4{0.f, 0.f, 0.f, 0.f};
+            for (int t = 0; t < NT; ++t) {
+                if (PACKED)
+                    wv[t][q] = cin ? __builtin_nontemporal_load((const floatx4 *)(wp[t] + (long)(4 * c + q) * 256))
+                                   : floatx4{0.f, 0.f, 0.f, 0.f};
+                else
+                    wv[t][q] = kin ? __builtin_nontemporal_load((const floatx4 *)(wp[t] + k + 16 * q))
+                                   : floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+            if (PACKED)  // contiguous 1 KB per wave; token rows >= N only feed discarded columns
+                xv[q] = cin ? *(const float4 *)(xp + (long)(4 * c + q) * 256) : make_float4(0.f, 0.f, 0.f, 0.f);
+            else
+                xv[q] = (xvalid && kin) ? *(const float4 *)(xp + k + 16 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
-    int c = w;
-    if (c < nchunk) load(c, wc, xc);
-    for (; c < nchunk; c += WPB) {
-        const int cn = c + WPB;
-        if (cn < nchunk) load(cn, wn, xn);  // keep the next chunk's loads in flight
+    auto compute = [&](const floatx4 (&wv)[NT][4], const float4 (&xv)[4]) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                acc[t] = mfma4(wc[t][q][0], xc[q].x, acc[t]);
-                acc[t] = mfma4(wc[t][q][1], xc[q].y, acc[t]);
-                acc[t] = mfma4(wc[t][q][2], xc[q].z, acc[t]);
-                acc[t] = mfma4(wc[t][q][3], xc[q].w, acc[t]);
+                acc[t] = mfma4(wv[t][q][0], xv[q].x, acc[t]);
+                acc[t] = mfma4(wv[t][q][1], xv[q].y, acc[t]);
+                acc[t] = mfma4(wv[t][q][2], xv[q].z, acc[t]);
+                acc[t] = mfma4(wv[t][q][3], xv[q].w, acc[t]);
             }
-        if (cn < nchunk) {
+    };
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                xc[q] = xn[q];
+    for (int j = 0; j < DEPTH - 1; ++j)
+        if (c_begin + w + j * WPB < nchunk) load(c_begin + w + j * WPB, wb[j], xb[j]);
+    for (int c = c_begin + w; c < nchunk; c += DEPTH * WPB) {
 #pragma unroll
-                for (int t = 0; t < NT; ++t) wc[t][q] = wn[t][q];
-            }
+        for (int j = 0; j < DEPTH; ++j) {
+            const int cl = c + (j + DEPTH - 1) * WPB;
+            if (cl < nchunk) load(cl, wb[(j + DEPTH - 1) % DEPTH], xb[(j + DEPTH - 1) % DEPTH]);
+            if (c + j * WPB < nchunk) compute(wb[j], xb[j]);
         }
     }
 #pragma unroll
@@ -307,8 +352,7 @@ skinny_kernel(const float *__restrict__ W, const float *__restrict__ W2, const f
     __syncthreads();
 
     // epilogue: thread (t, ln) owns rows m..m+3 of tile t for token n = ln % 16
-    const int tid = threadIdx.x;
-    const int n_items = DUAL ? 64 : NT * 64;
+    const int n_items = DUAL ? 64 : ITEMS;
     if (tid >= n_items) return;
     const int t = DUAL ? 0 : tid / 64, ln = tid % 64;
     const int n = ln & 15;
@@ -320,61 +364,190 @@ skinny_kernel(const float *__restrict__ W, const float *__restrict__ W2, const f
     float v[4] = {s0[0], s0[1], s0[2], s0[3]};
     const int nv = min(4, M - m);
 
+    if (epi.mode == EPI_PARTIAL) {  // raw split-K partial, [split][16][M]; the consumer reduces
+        float *o = epi.out + ((long)blockIdx.y * 16 + n) * M + m;
+        if (nv == 4 && (M & 3) == 0) *(float4 *)o = make_float4(v[0], v[1], v[2], v[3]);
+        else
+            for (int r = 0; r < nv; ++r) o[r] = v[r];
+        return;
+    }
     if constexpr (DUAL) {  // SwiGLU: silu(gate) * up
         floatx4 s1 = red[0][1][ln];
 #pragma unroll
         for (int ww = 1; ww < WPB; ++ww) s1 += red[ww][1][ln];
+        if (epi.out_packed && nv == 4) {
+            *(float4 *)(epi.out + packed_b_offset(n, m)) =
+                make_float4(silu_f(v[0]) * s1[0], silu_f(v[1]) * s1[1], silu_f(v[2]) * s1[2], silu_f(v[3]) * s1[3]);
+            return;
+        }
         float *o = epi.out + (long)n * epi.ldo + m;
         for (int r = 0; r < nv; ++r) o[r] = silu_f(v[r]) * s1[r];
         return;
     } else {
-    if (epi.bias)
-        for (int r = 0; r < nv; ++r) v[r] = v[r] + epi.bias[m + r];
-    if (epi.mode == EPI_STORE) {
-        float *o = epi.out + (long)n * epi.ldo + m;
-        for (int r = 0; r < nv; ++r) o[r] = apply_act(v[r], epi.act);
-    } else if (epi.mode == EPI_RESID) {
-        float *o = epi.out + (long)n * epi.ldo + m;
-        for (int r = 0; r < nv; ++r) o[r] = o[r] + v[r];
-    } else {  // EPI_QKV (m % 4 == 0, d % 16 == 0, dh even: the 4 rows share a section and head)
-        const int sec = m / epi.d, e = m - sec * epi.d, h = e / epi.dh, ee = e - h * epi.dh;
-        const int pos = epi.pos[n];
-        if (epi.rope && sec < 2) {
-#pragma unroll
-            for (int pr = 0; pr < 2; ++pr) {
-                int i = (ee + 2 * pr) / 2;
-                double inv = pow((double)epi.theta, -2.0 * i / (double)epi.dh);
-                double a = (double)pos * inv, cs = cos(a), sn = sin(a);
-                double x0 = v[2 * pr], x1 = v[2 * pr + 1];
-                v[2 * pr] = (float)(x0 * cs - x1 * sn);
-                v[2 * pr + 1] = (float)(x0 * sn + x1 * cs);
+        if (epi.bias)
+            for (int r = 0; r < nv; ++r) v[r] = v[r] + epi.bias[m + r];
+        if (epi.mode == EPI_STORE) {
+            if (epi.out_packed && nv == 4) {
+                *(float4 *)(epi.out + packed_b_offset(n, m)) = make_float4(
+                    apply_act(v[0], epi.act), apply_act(v[1], epi.act), apply_act(v[2], epi.act), apply_act(v[3], epi.act));
+                return;
             }
+            float *o = epi.out + (long)n * epi.ldo + m;
+            for (int r = 0; r < nv; ++r) o[r] = apply_act(v[r], epi.act);
+        } else if (epi.mode == EPI_RESID) {
+            float *o = epi.out + (long)n * epi.ldo + m;
+            for (int r = 0; r < nv; ++r) o[r] = o[r] + v[r];
+        } else {  // EPI_QKV (m % 4 == 0, d % 16 == 0, dh even: the 4 rows share a section and head)
+            const int sec = m / epi.d, e = m - sec * epi.d, h = e / epi.dh, ee = e - h * epi.dh;
+            const int pos = epi.pos[n];
+            if (epi.rope && sec < 2) {
+#pragma unroll
+                for (int pr = 0; pr < 2; ++pr) {
+                    int i = (ee + 2 * pr) / 2;
+                    double inv = pow((double)epi.theta, -2.0 * i / (double)epi.dh);
+                    double a = (double)pos * inv, cs = cos(a), sn = sin(a);
+                    double x0 = v[2 * pr], x1 = v[2 * pr + 1];
+                    v[2 * pr] = (float)(x0 * cs - x1 * sn);
+                    v[2 * pr + 1] = (float)(x0 * sn + x1 * cs);
+                }
+            }
+            float *dst;
+            if (sec == 0) dst = epi.q_out + (long)n * epi.d + e;
+            else dst = (sec == 1 ? epi.k_cache : epi.v_cache) + (long)n * epi.kv_sb + (long)h * epi.kv_sh +
+                       (long)pos * epi.dh + ee;
+            *(float4 *)dst = make_float4(v[0], v[1], v[2], v[3]);
         }
-        float *dst;
-        if (sec == 0) dst = epi.q_out + (long)n * epi.d + e;
-        else dst = (sec == 1 ? epi.k_cache : epi.v_cache) + (long)n * epi.kv_sb + (long)h * epi.kv_sh +
-                   (long)pos * epi.dh + ee;
-        *(float4 *)dst = make_float4(v[0], v[1], v[2], v[3]);
-    }
     }
 }
 
+template <int NT, int WPB, int DEPTH, bool DUAL, bool PACKED>
+static void launch_skinny(const float *W, const float *W2, const float *X, long ldx, int M, int N, int K,
+                          const SkinnyEpiArgs &epi, hipStream_t s)
+{
+    const int rows = DUAL ? 16 : NT * 16;
+    const int ks = epi.mode == EPI_PARTIAL ? std::max(1, epi.ksplit) : 1;
+    hipLaunchKernelGGL((skinny_kernel<NT, WPB, DEPTH, DUAL, PACKED>), dim3((M + rows - 1) / rows, ks), dim3(WPB * 64), 0,
+                       s, W, W2, X, ldx, M, N, K, epi);
+}
+
+// geometry by row count: enough workgroups to cover the 256 CUs first, then more bytes per
+// wave (two row tiles) once the row groups outnumber the CUs several times over
+SkinnyTuning skinny_default_tuning(int M, int K, bool dual)
+{
+    SkinnyTuning t;
+    const int rt = (M + 15) / 16;
+    t.nt = (!dual && rt >= 1536) ? 2 : 1;
+    t.wpb = (dual || rt >= 1536) ? 8 : (rt >= 512 ? 4 : 8);
+    t.depth = rt >= 512 ? 2 : 3;
+    (void)K;
+    return t;
+}
+
+int skinny_pick_ksplit(int M, int K)
+{
+    const int rgroups = (M + 15) / 16, nchunk = (K + 63) / 64;
+    int ks = std::max(1, std::min({1024 / std::max(rgroups, 1), nchunk / 2, 8}));
+    const int cpb = (nchunk + ks - 1) / ks;
+    return (nchunk + cpb - 1) / cpb;  // every split non-empty
+}
+
 jas_status skinny_gemm(const float *W, const float *W2, const float *X, long ldx, int M, int N, int K,
-                       const SkinnyEpiArgs &epi, hipStream_t s)
+                       const SkinnyEpiArgs &epi, hipStream_t s, bool packed, const SkinnyTuning *tune)
 {
     JAS_CHECK(N >= 1 && N <= 16 && M > 0 && K > 0 && K % 4 == 0 && ldx % 4 == 0, JAS_ERR_INVALID,
               "skinny_gemm: unsupported shape");
+    JAS_CHECK(!packed || K % 16 == 0, JAS_ERR_INVALID, "skinny_gemm: packed weights need K % 16 == 0");
+    JAS_CHECK(!epi.out_packed || (M % 16 == 0 && (epi.mode == EPI_STORE || epi.mode == EPI_SWIGLU)), JAS_ERR_INVALID,
+              "skinny_gemm: packed output needs M % 16 == 0");
     JAS_CHECK(al16(W) && al16(X) && (!W2 || al16(W2)), JAS_ERR_INVALID, "skinny_gemm: operands must be 16B aligned");
+    const bool dual = epi.mode == EPI_SWIGLU;
     if (epi.mode == EPI_QKV)
         JAS_CHECK(epi.d % 16 == 0 && epi.dh % 4 == 0 && M == 3 * epi.d, JAS_ERR_INVALID, "skinny_gemm: bad QKV shape");
-    if (epi.mode == EPI_SWIGLU) {
-        JAS_CHECK(W2 != nullptr, JAS_ERR_INVALID, "skinny_gemm: SwiGLU needs both weights");
-        hipLaunchKernelGGL((skinny_kernel<2, 8, true>), dim3(ceil_div(M, 16)), dim3(512), 0, s, W, W2, X, ldx, M, N, K,
-                           epi);
+    if (dual) JAS_CHECK(W2 != nullptr, JAS_ERR_INVALID, "skinny_gemm: SwiGLU needs both weights");
+    SkinnyTuning tu = tune ? *tune : skinny_default_tuning(M, K, dual);
+    const int nt = dual ? 2 : tu.nt;
+    SkinnyEpiArgs ep = epi;
+    const int nchunk = (K + 63) / 64;
+    if (ep.mode == EPI_PARTIAL) {
+        JAS_CHECK(!dual && ep.ksplit >= 1 && ep.out, JAS_ERR_INVALID, "skinny_gemm: bad split-K partial request");
+        ep.cpb = (nchunk + ep.ksplit - 1) / ep.ksplit;
+        ep.ksplit = (nchunk + ep.cpb - 1) / ep.cpb;  // splits actually used (all non-empty)
+        JAS_CHECK(ep.ksplit == epi.ksplit, JAS_ERR_INVALID, "skinny_gemm: K too short for the requested split");
     } else {
-        hipLaunchKernelGGL((skinny_kernel<1, 8, false>), dim3(ceil_div(M, 16)), dim3(512), 0, s, W, W2, X, ldx, M, N,
-                           K, epi);
+        ep.cpb = nchunk;
+        ep.ksplit = 1;
     }
+#define JAS_SK(NTV, WPBV, DV, PV, DEP)                                                         \
+    if (nt == NTV && tu.wpb == WPBV && dual == DV && packed == PV && tu.depth == DEP) {       \
+        launch_skinny<NTV, WPBV, DEP, DV, PV>(W, W2, X, ldx, M, N, K, ep, s);                 \
+        JAS_LAUNCH_CHECK();                                                                    \
+        return JAS_OK;                                                                         \
+    }
+#define JAS_SK_D(NTV, WPBV, DV, PV) JAS_SK(NTV, WPBV, DV, PV, 2) JAS_SK(NTV, WPBV, DV, PV, 3) JAS_SK(NTV, WPBV, DV, PV, 4)
+#define JAS_SK_P(NTV, WPBV, DV) JAS_SK_D(NTV, WPBV, DV, true) JAS_SK_D(NTV, WPBV, DV, false)
+    JAS_SK_P(1, 4, false) JAS_SK_P(1, 8, false) JAS_SK_P(2, 4, false) JAS_SK_P(2, 8, false) JAS_SK_P(2, 4, true)
+    JAS_SK_P(2, 8, true)
+    // 1024-thread workgroups get 128 VGPRs: depth 4 would spill
+    JAS_SK(1, 16, false, true, 2) JAS_SK(1, 16, false, true, 3) JAS_SK(1, 16, false, false, 2)
+    JAS_SK(1, 16, false, false, 3)
+#undef JAS_SK_P
+#undef JAS_SK_D
+#undef JAS_SK
+    return fail(JAS_ERR_INVALID, "skinny_gemm: unsupported tuning");
+}
+
+// ---------------------------------------------------------------- packed weight layout
+__global__ void weight_pack_kernel(const float *__restrict__ src, float *__restrict__ dst, int M, int Mp, int K,
+                                   int unpack)
+{
+    long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= (long)Mp * K) return;
+    int r, k;
+    weight_pack_coords(p, K, &r, &k);
+    if (unpack) {
+        if (r < M) dst[(long)r * K + k] = src[p];
+    } else {
+        dst[p] = r < M ? src[(long)r * K + k] : 0.0f;
+    }
+}
+
+__global__ void fill_normal_packed_kernel(float *x, int M, int Mp, int K, uint64_t key, float mean, float std)
+{
+    long stride = (long)gridDim.x * blockDim.x;
+    for (long p = (long)blockIdx.x * blockDim.x + threadIdx.x; p < (long)Mp * K; p += stride) {
+        int r, k;
+        weight_pack_coords(p, K, &r, &k);
+        if (r >= M) {
+            x[p] = 0.0f;
+            continue;
+        }
+        uint64_t i = (uint64_t)r * K + k;  // the row-major element index drives the generator
+        uint64_t a = splitmix64(key + 2 * i), b = splitmix64(key + 2 * i + 1);
+        double u1 = ((double)(a >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+        double u2 = (double)(b >> 11) * (1.0 / 9007199254740992.0);
+        double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+        x[p] = (float)((double)mean + (double)std * z);
+    }
+}
+
+jas_status weight_pack(const float *src, float *dst, int M, int K, bool unpack, hipStream_t s)
+{
+    JAS_CHECK(K % 16 == 0, JAS_ERR_INVALID, "weight_pack: K must be a multiple of 16");
+    const int Mp = (M + 15) / 16 * 16;
+    long n = (long)Mp * K;
+    hipLaunchKernelGGL(weight_pack_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, s, src, dst, M, Mp, K, unpack ? 1 : 0);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
+jas_status fill_normal_packed(float *x, int M, int K, uint64_t seed, uint64_t stream_id, float mean, float std,
+                              hipStream_t s)
+{
+    JAS_CHECK(K % 16 == 0, JAS_ERR_INVALID, "fill_normal_packed: K must be a multiple of 16");
+    const int Mp = (M + 15) / 16 * 16;
+    unsigned nb = (unsigned)std::min<long>(((long)Mp * K + 255) / 256, 65536);
+    hipLaunchKernelGGL(fill_normal_packed_kernel, dim3(nb), dim3(256), 0, s, x, M, Mp, K, stream_key(seed, stream_id),
+                       mean, std);
     JAS_LAUNCH_CHECK();
     return JAS_OK;
 }
@@ -403,8 +576,8 @@ extern "C" jas_status jas_gemm(int M, int N, int K, const float *A, long as0, lo
         e.bias = bias_mode == 1 ? bias : nullptr;
         e.out = C;
         e.ldo = cs1;
-        return skinny_gemm(A, nullptr, B, bs1, M, N, K, e, s);
+        return skinny_gemm(A, nullptr, B, bs1, M, N, K, e, s, false, nullptr);
     }
     return gemm_general(M, N, K, A, as0, as1, B, bs0, bs1, C, cs0, cs1, bias, bias_mode, act, accumulate, batch, abs_,
-                        bbs, cbs, biasbs, s);
+                        bbs, cbs, biasbs, s, false);
 }

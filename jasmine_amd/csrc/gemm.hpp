@@ -10,8 +10,10 @@ enum SkinnyEpi : int {
     EPI_STORE = 0,   // out[n*ldo + m] = act(acc + bias[m])
     EPI_RESID = 1,   // out[n*ldo + m] += acc + bias[m]        (residual stream update)
     EPI_SWIGLU = 2,  // out[n*ldo + m] = silu(acc_gate) * acc_up  (W = gate rows, W2 = up rows)
-    EPI_QKV = 3      // rows [0,d) q, [d,2d) k, [2d,3d) v: (+bias) (+RoPE on q,k), q -> q_out,
+    EPI_QKV = 3,     // rows [0,d) q, [d,2d) k, [2d,3d) v: (+bias) (+RoPE on q,k), q -> q_out,
                      // k/v -> KV cache at the token's position
+    EPI_PARTIAL = 4  // K split over `ksplit` workgroups; out[(s*16 + n)*M + m] = partial sum of
+                     // split s (no bias/activation); the consumer adds the splits in order
 };
 
 struct SkinnyEpiArgs {
@@ -20,6 +22,10 @@ struct SkinnyEpiArgs {
     const float *bias = nullptr;
     float *out = nullptr;
     long ldo = 0;
+    int ksplit = 1;  // EPI_PARTIAL: number of K splits (each gets ceil(chunks/ksplit) 64-chunks)
+    int cpb = 0;     // set by skinny_gemm: K chunks per split
+    int out_packed = 0;  // EPI_STORE / EPI_SWIGLU: write out in the packed B-operand layout
+                         // (packed_b_offset over ldo features) for the next packed GEMM
     // EPI_QKV
     float *q_out = nullptr;   // [n][d]
     float *k_cache = nullptr; // element (n, h, t, e) at n*kv_sb + h*kv_sh + t*dh + e
@@ -31,14 +37,57 @@ struct SkinnyEpiArgs {
     float theta = 10000.f;
 };
 
-// C(n, m) over N <= 16 tokens: acc = W[m, :] . X[n, :] with W [M][K] and X [N][ldx] both
-// K-contiguous.  W2 (EPI_SWIGLU only) has the same shape as W.
+// Launch geometry of the weight-streaming GEMM: NT 16-row tiles per workgroup (non-SwiGLU)
+// and WPB waves per workgroup splitting K.
+struct SkinnyTuning {
+    int nt = 1, wpb = 8, depth = 2;  // depth: chunk buffers in the load pipeline
+};
+SkinnyTuning skinny_default_tuning(int M, int K, bool dual);
+// K splits (<= 8, all non-empty) for an EPI_PARTIAL launch of an [M][K] weight
+int skinny_pick_ksplit(int M, int K);
+
+// Packed weight layout for a [M][K] matrix (K % 16 == 0, rows padded to Mp = ceil16(M)
+// with zeros): element (r, k) lives at
+//   ((r/16 * K/16 + k/16) * 64 + lane) * 4 + k%4,  lane = r%16 + 16 * ((k%16)/4)
+// i.e. every 16x16 block is the 64 float4 A-operand registers of one MFMA wave, in lane
+// order, and the blocks of a 16-row tile follow each other along K.
+__host__ __device__ inline long weight_pack_offset(int r, int k, int K)
+{
+    const long blk = (long)(r >> 4) * (K >> 4) + (k >> 4);
+    const int lane = (r & 15) + 16 * ((k & 15) >> 2);
+    return (blk * 64 + lane) * 4 + (k & 3);
+}
+__host__ __device__ inline void weight_pack_coords(long p, int K, int *r, int *k)
+{
+    const long blk = p >> 8;
+    const int within = (int)(p & 255), lane = within >> 2, e = within & 3;
+    const int K16 = K >> 4;
+    const long rt = blk / K16;
+    const int kc = (int)(blk - rt * K16);
+    *r = (int)(rt * 16 + (lane & 15));
+    *k = kc * 16 + 4 * (lane >> 4) + e;
+}
+// Packed B-operand (activation) layout of a [16 tokens][K] matrix: element (n, k) at
+//   ((k/16) * 64 + lane) * 4 + k%4,  lane = n + 16 * ((k%16)/4)
+// so one 16-wide K block is the 64 float4 B-operand registers of an MFMA wave in lane order.
+__host__ __device__ inline long packed_b_offset(int n, int k)
+{
+    return ((long)(k >> 4) * 64 + n + 16 * ((k & 15) >> 2)) * 4 + (k & 3);
+}
+jas_status weight_pack(const float *src, float *dst, int M, int K, bool unpack, hipStream_t s);
+jas_status fill_normal_packed(float *x, int M, int K, uint64_t seed, uint64_t stream_id, float mean, float std,
+                              hipStream_t s);
+
+// C(n, m) over N <= 16 tokens: acc = W[m, :] . X[n, :].  Row-major: W [M][K], X [N][ldx].
+// packed: W in weight_pack_offset layout and X in packed_b_offset layout (ldx ignored).
+// W2 (EPI_SWIGLU only) has the same shape and layout as W.
 jas_status skinny_gemm(const float *W, const float *W2, const float *X, long ldx, int M, int N, int K,
-                       const SkinnyEpiArgs &epi, hipStream_t s);
+                       const SkinnyEpiArgs &epi, hipStream_t s, bool packed = false,
+                       const SkinnyTuning *tune = nullptr);
 
 // General strided GEMM (see jas_gemm in jasmine_hip.h).
 jas_status gemm_general(int M, int N, int K, const float *A, long as0, long as1, const float *B, long bs0, long bs1,
                         float *C, long cs0, long cs1, const float *bias, int bias_mode, int act, int accumulate,
-                        int batch, long abs_, long bbs, long cbs, long biasbs, hipStream_t s);
+                        int batch, long abs_, long bbs, long cbs, long biasbs, hipStream_t s, bool a_packed = false);
 
 } // namespace jas

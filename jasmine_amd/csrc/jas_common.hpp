@@ -15,6 +15,14 @@ void set_error(const std::string &msg);
 jas_status fail(jas_status code, const std::string &msg);
 hipStream_t stream_or_default(jas_stream_t s);
 void *workspace(size_t bytes, hipStream_t s);
+// x[n] += sum_s part[(s*16 + n)*d ...] + bias; y = norm(x) (RMSNorm, or LayerNorm with b)
+jas_status resid_norm(float *x, const float *part, int ks, const float *bias, const float *g, const float *b, float *y,
+                      int N, int d, float eps, bool rms, hipStream_t s, bool y_packed = false);
+// decode attention with an optional packed-B output (o_packed_d = H*D features) for the
+// next packed GEMM; 0 = the jas_attn_decode layout O[b][h][D]
+jas_status attn_decode_impl(const float *q, const float *K, const float *V, float *O, const int32_t *seqlens, int B,
+                            int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, hipStream_t s,
+                            int o_packed_d);
 
 #define JAS_HIP(expr)                                                                 \
     do {                                                                              \

@@ -23,8 +23,13 @@
 
 namespace jas {
 
+// A stacked weight tensor: `layers` matrices of [rows][cols]; packed matrices use the
+// MFMA-native layout of weight_pack_offset with rows padded to a multiple of 16.
 struct Tensor {
     size_t off = 0, count = 0;
+    int layers = 1, rows = 1, cols = 1;
+    bool packed = false;
+    long lstride() const { return (long)(packed ? (rows + 15) / 16 * 16 : rows) * cols; }
 };
 
 __global__ void set_positions_kernel(int32_t *pos, int32_t *seqlens, int B, int p)
@@ -68,6 +73,19 @@ __global__ void swiglu_kernel(const float *__restrict__ gate, const float *__res
     if (i < n) out[i] = silu_f(gate[i]) * up[i];
 }
 
+// token embedding gather from a packed [V][d] table (GPT-2 ties it to the LM head)
+__global__ void embed_packed_kernel(const float *__restrict__ wte, const float *__restrict__ wpe,
+                                    const int32_t *__restrict__ ids, const int32_t *__restrict__ pos,
+                                    float *__restrict__ out, int n, int d)
+{
+    long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= (long)n * d) return;
+    int t = (int)(g / d), e = (int)(g % d);
+    float v = wte[weight_pack_offset(ids[t], e, d)];
+    if (wpe) v = v + wpe[(long)pos[t] * d + e];
+    out[g] = v;
+}
+
 __global__ void copy_ids_kernel(const int32_t *src, int32_t *dst, int B)
 {
     int b = blockIdx.x * blockDim.x + threadIdx.x;
@@ -92,6 +110,8 @@ struct jas_lm {
     int32_t *ids = nullptr, *pos = nullptr, *seqlens = nullptr, *hist = nullptr;
     int hist_cap = 0;
     void *attn_ws = nullptr;
+    float *part = nullptr;  // K-split partials of the residual projections [split][16][d]
+    int ks_o = 1, ks_d = 1;
     size_t attn_ws_bytes = 0;
     // prefill buffers (grown on demand)
     float *pX = nullptr, *pH = nullptr, *pQKV = nullptr, *pATT = nullptr, *pG = nullptr, *pU = nullptr, *pFF = nullptr;
@@ -110,19 +130,29 @@ struct jas_lm {
         auto it = tensors.find(n);
         return it == tensors.end() || it->second.count == 0 ? nullptr : arena + it->second.off;
     }
-    float *Wm(const char *n) { return const_cast<float *>(W(n)); }
+    // layer l of a stacked tensor (nullptr when the model kind lacks it)
+    const float *LW(const char *n, int l) const
+    {
+        auto it = tensors.find(n);
+        if (it == tensors.end() || it->second.count == 0) return nullptr;
+        return arena + it->second.off + (long)l * it->second.lstride();
+    }
     int dh() const { return cfg.d_model / cfg.n_head; }
 };
 
 namespace {
 
-void add_tensor(jas_lm *lm, const char *name, size_t count, size_t &cursor)
+void add_tensor(jas_lm *lm, const char *name, int layers, int rows, int cols, bool packed, size_t &cursor)
 {
     Tensor t;
     t.off = cursor;
-    t.count = count;
+    t.layers = layers;
+    t.rows = rows;
+    t.cols = cols;
+    t.packed = packed;
+    t.count = (size_t)layers * t.lstride();
     lm->tensors[name] = t;
-    cursor += (count + 63) & ~size_t(63);  // 256-byte aligned tensors
+    cursor += (t.count + 63) & ~size_t(63);  // 256-byte aligned tensors
 }
 
 jas_status prof_begin(jas_lm *lm, int cls)
@@ -166,9 +196,8 @@ jas_status norm_rows(jas_lm *lm, const float *x, float *y, int n_vec, long vstri
         g = lm->W("lnf_g");
         b = lm->W("lnf_b");
     } else {
-        g = lm->W(which == 1 ? "ln1_g" : "ln2_g") + (long)l_or_f * d;
-        const float *bb = lm->W(which == 1 ? "ln1_b" : "ln2_b");
-        b = bb ? bb + (long)l_or_f * d : nullptr;
+        g = lm->LW(which == 1 ? "ln1_g" : "ln2_g", l_or_f);
+        b = lm->LW(which == 1 ? "ln1_b" : "ln2_b", l_or_f);
     }
     TRY(prof_begin(lm, 2));
     if (c.kind == 0) TRY(jas_layernorm(x, y, n_vec, d, vstride, d, 1, c.eps, g, b, lm->stream));
@@ -180,7 +209,7 @@ jas_status norm_rows(jas_lm *lm, const float *x, float *y, int n_vec, long vstri
 jas_status proj(jas_lm *lm, const float *Wt, const float *X, int N, int M, int K, const SkinnyEpiArgs &e)
 {
     TRY(prof_begin(lm, 0));
-    TRY(skinny_gemm(Wt, nullptr, X, K, M, N, K, e, lm->stream));
+    TRY(skinny_gemm(Wt, nullptr, X, K, M, N, K, e, lm->stream, true));
     return prof_end(lm);
 }
 
@@ -205,6 +234,20 @@ jas_status ensure_prefill(jas_lm *lm, long tokens)
     return JAS_OK;
 }
 
+jas_status embed(jas_lm *lm, const int32_t *ids, const int32_t *pos, float *out, int n)
+{
+    const jas_lm_config &c = lm->cfg;
+    TRY(prof_begin(lm, 2));
+    if (c.kind == 0) {  // GPT-2: the tied, packed wte plus learned positions
+        hipLaunchKernelGGL(embed_packed_kernel, dim3(ceil_div((long)n * c.d_model, 256)), dim3(256), 0, lm->stream,
+                           lm->W("wte"), lm->W("wpe"), ids, pos, out, n, c.d_model);
+        JAS_LAUNCH_CHECK();
+    } else {
+        TRY(jas_embed(lm->W("wte"), nullptr, ids, pos, out, n, c.d_model, lm->stream));
+    }
+    return prof_end(lm);
+}
+
 // one decode step for lm->B sequences: d_ids in, argmax written back into d_ids
 jas_status decode_step(jas_lm *lm)
 {
@@ -213,14 +256,19 @@ jas_status decode_step(jas_lm *lm)
     JAS_CHECK(lm->position < c.max_ctx, JAS_ERR_RANGE, "jas_lm_decode: KV cache full (max_ctx reached)");
     hipStream_t s = lm->stream;
     hipLaunchKernelGGL(set_positions_kernel, dim3(1), dim3(256), 0, s, lm->pos, lm->seqlens, B, lm->position);
-    TRY(prof_begin(lm, 2));
-    TRY(jas_embed(lm->W("wte"), c.kind == 0 ? lm->W("wpe") : nullptr, lm->ids, lm->pos, lm->x, B, d, s));
-    TRY(prof_end(lm));
+    TRY(embed(lm, lm->ids, lm->pos, lm->x, B));
+    // The projections that feed the residual stream (O and down/proj) run K-split and leave
+    // their partial sums in lm->part; the next norm kernel adds them (plus the bias) to x.
+    int pend_ks = 0;
+    const float *pend_bias = nullptr;
     for (int l = 0; l < c.n_layer; ++l) {
-        TRY(norm_rows(lm, lm->x, lm->h, B, d, l, 1));
+        TRY(prof_begin(lm, 2));
+        TRY(resid_norm(lm->x, lm->part, pend_ks, pend_bias, lm->LW("ln1_g", l), lm->LW("ln1_b", l), lm->h, B, d,
+                       c.eps, c.kind == 1, s, true));
+        TRY(prof_end(lm));
         SkinnyEpiArgs eq;
         eq.mode = EPI_QKV;
-        eq.bias = lm->W("b_qkv") ? lm->W("b_qkv") + (long)l * 3 * d : nullptr;
+        eq.bias = lm->LW("b_qkv", l);
         eq.q_out = lm->q;
         eq.k_cache = lm->kc + l * lm->kv_layer;
         eq.v_cache = lm->vc + l * lm->kv_layer;
@@ -231,49 +279,53 @@ jas_status decode_step(jas_lm *lm)
         eq.dh = dh;
         eq.rope = c.kind == 1;
         eq.theta = c.rope_theta;
-        TRY(proj(lm, lm->W("w_qkv") + (long)l * 3 * d * d, lm->h, B, 3 * d, d, eq));
+        TRY(proj(lm, lm->LW("w_qkv", l), lm->h, B, 3 * d, d, eq));
         TRY(prof_begin(lm, 1));
-        TRY(jas_attn_decode(lm->q, lm->kc + l * lm->kv_layer, lm->vc + l * lm->kv_layer, lm->att, lm->seqlens, B, H,
-                            dh, lm->position + 1, lm->kv_sb, lm->kv_sh, 1.0f / sqrtf((float)dh), lm->attn_ws, s));
+        TRY(attn_decode_impl(lm->q, lm->kc + l * lm->kv_layer, lm->vc + l * lm->kv_layer, lm->att, lm->seqlens, B, H,
+                             dh, lm->position + 1, lm->kv_sb, lm->kv_sh, 1.0f / sqrtf((float)dh), lm->attn_ws, s, d));
         TRY(prof_end(lm));
         SkinnyEpiArgs eo;
-        eo.mode = EPI_RESID;
-        eo.bias = lm->W("b_o") ? lm->W("b_o") + (long)l * d : nullptr;
-        eo.out = lm->x;
-        eo.ldo = d;
-        TRY(proj(lm, lm->W("w_o") + (long)l * d * d, lm->att, B, d, d, eo));
-        TRY(norm_rows(lm, lm->x, lm->h, B, d, l, 2));
+        eo.mode = EPI_PARTIAL;
+        eo.out = lm->part;
+        eo.ksplit = lm->ks_o;
+        TRY(proj(lm, lm->LW("w_o", l), lm->att, B, d, d, eo));
+        TRY(prof_begin(lm, 2));
+        TRY(resid_norm(lm->x, lm->part, lm->ks_o, lm->LW("b_o", l), lm->LW("ln2_g", l), lm->LW("ln2_b", l), lm->h, B,
+                       d, c.eps, c.kind == 1, s, true));
+        TRY(prof_end(lm));
+        SkinnyEpiArgs ed;
+        ed.mode = EPI_PARTIAL;
+        ed.out = lm->part;
+        ed.ksplit = lm->ks_d;
         if (c.kind == 0) {
             SkinnyEpiArgs ef;
             ef.mode = EPI_STORE;
             ef.act = JAS_ACT_GELU;
-            ef.bias = lm->W("b_fc") + (long)l * F;
+            ef.bias = lm->LW("b_fc", l);
             ef.out = lm->ff;
             ef.ldo = F;
-            TRY(proj(lm, lm->W("w_fc") + (long)l * F * d, lm->h, B, F, d, ef));
-            SkinnyEpiArgs ep;
-            ep.mode = EPI_RESID;
-            ep.bias = lm->W("b_proj") + (long)l * d;
-            ep.out = lm->x;
-            ep.ldo = d;
-            TRY(proj(lm, lm->W("w_proj") + (long)l * d * F, lm->ff, B, d, F, ep));
+            ef.out_packed = 1;
+            TRY(proj(lm, lm->LW("w_fc", l), lm->h, B, F, d, ef));
+            TRY(proj(lm, lm->LW("w_proj", l), lm->ff, B, d, F, ed));
+            pend_bias = lm->LW("b_proj", l);
         } else {
             SkinnyEpiArgs eg;
             eg.mode = EPI_SWIGLU;
             eg.out = lm->ff;
             eg.ldo = F;
+            eg.out_packed = 1;
             TRY(prof_begin(lm, 0));
-            TRY(skinny_gemm(lm->W("w_gate") + (long)l * F * d, lm->W("w_up") + (long)l * F * d, lm->h, d, F, B, d, eg,
-                            s));
+            TRY(skinny_gemm(lm->LW("w_gate", l), lm->LW("w_up", l), lm->h, d, F, B, d, eg, s, true));
             TRY(prof_end(lm));
-            SkinnyEpiArgs ed;
-            ed.mode = EPI_RESID;
-            ed.out = lm->x;
-            ed.ldo = d;
-            TRY(proj(lm, lm->W("w_down") + (long)l * d * F, lm->ff, B, d, F, ed));
+            TRY(proj(lm, lm->LW("w_down", l), lm->ff, B, d, F, ed));
+            pend_bias = nullptr;
         }
+        pend_ks = lm->ks_d;
     }
-    TRY(norm_rows(lm, lm->x, lm->h, B, d, -1, 0));
+    TRY(prof_begin(lm, 2));
+    TRY(resid_norm(lm->x, lm->part, pend_ks, pend_bias, lm->W("lnf_g"), lm->W("lnf_b"), lm->h, B, d, c.eps,
+                   c.kind == 1, s, true));
+    TRY(prof_end(lm));
     SkinnyEpiArgs eh;
     eh.mode = EPI_STORE;
     eh.out = lm->logits;
@@ -286,6 +338,24 @@ jas_status decode_step(jas_lm *lm)
     return JAS_OK;
 }
 
+} // namespace
+
+namespace {
+// the generator index of element (l, r, k) is (l*rows + r)*cols + k, as for a row-major
+// [layers*rows][cols] tensor; each packed layer is filled with its own slice of that stream
+jas_status fill_normal_packed_layers(jas_lm *lm, const Tensor &t, float *p, uint64_t seed, uint64_t sid, float std)
+{
+    if (t.layers == 1) return fill_normal_packed(p, t.rows, t.cols, seed, sid, 0.0f, std, lm->stream);
+    // per layer: generate row-major into a scratch buffer, then pack
+    float *tmp = nullptr;
+    TRY(jas_malloc((void **)&tmp, (size_t)t.rows * t.cols * t.layers * sizeof(float)));
+    jas_status st = jas_fill_normal(tmp, (size_t)t.rows * t.cols * t.layers, seed, sid, 0.0f, std, lm->stream);
+    for (int l = 0; l < t.layers && st == JAS_OK; ++l)
+        st = weight_pack(tmp + (long)l * t.rows * t.cols, p + (long)l * t.lstride(), t.rows, t.cols, false, lm->stream);
+    (void)hipStreamSynchronize(lm->stream);
+    (void)hipFree(tmp);
+    return st;
+}
 } // namespace
 
 extern "C" {
@@ -304,6 +374,8 @@ jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out)
     JAS_CHECK(dh == 32 || dh == 64 || dh == 128, JAS_ERR_INVALID, "jas_lm_create: head dim must be 32, 64 or 128");
     JAS_CHECK(c.d_model % 64 == 0 && c.d_ff % 16 == 0, JAS_ERR_INVALID,
               "jas_lm_create: d_model must be a multiple of 64 and d_ff of 16");
+    // one 16-row packed tile never mixes two heads or the q/k/v sections
+    JAS_CHECK((c.d_model / c.n_head) % 16 == 0, JAS_ERR_INVALID, "jas_lm_create: head dim must be a multiple of 16");
     JAS_CHECK(c.max_batch <= 16, JAS_ERR_INVALID, "jas_lm_create: max_batch above 16 is not supported");
     TRY(jas_init(-1));
     jas_lm *lm = new jas_lm();
@@ -311,29 +383,30 @@ jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out)
     JAS_HIP(hipStreamCreateWithFlags(&lm->stream, hipStreamNonBlocking));
     const size_t d = c.d_model, F = c.d_ff, L = c.n_layer, V = c.vocab;
     size_t cur = 0;
-    add_tensor(lm, "wte", V * d, cur);
-    if (c.kind == 0) add_tensor(lm, "wpe", (size_t)c.max_ctx * d, cur);
-    add_tensor(lm, "ln1_g", L * d, cur);
-    if (c.kind == 0) add_tensor(lm, "ln1_b", L * d, cur);
-    add_tensor(lm, "w_qkv", L * 3 * d * d, cur);
-    if (c.kind == 0) add_tensor(lm, "b_qkv", L * 3 * d, cur);
-    add_tensor(lm, "w_o", L * d * d, cur);
-    if (c.kind == 0) add_tensor(lm, "b_o", L * d, cur);
-    add_tensor(lm, "ln2_g", L * d, cur);
-    if (c.kind == 0) add_tensor(lm, "ln2_b", L * d, cur);
+    const int Li = c.n_layer, di = c.d_model, Fi = c.d_ff, Vi = c.vocab;
+    add_tensor(lm, "wte", 1, Vi, di, c.kind == 0, cur);  // GPT-2: also the (packed) LM head
+    if (c.kind == 0) add_tensor(lm, "wpe", 1, c.max_ctx, di, false, cur);
+    add_tensor(lm, "ln1_g", Li, 1, di, false, cur);
+    if (c.kind == 0) add_tensor(lm, "ln1_b", Li, 1, di, false, cur);
+    add_tensor(lm, "w_qkv", Li, 3 * di, di, true, cur);
+    if (c.kind == 0) add_tensor(lm, "b_qkv", Li, 1, 3 * di, false, cur);
+    add_tensor(lm, "w_o", Li, di, di, true, cur);
+    if (c.kind == 0) add_tensor(lm, "b_o", Li, 1, di, false, cur);
+    add_tensor(lm, "ln2_g", Li, 1, di, false, cur);
+    if (c.kind == 0) add_tensor(lm, "ln2_b", Li, 1, di, false, cur);
     if (c.kind == 0) {
-        add_tensor(lm, "w_fc", L * F * d, cur);
-        add_tensor(lm, "b_fc", L * F, cur);
-        add_tensor(lm, "w_proj", L * d * F, cur);
-        add_tensor(lm, "b_proj", L * d, cur);
+        add_tensor(lm, "w_fc", Li, Fi, di, true, cur);
+        add_tensor(lm, "b_fc", Li, 1, Fi, false, cur);
+        add_tensor(lm, "w_proj", Li, di, Fi, true, cur);
+        add_tensor(lm, "b_proj", Li, 1, di, false, cur);
     } else {
-        add_tensor(lm, "w_gate", L * F * d, cur);
-        add_tensor(lm, "w_up", L * F * d, cur);
-        add_tensor(lm, "w_down", L * d * F, cur);
+        add_tensor(lm, "w_gate", Li, Fi, di, true, cur);
+        add_tensor(lm, "w_up", Li, Fi, di, true, cur);
+        add_tensor(lm, "w_down", Li, di, Fi, true, cur);
     }
-    add_tensor(lm, "lnf_g", d, cur);
-    if (c.kind == 0) add_tensor(lm, "lnf_b", d, cur);
-    if (c.kind == 1) add_tensor(lm, "w_head", V * d, cur);
+    add_tensor(lm, "lnf_g", 1, 1, di, false, cur);
+    if (c.kind == 0) add_tensor(lm, "lnf_b", 1, 1, di, false, cur);
+    if (c.kind == 1) add_tensor(lm, "w_head", 1, Vi, di, true, cur);
     lm->arena_count = cur;
     jas_status st = jas_malloc((void **)&lm->arena, cur * sizeof(float));
     if (st != JAS_OK) {
@@ -347,10 +420,13 @@ jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out)
     size_t kvn = (size_t)L * lm->kv_layer;
     st = jas_malloc((void **)&lm->kc, kvn * sizeof(float));
     if (st == JAS_OK) st = jas_malloc((void **)&lm->vc, kvn * sizeof(float));
-    struct { float **p; size_t n; } fb[] = {{&lm->x, Bm * d}, {&lm->h, Bm * d}, {&lm->q, Bm * d}, {&lm->att, Bm * d},
-                                            {&lm->ff, Bm * F}, {&lm->logits, Bm * V}};
-    for (auto &f : fb)
+    // decode activations span all 16 MFMA token columns (the packed B-operand layout)
+    struct { float **p; size_t n; } fb[] = {{&lm->x, 16 * d}, {&lm->h, 16 * d}, {&lm->q, 16 * d}, {&lm->att, 16 * d},
+                                            {&lm->ff, 16 * F}, {&lm->logits, Bm * V}};
+    for (auto &f : fb) {
         if (st == JAS_OK) st = jas_malloc((void **)f.p, f.n * sizeof(float));
+        if (st == JAS_OK) st = jas_memset(*f.p, 0, f.n * sizeof(float), lm->stream);
+    }
     if (st == JAS_OK) st = jas_malloc((void **)&lm->ids, 64 * sizeof(int32_t));
     if (st == JAS_OK) st = jas_malloc((void **)&lm->pos, 64 * sizeof(int32_t));
     if (st == JAS_OK) st = jas_malloc((void **)&lm->seqlens, 64 * sizeof(int32_t));
@@ -358,6 +434,11 @@ jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out)
     for (int b = 1; b < Bm; ++b)  // workspace must cover every batch size actually used
         lm->attn_ws_bytes = std::max(lm->attn_ws_bytes, jas_attn_decode_workspace(b, c.n_head, dh, c.max_ctx));
     if (st == JAS_OK && lm->attn_ws_bytes) st = jas_malloc(&lm->attn_ws, lm->attn_ws_bytes);
+    // K splits of the d-row residual projections: enough workgroups to cover the chip
+    lm->ks_o = skinny_pick_ksplit(c.d_model, c.d_model);
+    lm->ks_d = skinny_pick_ksplit(c.d_model, c.d_ff);
+    if (st == JAS_OK)
+        st = jas_malloc((void **)&lm->part, sizeof(float) * (size_t)std::max(lm->ks_o, lm->ks_d) * 16 * c.d_model);
     if (st != JAS_OK) {
         jas_lm_destroy(lm);
         return st;
@@ -371,7 +452,7 @@ jas_status jas_lm_destroy(jas_lm *lm)
     if (!lm) return JAS_OK;
     if (lm->stream) (void)hipStreamSynchronize(lm->stream);
     void *ptrs[] = {lm->arena, lm->kc, lm->vc, lm->x, lm->h, lm->q, lm->att, lm->ff, lm->logits, lm->ids, lm->pos,
-                    lm->seqlens, lm->hist, lm->attn_ws, lm->pX, lm->pH, lm->pQKV, lm->pATT, lm->pG, lm->pU, lm->pFF,
+                    lm->seqlens, lm->hist, lm->attn_ws, lm->part, lm->pX, lm->pH, lm->pQKV, lm->pATT, lm->pG, lm->pU, lm->pFF,
                     lm->pIds, lm->pPos};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
@@ -395,6 +476,8 @@ jas_status jas_lm_init_random(jas_lm *lm, uint64_t seed, float std)
             TRY(jas_memcpy_h2d(p, ones.data(), cnt * sizeof(float), lm->stream));
         } else if (n[0] == 'b' || n == "ln1_b" || n == "ln2_b" || n == "lnf_b") {
             JAS_HIP(hipMemsetAsync(p, 0, cnt * sizeof(float), lm->stream));
+        } else if (kv.second.packed) {  // same values as a row-major fill of [layers*rows][cols]
+            TRY(fill_normal_packed_layers(lm, kv.second, p, seed, sid, std));
         } else {
             TRY(jas_fill_normal(p, cnt, seed, sid, 0.0f, std, lm->stream));
         }
@@ -403,16 +486,54 @@ jas_status jas_lm_init_random(jas_lm *lm, uint64_t seed, float std)
     return JAS_OK;
 }
 
-jas_status jas_lm_weight(jas_lm *lm, const char *name, float **ptr, size_t *count)
+jas_status jas_lm_weight_shape(jas_lm *lm, const char *name, int *layers, int *rows, int *cols)
 {
-    JAS_CHECK(lm && name && ptr && count, JAS_ERR_INVALID, "jas_lm_weight: null argument");
+    JAS_CHECK(lm && name && layers && rows && cols, JAS_ERR_INVALID, "jas_lm_weight_shape: null argument");
     auto it = lm->tensors.find(name);
-    *ptr = nullptr;
-    *count = 0;
+    *layers = *rows = *cols = 0;
     if (it == lm->tensors.end()) return JAS_OK;
-    *ptr = lm->arena + it->second.off;
-    *count = it->second.count;
+    *layers = it->second.layers;
+    *rows = it->second.rows;
+    *cols = it->second.cols;
     return JAS_OK;
+}
+
+// host <-> device copy of a tensor in logical row-major [layers][rows][cols] order
+static jas_status weight_copy(jas_lm *lm, const char *name, float *h, size_t count, bool to_host)
+{
+    JAS_CHECK(lm && name && h, JAS_ERR_INVALID, "jas_lm weight copy: null argument");
+    auto it = lm->tensors.find(name);
+    JAS_CHECK(it != lm->tensors.end(), JAS_ERR_INVALID, std::string("jas_lm: no weight named ") + name);
+    const Tensor &t = it->second;
+    const size_t n = (size_t)t.layers * t.rows * t.cols;
+    JAS_CHECK(count == n, JAS_ERR_INVALID, "jas_lm weight copy: element count mismatch");
+    float *dev = lm->arena + t.off;
+    if (!t.packed) {
+        return to_host ? jas_memcpy_d2h(h, dev, n * sizeof(float), lm->stream)
+                       : jas_memcpy_h2d(dev, h, n * sizeof(float), lm->stream);
+    }
+    float *tmp = nullptr;
+    TRY(jas_malloc((void **)&tmp, n * sizeof(float)));
+    jas_status st = JAS_OK;
+    const long lsz = (long)t.rows * t.cols;
+    if (!to_host) st = jas_memcpy_h2d(tmp, h, n * sizeof(float), lm->stream);
+    for (int l = 0; l < t.layers && st == JAS_OK; ++l)
+        st = to_host ? weight_pack(dev + l * t.lstride(), tmp + l * lsz, t.rows, t.cols, true, lm->stream)
+                     : weight_pack(tmp + l * lsz, dev + l * t.lstride(), t.rows, t.cols, false, lm->stream);
+    if (to_host && st == JAS_OK) st = jas_memcpy_d2h(h, tmp, n * sizeof(float), lm->stream);
+    (void)hipStreamSynchronize(lm->stream);
+    (void)hipFree(tmp);
+    return st;
+}
+
+jas_status jas_lm_get_weight(jas_lm *lm, const char *name, float *h_dst, size_t count)
+{
+    return weight_copy(lm, name, h_dst, count, true);
+}
+
+jas_status jas_lm_set_weight(jas_lm *lm, const char *name, const float *h_src, size_t count)
+{
+    return weight_copy(lm, name, const_cast<float *>(h_src), count, false);
 }
 
 jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_t *h_next, float *h_logits)
@@ -431,7 +552,7 @@ jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_
     lm->position = 0;
     TRY(jas_memcpy_h2d(lm->pIds, h_ids, T * sizeof(int32_t), s));
     hipLaunchKernelGGL(prefill_positions_kernel, dim3(ceil_div(T, 256)), dim3(256), 0, s, lm->pPos, B, P);
-    TRY(jas_embed(lm->W("wte"), c.kind == 0 ? lm->W("wpe") : nullptr, lm->pIds, lm->pPos, lm->pX, (int)T, d, s));
+    TRY(embed(lm, lm->pIds, lm->pPos, lm->pX, (int)T));
     const bool verbose = getenv("JAS_VERBOSE") != nullptr;
     for (int l = 0; l < c.n_layer; ++l) {
         if (verbose && l % 4 == 0) {  // progress for long prefills (synchronises, diagnostics only)
@@ -440,10 +561,10 @@ jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_
             fflush(stderr);
         }
         TRY(norm_rows(lm, lm->pX, lm->pH, (int)T, d, l, 1));
-        const float *bq = lm->W("b_qkv") ? lm->W("b_qkv") + (long)l * 3 * d : nullptr;
-        // QKV[n][m] = sum_k w_qkv[m][k] H[n][k] (+ b[m])
-        TRY(gemm_general(3 * d, (int)T, d, lm->W("w_qkv") + (long)l * 3 * d * d, d, 1, lm->pH, 1, d, lm->pQKV, 1,
-                         3L * d, bq, bq ? 1 : 0, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s));
+        const float *bq = lm->LW("b_qkv", l);
+        // QKV[n][m] = sum_k w_qkv[m][k] H[n][k] (+ b[m]); weights in the packed layout
+        TRY(gemm_general(3 * d, (int)T, d, lm->LW("w_qkv", l), d, 1, lm->pH, 1, d, lm->pQKV, 1, 3L * d, bq,
+                         bq ? 1 : 0, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true));
         if (c.kind == 1)  // q and k sections are 2H consecutive heads of each row
             TRY(jas_rope_llama(lm->pQKV, lm->pPos, (int)T, 2 * H, dh, 3L * d, c.rope_theta, s));
         float *kcl = lm->kc + l * lm->kv_layer, *vcl = lm->vc + l * lm->kv_layer;
@@ -451,33 +572,36 @@ jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_
                            B, P, H, dh, c.max_ctx);
         TRY(jas_attn_prefill(lm->pQKV, kcl, vcl, lm->pATT, B, H, P, P, dh, (long)P * 3 * d, dh, 3L * d, lm->kv_sb,
                              lm->kv_sh, dh, (long)P * d, dh, d, 1.0f / sqrtf((float)dh), 1, JAS_F32, s));
-        const float *bo = lm->W("b_o") ? lm->W("b_o") + (long)l * d : nullptr;
-        TRY(gemm_general(d, (int)T, d, lm->W("w_o") + (long)l * d * d, d, 1, lm->pATT, 1, d, lm->pX, 1, d, bo,
-                         bo ? 1 : 0, JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s));
+        const float *bo = lm->LW("b_o", l);
+        TRY(gemm_general(d, (int)T, d, lm->LW("w_o", l), d, 1, lm->pATT, 1, d, lm->pX, 1, d, bo, bo ? 1 : 0,
+                         JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s, true));
         TRY(norm_rows(lm, lm->pX, lm->pH, (int)T, d, l, 2));
         if (c.kind == 0) {
-            TRY(gemm_general(F, (int)T, d, lm->W("w_fc") + (long)l * F * d, d, 1, lm->pH, 1, d, lm->pG, 1, F,
-                             lm->W("b_fc") + (long)l * F, 1, JAS_ACT_GELU, 0, 1, 0, 0, 0, 0, s));
-            TRY(gemm_general(d, (int)T, F, lm->W("w_proj") + (long)l * d * F, F, 1, lm->pG, 1, F, lm->pX, 1, d,
-                             lm->W("b_proj") + (long)l * d, 1, JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s));
+            TRY(gemm_general(F, (int)T, d, lm->LW("w_fc", l), d, 1, lm->pH, 1, d, lm->pG, 1, F, lm->LW("b_fc", l), 1,
+                             JAS_ACT_GELU, 0, 1, 0, 0, 0, 0, s, true));
+            TRY(gemm_general(d, (int)T, F, lm->LW("w_proj", l), F, 1, lm->pG, 1, F, lm->pX, 1, d,
+                             lm->LW("b_proj", l), 1, JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s, true));
         } else {
-            TRY(gemm_general(F, (int)T, d, lm->W("w_gate") + (long)l * F * d, d, 1, lm->pH, 1, d, lm->pG, 1, F,
-                             nullptr, 0, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s));
-            TRY(gemm_general(F, (int)T, d, lm->W("w_up") + (long)l * F * d, d, 1, lm->pH, 1, d, lm->pU, 1, F, nullptr,
-                             0, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s));
+            TRY(gemm_general(F, (int)T, d, lm->LW("w_gate", l), d, 1, lm->pH, 1, d, lm->pG, 1, F, nullptr, 0,
+                             JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true));
+            TRY(gemm_general(F, (int)T, d, lm->LW("w_up", l), d, 1, lm->pH, 1, d, lm->pU, 1, F, nullptr, 0,
+                             JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true));
             hipLaunchKernelGGL(swiglu_kernel, dim3(ceil_div(T * F, 256)), dim3(256), 0, s, lm->pG, lm->pU, lm->pFF,
                                T * F);
-            TRY(gemm_general(d, (int)T, F, lm->W("w_down") + (long)l * d * F, F, 1, lm->pFF, 1, F, lm->pX, 1, d,
-                             nullptr, 0, JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s));
+            TRY(gemm_general(d, (int)T, F, lm->LW("w_down", l), F, 1, lm->pFF, 1, F, lm->pX, 1, d, nullptr, 0,
+                             JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s, true));
         }
     }
-    // final norm and LM head on the last position of every sequence
-    TRY(norm_rows(lm, lm->pX + (long)(P - 1) * d, lm->h, B, (long)P * d, -1, 0));
+    // final norm and LM head on the last position of every sequence (packed B operand)
+    JAS_HIP(hipMemcpy2DAsync(lm->x, d * sizeof(float), lm->pX + (long)(P - 1) * d, (size_t)P * d * sizeof(float),
+                             d * sizeof(float), B, hipMemcpyDeviceToDevice, s));
+    TRY(resid_norm(lm->x, nullptr, 0, nullptr, lm->W("lnf_g"), lm->W("lnf_b"), lm->h, B, d, c.eps, c.kind == 1, s,
+                   true));
     SkinnyEpiArgs eh;
     eh.mode = EPI_STORE;
     eh.out = lm->logits;
     eh.ldo = V;
-    TRY(skinny_gemm(c.kind == 0 ? lm->W("wte") : lm->W("w_head"), nullptr, lm->h, d, V, B, d, eh, s));
+    TRY(skinny_gemm(c.kind == 0 ? lm->W("wte") : lm->W("w_head"), nullptr, lm->h, d, V, B, d, eh, s, true));
     TRY(jas_argmax(lm->logits, B, V, V, lm->ids, s));
     lm->position = P;
     if (h_next) TRY(jas_memcpy_d2h(h_next, lm->ids, B * sizeof(int32_t), s));

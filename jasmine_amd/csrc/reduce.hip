@@ -310,6 +310,96 @@ static jas_status reduce_t(const jas_leaf *in, int op, int axis, void *d_out, hi
     return JAS_OK;
 }
 
+// ---------------- residual update + norm (decode) ----------------
+// x[n] += (sum_s part[s][n] + bias); y[n] = norm(x[n]) * g (+ b).  `part` holds the K-split
+// partial sums of the projection that feeds the residual stream ([split][16][d], split
+// order), so the split-K reduction costs no launch of its own.  One workgroup per token.
+template <int PER, bool RMS>
+__global__ void __launch_bounds__(256)
+resid_norm_kernel(float *__restrict__ x, const float *__restrict__ part, int ks, const float *__restrict__ bias,
+                  const float *__restrict__ g, const float *__restrict__ bta, float *__restrict__ y, int d, float eps,
+                  int y_packed)
+{
+    __shared__ float red[4];
+    const int n = blockIdx.x, t = threadIdx.x;
+    float *xr = x + (long)n * d;
+    float v[PER];
+#pragma unroll
+    for (int k = 0; k < PER / 4; ++k) {
+        const int e = (k * 256 + t) * 4;
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (e < d) {
+            a = *(const float4 *)(xr + e);
+            if (ks > 0) {
+                float4 sacc = *(const float4 *)(part + (long)n * d + e);
+                for (int sp = 1; sp < ks; ++sp) {
+                    float4 q = *(const float4 *)(part + ((long)sp * 16 + n) * d + e);
+                    sacc.x += q.x; sacc.y += q.y; sacc.z += q.z; sacc.w += q.w;
+                }
+                if (bias) {
+                    float4 bb = *(const float4 *)(bias + e);
+                    sacc.x += bb.x; sacc.y += bb.y; sacc.z += bb.z; sacc.w += bb.w;
+                }
+                a.x += sacc.x; a.y += sacc.y; a.z += sacc.z; a.w += sacc.w;
+                *(float4 *)(xr + e) = a;
+            }
+        }
+        v[4 * k] = a.x; v[4 * k + 1] = a.y; v[4 * k + 2] = a.z; v[4 * k + 3] = a.w;
+    }
+    float mean = 0.f;
+    if (!RMS) {
+        float sm = 0.f;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) sm += v[k];
+        mean = block_sum<256>(sm, red) / (float)d;
+    }
+    float s2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const int e = ((k / 4) * 256 + t) * 4;
+        const float dv = e < d ? v[k] - mean : 0.f;
+        s2 += dv * dv;
+    }
+    const float den = sqrtf(block_sum<256>(s2, red) / (float)d + eps);
+#pragma unroll
+    for (int k = 0; k < PER / 4; ++k) {
+        const int e = (k * 256 + t) * 4;
+        if (e >= d) continue;
+        float4 gg = *(const float4 *)(g + e), o;
+        o.x = (v[4 * k] - mean) / den * gg.x;
+        o.y = (v[4 * k + 1] - mean) / den * gg.y;
+        o.z = (v[4 * k + 2] - mean) / den * gg.z;
+        o.w = (v[4 * k + 3] - mean) / den * gg.w;
+        if (!RMS && bta) {
+            float4 bb = *(const float4 *)(bta + e);
+            o.x += bb.x; o.y += bb.y; o.z += bb.z; o.w += bb.w;
+        }
+        // packed: the 4 features e..e+3 of token n are one lane's B-operand float4
+        const long yo = y_packed ? ((long)(e >> 4) * 64 + n + 16 * ((e & 15) >> 2)) * 4 : (long)n * d + e;
+        *(float4 *)(y + yo) = o;
+    }
+}
+
+jas_status resid_norm(float *x, const float *part, int ks, const float *bias, const float *g, const float *b, float *y,
+                      int N, int d, float eps, bool rms, hipStream_t s, bool y_packed)
+{
+    JAS_CHECK(d % 4 == 0 && d <= 8192 && N >= 1 && N <= 16 && g, JAS_ERR_INVALID, "resid_norm: unsupported shape");
+    JAS_CHECK(!y_packed || d % 16 == 0, JAS_ERR_INVALID, "resid_norm: packed output needs d % 16 == 0");
+    const int yp = y_packed ? 1 : 0;
+#define JAS_RN(PER)                                                                                              \
+    if (d <= PER * 256) {                                                                                        \
+        if (rms) hipLaunchKernelGGL((resid_norm_kernel<PER, true>), dim3(N), dim3(256), 0, s, x, part, ks, bias, \
+                                    g, b, y, d, eps, yp);                                                        \
+        else hipLaunchKernelGGL((resid_norm_kernel<PER, false>), dim3(N), dim3(256), 0, s, x, part, ks, bias, g, \
+                                b, y, d, eps, yp);                                                               \
+        JAS_LAUNCH_CHECK();                                                                                      \
+        return JAS_OK;                                                                                           \
+    }
+    JAS_RN(4) JAS_RN(8) JAS_RN(16) JAS_RN(32)
+#undef JAS_RN
+    return fail(JAS_ERR_INVALID, "resid_norm: d too large");
+}
+
 } // namespace jas
 
 using namespace jas;

@@ -114,3 +114,17 @@ def test_lm_errors(jas):
     lm.decode(np.array([1], np.int32))
     with pytest.raises(JasError, match="max_ctx"):  # KV cache capacity (8)
         lm.decode(np.array([1], np.int32))
+
+
+def test_weight_set_get_roundtrip(jas):
+    # projection weights live in the packed MFMA layout on the device; the host view is
+    # always logical row-major [layers][rows][cols]
+    cfg = jas.LmConfig(0, 2, 64, 2, 128, 50, 8, 1, 1e-5, 1e4)  # vocab 50: padded packed rows
+    lm = jas.Lm(cfg)
+    rng = np.random.default_rng(0)
+    for name in ("wte", "w_qkv", "w_fc", "w_proj", "b_qkv", "ln1_g"):
+        l, r, c = lm.weight_shape(name)
+        a = rng.standard_normal(l * r * c).astype(np.float32)
+        lm.set_weight(name, a)
+        assert np.array_equal(lm.weight(name), a), name
+    assert lm.weight_shape("w_gate") == (0, 0, 0)
