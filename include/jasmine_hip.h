@@ -121,6 +121,13 @@ jas_status jas_ew_eval(const jas_ew_ins *prog, int n_ins, const jas_leaf *leaves
 jas_status jas_reduce(const jas_leaf *in, int op, int axis, void *d_out, int32_t out_dtype,
                       jas_stream_t stream);
 
+/* mat_view_t::assign (mat_view_t.hpp:53-63): write the dense row-major [rows, cols] matrix
+ * src (dtype src_dtype) through the view/broadcast mapping of `dst` (element (i, j) of the
+ * view, i < rows, j < cols), converting to dst's dtype.  Where jasmine's modulo mapping
+ * sends several (i, j) to one element, one of them wins (not necessarily the last). */
+jas_status jas_leaf_assign(const void *d_src, int32_t src_dtype, int rows, int cols, const jas_leaf *dst,
+                           jas_stream_t stream);
+
 /* ------------------------------------------------------------------ L2 row ops */
 /* All row ops act on `n_vec` vectors of length `len`; element e of vector v is read from
  * x[v * x_vstride + e * estride] and written to y[v * y_vstride + e * estride] (row-wise:
@@ -131,6 +138,10 @@ jas_status jas_reduce(const jas_leaf *in, int op, int axis, void *d_out, int32_t
  * y = exp(x - max) / sum, one HBM read + one write per vector. */
 jas_status jas_softmax(const float *d_x, float *d_y, int n_vec, int len, long x_vstride, long y_vstride,
                        long estride, jas_stream_t stream);
+/* The causal mask of mat_head_gen_t::forward (mat_mha_t.hpp:58-67): S[i][j] = value for
+ * j > i on a row-major [rows, cols] matrix with leading dimension ld. */
+jas_status jas_causal_mask(float *d_S, int rows, int cols, long ld, float value, jas_stream_t stream);
+jas_status jas_causal_mask_f64(double *d_S, int rows, int cols, long ld, double value, jas_stream_t stream);
 /* whole-matrix softmax mat_softmax_t (mat_express_t.hpp:630-679), dense n floats */
 jas_status jas_softmax_global(const float *d_x, float *d_y, long n, jas_stream_t stream);
 /* LayerNorm: y = (x - mean) / sqrt(var + eps) * g[e] + b[e]  (population variance).
@@ -166,6 +177,14 @@ jas_status jas_gemm(int M, int N, int K,
                     int batch, long a_bstride, long b_bstride, long c_bstride, long bias_bstride,
                     jas_stream_t stream);
 
+/* Same contract in fp64 (mat_dot_t on mat_t<double>), on the fp64 matrix cores
+ * (v_mfma_f64_16x16x4_f64); no activation or accumulate, bias_mode 0/1/2 as above. */
+jas_status jas_gemm_f64(int M, int N, int K,
+                        const double *d_A, long as0, long as1,
+                        const double *d_B, long bs0, long bs1,
+                        double *d_C, long cs0, long cs1,
+                        const double *d_bias, int bias_mode, jas_stream_t stream);
+
 /* ------------------------------------------------------------------ attention */
 /* Causal / full flash attention forward, token-major Q[B,H,Sq,D], K,V[B,H,Sk,D] -> O.
  * Replaces the materialised S = Q'K / sqrt(d) -> mask -> hsoftmax -> V P' sequence of
@@ -192,6 +211,7 @@ jas_status jas_attn_decode(const float *d_q, const float *d_K, const float *d_V,
 /* jasmine RoPE_net_t::forward (mat_RoPE_t.hpp:166-188) with mat_RoPE_t::init angles
  * (mat_RoPE_t.hpp:107-131); x, y row-major [d, T] feature-major. */
 jas_status jas_rope_jasmine(const float *d_x, float *d_y, int d, int T, jas_stream_t stream);
+jas_status jas_rope_jasmine_f64(const double *d_x, double *d_y, int d, int T, jas_stream_t stream);
 /* LLaMA rotary on interleaved pairs, in place: x[(n * nh + h) * hstride ...], n tokens with
  * positions pos[n] (device int32), nh heads of dh each, token stride tstride elements. */
 jas_status jas_rope_llama(float *d_x, const int32_t *d_pos, int n, int nh, int dh, long tstride,

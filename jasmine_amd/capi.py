@@ -55,12 +55,17 @@ _sigs = {
     "jas_reduce": [C.POINTER(Leaf), I, I, VP, C.c_int32, VP],
     "jas_softmax": [VP, VP, I, I, L, L, L, VP],
     "jas_softmax_global": [VP, VP, L, VP],
+    "jas_causal_mask": [VP, I, I, L, C.c_float, VP],
+    "jas_causal_mask_f64": [VP, I, I, L, C.c_double, VP],
+    "jas_leaf_assign": [VP, C.c_int32, I, I, C.POINTER(Leaf), VP],
     "jas_layernorm": [VP, VP, I, I, L, L, L, C.c_float, VP, VP, VP],
     "jas_rmsnorm": [VP, VP, I, I, L, L, L, C.c_float, VP, VP],
     "jas_gemm": [I, I, I, VP, L, L, VP, L, L, VP, L, L, VP, I, I, I, I, L, L, L, L, VP],
+    "jas_gemm_f64": [I, I, I, VP, L, L, VP, L, L, VP, L, L, VP, I, VP],
     "jas_attn_prefill": [VP, VP, VP, VP, I, I, I, I, I, L, L, L, L, L, L, L, L, L, C.c_float, I, I, VP],
     "jas_attn_decode": [VP, VP, VP, VP, VP, I, I, I, I, L, L, C.c_float, VP, VP],
     "jas_rope_jasmine": [VP, VP, I, I, VP],
+    "jas_rope_jasmine_f64": [VP, VP, I, I, VP],
     "jas_rope_llama": [VP, VP, I, I, I, L, C.c_float, VP],
     "jas_embed": [VP, VP, VP, VP, VP, I, I, VP],
     "jas_argmax": [VP, I, I, L, VP, VP],

@@ -191,9 +191,45 @@ __global__ void __launch_bounds__(256) ew_eval_kernel(const EwArgs A)
     }
 }
 
+__device__ __forceinline__ void store_elem(void *p, long idx, int dtype, double v)
+{
+    switch (dtype) {
+    case JAS_F64: ((double *)p)[idx] = v; break;
+    case JAS_I32: ((int32_t *)p)[idx] = (int32_t)v; break;
+    default: ((float *)p)[idx] = (float)v; break;
+    }
+}
+
+__global__ void leaf_assign_kernel(const void *src, int src_dtype, int rows, int cols, LeafDev L)
+{
+    long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= (long)rows * cols) return;
+    int i = (int)(g / cols), j = (int)(g % cols);
+    store_elem((void *)L.p, leaf_index(L, i, j), L.dtype, load_elem(src, g, src_dtype));
+}
+
 } // namespace jas
 
 using namespace jas;
+
+extern "C" jas_status jas_leaf_assign(const void *src, int32_t src_dtype, int rows, int cols, const jas_leaf *dst,
+                                      jas_stream_t stream)
+{
+    JAS_CHECK(src && dst && dst->d_data && rows >= 0 && cols >= 0, JAS_ERR_INVALID, "jas_leaf_assign: bad arguments");
+    JAS_CHECK(dst->rows > 0 && dst->cols > 0, JAS_ERR_INVALID, "jas_leaf_assign: empty destination");
+    if (!rows || !cols) return JAS_OK;
+    LeafDev L = classify(*dst, rows, cols);
+    if (L.kind == LK_CONTIG) {
+        L.kind = LK_STRIDED;
+        L.rs = cols;
+        L.cs = 1;
+    }
+    long n = (long)rows * cols;
+    hipLaunchKernelGGL(leaf_assign_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, stream_or_default(stream), src,
+                       src_dtype, rows, cols, L);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
 
 extern "C" jas_status jas_ew_eval(const jas_ew_ins *prog, int n_ins, const jas_leaf *leaves, int n_leaves,
                                   void *d_out, int32_t out_dtype, int rows, int cols, jas_stream_t stream)

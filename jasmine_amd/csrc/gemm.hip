@@ -552,9 +552,78 @@ jas_status fill_normal_packed(float *x, int M, int K, uint64_t seed, uint64_t st
     return JAS_OK;
 }
 
+// ---------------------------------------------------------------- fp64 GEMM
+// 64x64 tile, K step 8, 256 threads (4 waves as 2x2 of 32x32): v_mfma_f64_16x16x4_f64 with
+// A[i = l%16][k = l/16], B[k = l/16][j = l%16], D (one double per lane per 4 rows):
+// rows 4*(l/16) + r, column l%16 for r = 0..3 across the four result registers.
+typedef double doublex4 __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(256)
+gemm_f64_kernel(int M, int N, int K, const double *__restrict__ A, long as0, long as1, const double *__restrict__ B,
+                long bs0, long bs1, double *__restrict__ C, long cs0, long cs1, const double *__restrict__ bias,
+                int bias_mode)
+{
+    __shared__ double As[64][9];
+    __shared__ double Bs[64][9];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g = lane >> 4;
+    const int wm = w >> 1, wn = w & 1;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    doublex4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = doublex4{0.0, 0.0, 0.0, 0.0};
+    for (int k0 = 0; k0 < K; k0 += 8) {
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {  // 64 x 8 tiles of A and B, 512 elements each
+            int idx = tid + q * 256, o = idx >> 3, k = idx & 7;
+            int gm = m0 + o, gn = n0 + o, gk = k0 + k;
+            As[o][k] = (gm < M && gk < K) ? A[(long)gm * as0 + (long)gk * as1] : 0.0;
+            Bs[o][k] = (gn < N && gk < K) ? B[(long)gk * bs0 + (long)gn * bs1] : 0.0;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 8; kk += 4)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(As[wm * 32 + i * 16 + r16][kk + g],
+                                                                     Bs[wn * 32 + j * 16 + r16][kk + g], acc[i][j], 0,
+                                                                     0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                int m = m0 + wm * 32 + i * 16 + 4 * g + r, n = n0 + wn * 32 + j * 16 + r16;
+                if (m >= M || n >= N) continue;
+                double v = acc[i][j][r];
+                if (bias_mode == 1) v = v + bias[m];
+                else if (bias_mode == 2) v = v + bias[n];
+                C[(long)m * cs0 + (long)n * cs1] = v;
+            }
+}
+
 } // namespace jas
 
 using namespace jas;
+
+extern "C" jas_status jas_gemm_f64(int M, int N, int K, const double *A, long as0, long as1, const double *B, long bs0,
+                                   long bs1, double *C, long cs0, long cs1, const double *bias, int bias_mode,
+                                   jas_stream_t stream)
+{
+    JAS_CHECK(M >= 0 && N >= 0 && K >= 0 && A && B && C, JAS_ERR_INVALID, "jas_gemm_f64: bad arguments");
+    JAS_CHECK(bias_mode >= 0 && bias_mode <= 2 && (bias_mode == 0 || bias), JAS_ERR_INVALID, "jas_gemm_f64: bad bias");
+    if (M == 0 || N == 0) return JAS_OK;
+    hipLaunchKernelGGL(gemm_f64_kernel, dim3(ceil_div(N, 64), ceil_div(M, 64)), dim3(256), 0, stream_or_default(stream),
+                       M, N, K, A, as0, as1, B, bs0, bs1, C, cs0, cs1, bias, bias_mode);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
 
 extern "C" jas_status jas_gemm(int M, int N, int K, const float *A, long as0, long as1, const float *B, long bs0,
                                long bs1, float *C, long cs0, long cs1, const float *bias, int bias_mode, int act,

@@ -8,37 +8,54 @@ namespace jas {
 // mat_RoPE_t::init cache entry (mat_RoPE_t.hpp:107-131) for val_type float:
 // angle = (float)(c / pow(10000.0, (float)(r/2) / (float)d)); cos where r, c have equal
 // parity, -sin at (even, odd), sin at (odd, even).
-__device__ __forceinline__ float rope_jas_entry(int r, int c, int d)
+template <typename T>
+__device__ __forceinline__ T rope_jas_entry(int r, int c, int d)
 {
-    float e = (float)(r / 2) / (float)d;
-    float angle = (float)((double)c / pow(10000.0, (double)e));
-    if ((r & 1) == (c & 1)) return cosf(angle);
-    return (r & 1) ? sinf(angle) : -sinf(angle);
+    // (i / 2) / static_cast<val_type>(m_d) and the angle are val_type; pow is double
+    T e = (T)(r / 2) / (T)d;
+    T angle = (T)((double)c / pow(10000.0, (double)e));
+    if ((r & 1) == (c & 1)) return cos(angle);
+    return (r & 1) ? sin(angle) : -sin(angle);
 }
 
 // RoPE_net_t::forward (mat_RoPE_t.hpp:166-188): y[2i+r, m] = sum_c block(r, c) x[2i+c, m],
 // a float dot of two terms accumulated from 0 (no fused multiply-add).
-__global__ void rope_jas_kernel(const float *__restrict__ x, float *__restrict__ y, int d, int T)
+template <typename V>
+__global__ void rope_jas_kernel(const V *__restrict__ x, V *__restrict__ y, int d, int T)
 {
 #pragma clang fp contract(off)
     long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
     int half = d / 2;
     if (g >= (long)half * T) return;
     int i = (int)(g / T), m = (int)(g % T);
-    float x0 = x[(long)(2 * i) * T + m], x1 = x[(long)(2 * i + 1) * T + m];
+    V x0 = x[(long)(2 * i) * T + m], x1 = x[(long)(2 * i + 1) * T + m];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-        float s = 0.0f;
-        s = s + rope_jas_entry(2 * i + r, 2 * m, d) * x0;
-        s = s + rope_jas_entry(2 * i + r, 2 * m + 1, d) * x1;
+        V s = (V)0;
+        s = s + rope_jas_entry<V>(2 * i + r, 2 * m, d) * x0;
+        s = s + rope_jas_entry<V>(2 * i + r, 2 * m + 1, d) * x1;
         y[(long)(2 * i + r) * T + m] = s;
     }
 }
 
-__global__ void zero_row_kernel(float *y, int T)
+template <typename V>
+__global__ void zero_row_kernel(V *y, int T)
 {
     int m = blockIdx.x * blockDim.x + threadIdx.x;
-    if (m < T) y[m] = 0.0f;
+    if (m < T) y[m] = (V)0;
+}
+
+template <typename V>
+static jas_status rope_jas(const V *x, V *y, int d, int T, jas_stream_t stream)
+{
+    JAS_CHECK(x && y && d > 0 && T > 0, JAS_ERR_INVALID, "jas_rope_jasmine: bad arguments");
+    hipStream_t s = stream_or_default(stream);
+    long n = (long)(d / 2) * T;
+    if (n) hipLaunchKernelGGL(rope_jas_kernel<V>, dim3(ceil_div(n, 256)), dim3(256), 0, s, x, y, d, T);
+    if (d & 1)  // the odd trailing row of the zero-initialised result stays 0 (mat_RoPE_t.hpp:176-186)
+        hipLaunchKernelGGL(zero_row_kernel<V>, dim3(ceil_div(T, 256)), dim3(256), 0, s, y + (long)(d - 1) * T, T);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
 }
 
 // LLaMA rotary, interleaved pairs, angles in double (positions reach thousands of radians)
@@ -121,14 +138,12 @@ extern "C" {
 
 jas_status jas_rope_jasmine(const float *x, float *y, int d, int T, jas_stream_t stream)
 {
-    JAS_CHECK(x && y && d > 0 && T > 0, JAS_ERR_INVALID, "jas_rope_jasmine: bad arguments");
-    hipStream_t s = stream_or_default(stream);
-    long n = (long)(d / 2) * T;
-    if (n) hipLaunchKernelGGL(rope_jas_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, s, x, y, d, T);
-    if (d & 1)  // the odd trailing row of the zero-initialised result stays 0 (mat_RoPE_t.hpp:176-186)
-        hipLaunchKernelGGL(zero_row_kernel, dim3(ceil_div(T, 256)), dim3(256), 0, s, y + (long)(d - 1) * T, T);
-    JAS_LAUNCH_CHECK();
-    return JAS_OK;
+    return rope_jas<float>(x, y, d, T, stream);
+}
+
+jas_status jas_rope_jasmine_f64(const double *x, double *y, int d, int T, jas_stream_t stream)
+{
+    return rope_jas<double>(x, y, d, T, stream);
 }
 
 jas_status jas_rope_llama(float *x, const int32_t *pos, int n, int nh, int dh, long tstride, float theta,

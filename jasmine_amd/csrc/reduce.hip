@@ -142,6 +142,7 @@ __global__ void __launch_bounds__(256)
 rowop_col_kernel(const float *__restrict__ x, float *__restrict__ y, int n_vec, int len, long vstride, long ystride, long estride,
                  float eps, const float *__restrict__ g, const float *__restrict__ bta)
 {
+#pragma clang fp contract(off)  // same float roundings as jasmine's sequential column loops
     int v = blockIdx.x * blockDim.x + threadIdx.x;
     if (v >= n_vec) return;
     const float *xr = x + (long)v * vstride;
@@ -400,11 +401,40 @@ jas_status resid_norm(float *x, const float *part, int ks, const float *bias, co
     return fail(JAS_ERR_INVALID, "resid_norm: d too large");
 }
 
+template <typename T>
+__global__ void causal_mask_kernel(T *S, int rows, int cols, long ld, T value)
+{
+    long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= (long)rows * cols) return;
+    int i = (int)(g / cols), j = (int)(g % cols);
+    if (j > i) S[(long)i * ld + j] = value;
+}
+
 } // namespace jas
 
 using namespace jas;
 
 extern "C" {
+
+jas_status jas_causal_mask(float *S, int rows, int cols, long ld, float value, jas_stream_t stream)
+{
+    JAS_CHECK(S && rows >= 0 && cols >= 0 && ld >= cols, JAS_ERR_INVALID, "jas_causal_mask: bad arguments");
+    long n = (long)rows * cols;
+    if (n) hipLaunchKernelGGL(causal_mask_kernel<float>, dim3(ceil_div(n, 256)), dim3(256), 0, stream_or_default(stream),
+                              S, rows, cols, ld, value);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
+jas_status jas_causal_mask_f64(double *S, int rows, int cols, long ld, double value, jas_stream_t stream)
+{
+    JAS_CHECK(S && rows >= 0 && cols >= 0 && ld >= cols, JAS_ERR_INVALID, "jas_causal_mask: bad arguments");
+    long n = (long)rows * cols;
+    if (n) hipLaunchKernelGGL(causal_mask_kernel<double>, dim3(ceil_div(n, 256)), dim3(256), 0,
+                              stream_or_default(stream), S, rows, cols, ld, value);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
 
 jas_status jas_softmax(const float *x, float *y, int n_vec, int len, long vstride, long ystride, long estride,
                        jas_stream_t s)

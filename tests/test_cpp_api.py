@@ -1,0 +1,199 @@
+"""The C++20 jasmine-compatible API (jasmine_amd/include) against the reference's outputs.
+
+tests/cpp/api_driver.cpp is written as jasmine user code (mat_t, views, expressions, nets,
+mat_mha_t, transformer_base_t, weights through an init_t<> hook) and compiled against this
+project's headers into tests/cpp/libjasapi.so.  Each api_X entry point gets the inputs the
+reference's ref_X call got when tests/golden/jasmine_golden.npz was written, so these tests
+compare the device path of the C++ API with the reference's own outputs.
+
+Tolerance (fp32): |api - ref| <= 1e-3 + 1e-4 |ref|; elementwise +-*/ trees and per-row /
+per-column reductions are also checked bit-exact, as their arithmetic order is jasmine's.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from oracle_lib import fp, ip
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "cpp", "libjasapi.so")
+GOLD = os.path.join(HERE, "golden", "jasmine_golden.npz")
+
+
+def load_api():
+    if not os.path.exists(LIB):
+        raise RuntimeError(f"{LIB} is not built (make -C tests/cpp, or __graft_entry__.build())")
+    lib = ctypes.CDLL(LIB)
+    lib.api_last_error.restype = ctypes.c_char_p
+    lib.api_transformer_nparams.restype = ctypes.c_long
+    return lib
+
+
+@pytest.fixture(scope="module")
+def api():
+    return load_api()
+
+
+@pytest.fixture(scope="module")
+def g():
+    return np.load(GOLD)
+
+
+def ok(lib, rc):
+    assert rc == 0, lib.api_last_error().decode()
+
+
+def close(a, b, atol=1e-3, rtol=1e-4):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    assert np.all(np.isfinite(a) == np.isfinite(b)), "non-finite mismatch"
+    fin = np.isfinite(b)
+    err = np.abs(a - b)[fin]
+    assert np.all(err <= atol + rtol * np.abs(b)[fin]), f"max abs err {err.max():.3g}"
+
+
+def bitexact(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+# ------------------------------------------------------------------ CPU (no device calls)
+def test_api_library_exports(api):
+    for name in ("api_gemm", "api_gemm_tn", "api_cfg2_expr", "api_expr", "api_hsoftmax", "api_softmax_global",
+                 "api_reductions", "api_linear", "api_relu", "api_sigmoid", "api_layernorm_cols", "api_head",
+                 "api_mha", "api_rope", "api_transformer", "api_transformer_nparams", "api_last_error"):
+        assert hasattr(api, name), name
+
+
+@pytest.mark.parametrize("d,H,ne,nd", [(12, 3, 2, 2), (8, 2, 1, 3), (16, 4, 3, 1)])
+def test_api_transformer_parameter_walk(api, d, H, ne, nd):
+    """init_weight visits what the reference visits: per head Wq,bq,Wk,bk,Wv,bv (dh x dh + dh)
+    and the output projection (d x d + d) per attention block, then the FFN weight (d x d + d);
+    the encoder layer has one attention block, the decoder layer two.  layer_norm_net_t
+    creates gamma/beta at its first forward (mat_net_t.hpp:209-224), so no LN parameter is
+    visited."""
+    dh = d // H
+    mha = 3 * H * (dh * dh + dh) + d * d + d
+    ffn = d * d + d
+    want = ne * (mha + ffn) + nd * (2 * mha + ffn)
+    assert api.api_transformer_nparams(d, H, ne, nd) == want
+    if "_ref" in os.listdir(os.path.join(os.path.dirname(HERE), "oracle")):
+        from oracle_lib import ref
+        if ref is not None:
+            assert ref.ref_transformer_nparams(d, H, ne, nd) == want
+
+
+# ------------------------------------------------------------------ GPU parity
+@pytest.mark.gpu
+def test_api_expressions(api, g):
+    n = 0
+    while f"expr{n}_id" in g:
+        eid = int(g[f"expr{n}_id"])
+        a, b, want = g[f"expr{n}_a"], g[f"expr{n}_b"], g[f"expr{n}_out"]
+        r, c = np.zeros(1, np.int32), np.zeros(1, np.int32)
+        out = np.zeros(want.shape, np.float32)
+        ok(api, api.api_expr(eid, fp(a), a.shape[0], a.shape[1], fp(b), b.shape[0], b.shape[1], fp(out), ip(r), ip(c)))
+        assert (r[0], c[0]) == want.shape
+        close(out, want)
+        if eid not in (3, 4):  # exp / sigmoid go through libm-class functions
+            assert bitexact(out, want), (n, eid)
+        n += 1
+    assert n >= 13
+
+
+@pytest.mark.gpu
+def test_api_cfg2_expression(api, g):
+    a, b, c, want = g["cfg2_a"], g["cfg2_b"], g["cfg2_c"], g["cfg2_d"]
+    d = np.zeros_like(a)
+    ok(api, api.api_cfg2_expr(fp(a), fp(b), fp(c), fp(d), a.shape[0], a.shape[1]))
+    close(d, want)
+
+
+@pytest.mark.gpu
+def test_api_row_and_column_ops(api, g):
+    x = g["x"]
+    R, C = x.shape
+    for fn, key in ((api.api_hsoftmax, "hsoftmax"), (api.api_softmax_global, "softmax_global"),
+                    (api.api_layernorm_cols, "layernorm_cols"), (api.api_relu, "relu"),
+                    (api.api_sigmoid, "sigmoid")):
+        y = np.zeros_like(x)
+        ok(api, fn(fp(x), R, C, fp(y)))
+        close(y, g[key], atol=1e-5, rtol=1e-5)
+    y = np.zeros_like(x)
+    ok(api, api.api_relu(fp(x), R, C, fp(y)))
+    assert bitexact(y, g["relu"])
+
+
+@pytest.mark.gpu
+def test_api_reductions(api, g):
+    x = g["x"]
+    R, C = x.shape
+    hs, vs, hm, vmn, hmn = (np.zeros(k, np.float32) for k in (R, C, R, C, R))
+    sc = np.zeros(3, np.float32)
+    ok(api, api.api_reductions(fp(x), R, C, fp(hs), fp(vs), fp(hm), fp(vmn), fp(hmn), fp(sc)))
+    for got, key in ((hs, "hsum"), (vs, "vsum"), (hm, "hmax"), (vmn, "vmean"), (hmn, "hmean")):
+        assert bitexact(got, g[key].reshape(got.shape)), key
+    close(sc, g["sum_max_mean"], atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.gpu
+def test_api_gemm_and_linear(api, g):
+    A, B, want = g["gemm_a"], g["gemm_b"], g["gemm_c"]
+    M, K = A.shape
+    N = B.shape[1]
+    C = np.zeros((M, N), np.float32)
+    ok(api, api.api_gemm(M, N, K, fp(A), fp(B), fp(C)))
+    close(C, want, atol=1e-5, rtol=1e-5)
+    At = np.ascontiguousarray(A.T)
+    ok(api, api.api_gemm_tn(M, N, K, fp(At), fp(B), fp(C)))
+    close(C, want, atol=1e-5, rtol=1e-5)
+    W, b, X, want = g["linear_w"], g["linear_b"], g["linear_x"], g["linear_y"]
+    Y = np.zeros_like(want)
+    ok(api, api.api_linear(fp(W), fp(b), fp(X), W.shape[0], W.shape[1], X.shape[1], fp(Y)))
+    close(Y, want, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.gpu
+def test_api_head(api, g):
+    Wh, Xq, Xk = g["head_w"], g["head_xq"], g["head_xk"]
+    dh, T = Xq.shape
+    Tk = Xk.shape[1]
+    for mask in (0, 1):
+        Y = np.zeros((dh, T), np.float32)
+        ok(api, api.api_head(fp(Xq), None, dh, T, T, fp(Wh), mask, fp(Y)))
+        close(Y, g[f"head_self_m{mask}"])
+    Y = np.zeros((dh, T), np.float32)
+    ok(api, api.api_head(fp(Xq), fp(Xk), dh, T, Tk, fp(Wh), 0, fp(Y)))
+    close(Y, g["head_cross"])
+
+
+@pytest.mark.gpu
+def test_api_mha(api, g):
+    Wm, Xm, want = g["mha_w"], g["mha_x"], g["mha_y"]
+    d, T = Xm.shape
+    Y = np.zeros_like(want)
+    ok(api, api.api_mha(fp(Xm), None, d, 3, T, T, fp(Wm), 1, fp(Y)))
+    close(Y, want)
+
+
+@pytest.mark.gpu
+def test_api_rope(api, g):
+    X, want = g["rope_x"], g["rope_y"]
+    Y = np.zeros_like(X)
+    ok(api, api.api_rope(fp(X), X.shape[0], X.shape[1], fp(Y)))
+    close(Y, want, atol=1e-6, rtol=1e-5)
+
+
+@pytest.mark.gpu
+def test_api_transformer(api, g):
+    d, H, ne, nd, Te, Td = (int(v) for v in g["tf_dims"])
+    Wt, en, de = g["tf_w"], g["tf_en"], g["tf_de"]
+    Y = np.zeros((d, Td), np.float32)
+    ok(api, api.api_transformer(fp(en), Te, fp(de), Td, d, H, ne, nd, fp(Wt), fp(Y)))
+    close(Y, g["tf_y"])
+    # causal prefix: the first 3 decoder columns alone give the reference's 3-token output
+    Yp = np.zeros((d, 3), np.float32)
+    ok(api, api.api_transformer(fp(en), Te, fp(np.ascontiguousarray(de[:, :3])), 3, d, H, ne, nd, fp(Wt), fp(Yp)))
+    close(Yp, g["tf_prefix3"])
+    close(Y[:, :3], Yp)
