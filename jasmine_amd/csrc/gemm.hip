@@ -554,8 +554,8 @@ jas_status fill_normal_packed(float *x, int M, int K, uint64_t seed, uint64_t st
 
 // ---------------------------------------------------------------- fp64 GEMM
 // 64x64 tile, K step 8, 256 threads (4 waves as 2x2 of 32x32): v_mfma_f64_16x16x4_f64 with
-// A[i = l%16][k = l/16], B[k = l/16][j = l%16], D (one double per lane per 4 rows):
-// rows 4*(l/16) + r, column l%16 for r = 0..3 across the four result registers.
+// A[i = l%16][k = l/16], B[k = l/16][j = l%16]; result register r of lane l holds
+// D[i = l/16 + 4r][j = l%16] (the fp64 form interleaves rows, unlike the fp32 16x16x4).
 typedef double doublex4 __attribute__((ext_vector_type(4)));
 
 __global__ void __launch_bounds__(256)
@@ -599,7 +599,7 @@ gemm_f64_kernel(int M, int N, int K, const double *__restrict__ A, long as0, lon
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                int m = m0 + wm * 32 + i * 16 + 4 * g + r, n = n0 + wn * 32 + j * 16 + r16;
+                int m = m0 + wm * 32 + i * 16 + g + 4 * r, n = n0 + wn * 32 + j * 16 + r16;
                 if (m >= M || n >= N) continue;
                 double v = acc[i][j][r];
                 if (bias_mode == 1) v = v + bias[m];

@@ -344,3 +344,59 @@ def test_embed_argmax_fill(jas):
     dn = jas.DeviceArray(100003)
     jas.check(jas.lib.jas_fill_normal(dn.p, 100003, 9, 3, 0.0, 0.02, None))
     close(dn.numpy(), normal(100003, 9, 3, std=0.02), atol=1e-7, rtol=1e-6)
+
+
+# ---------------------------------------------------------------- API support kernels
+def test_leaf_assign_block_and_convert(jas):
+    dst = np.zeros((7, 9), np.float32)
+    dd = jas.to_device(dst)
+    src = normal((3, 4), 5, 1).astype(np.float64)
+    ds = jas.to_device(src)
+    lf = jas.leaf(dd, roff=2, coff=3, vrows=3, vcols=4)
+    jas.check(jas.lib.jas_leaf_assign(ds.p, 1,  # JAS_F64
+                                           3, 4, __import__("ctypes").byref(lf), None))
+    want = dst.copy()
+    want[2:5, 3:7] = src.astype(np.float32)
+    assert np.array_equal(dd.numpy(), want)
+
+
+def test_causal_mask(jas):
+    for dt, fn in ((np.float32, jas.lib.jas_causal_mask), (np.float64, jas.lib.jas_causal_mask_f64)):
+        s = normal((6, 9), 5, 2).astype(dt)
+        d = jas.to_device(s)
+        ninf = __import__("ctypes").c_float(-np.inf) if dt == np.float32 else __import__("ctypes").c_double(-np.inf)
+        jas.check(fn(d.p, 5, 8, 9, ninf, None))  # 5 x 8 block of a 6 x 9 matrix, ld 9
+        want = s.copy()
+        for i in range(5):
+            want[i, i + 1:8] = -np.inf
+        assert np.array_equal(d.numpy(), want)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (17, 9, 33), (64, 80, 100), (130, 7, 257)])
+def test_gemm_f64(jas, M, N, K):
+    A, B = normal((M, K), 6, 1).astype(np.float64), normal((K, N), 6, 2).astype(np.float64)
+    bias = normal(M, 6, 3).astype(np.float64)
+    dA, dB, dbias, dC = jas.to_device(A), jas.to_device(B), jas.to_device(bias), jas.DeviceArray((M, N), np.float64)
+    jas.check(jas.lib.jas_gemm_f64(M, N, K, dA.p, K, 1, dB.p, N, 1, dC.p, N, 1, dbias.p, 1, None))
+    want = A @ B + bias[:, None]
+    assert np.max(np.abs(dC.numpy() - want)) <= 1e-12 * (1 + np.max(np.abs(want))) * np.sqrt(K)
+
+
+def test_rope_jasmine_f64(jas):
+    d, T = 10, 7
+    x = normal((d, T), 6, 4).astype(np.float64)
+    dx, dy = jas.to_device(x), jas.DeviceArray((d, T), np.float64)
+    jas.check(jas.lib.jas_rope_jasmine_f64(dx.p, dy.p, d, T, None))
+
+    def entry(r, c):  # mat_RoPE_t::init in double (mat_RoPE_t.hpp:99-134)
+        a = c / 10000.0 ** ((r // 2) / float(d))
+        if r % 2 == c % 2:
+            return np.cos(a)
+        return -np.sin(a) if r % 2 == 0 else np.sin(a)
+
+    want = np.zeros_like(x)
+    for m in range(T):
+        for i in range(d // 2):
+            for r in range(2):
+                want[2 * i + r, m] = entry(2 * i + r, 2 * m) * x[2 * i, m] + entry(2 * i + r, 2 * m + 1) * x[2 * i + 1, m]
+    assert np.max(np.abs(dy.numpy() - want)) <= 1e-13
