@@ -29,6 +29,7 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, datasheet
 FP32_MFMA_TFLOPS = 157.3   # MI355X dense fp32 matrix, datasheet
+BF16_MFMA_TFLOPS = 2500.0  # MI355X dense bf16 matrix, datasheet
 
 
 def log(*a):
@@ -98,6 +99,88 @@ def run_gpt2(jas, steps=32, warmup=4):
     return B * steps / dt, 1e3 * dt / steps
 
 
+def run_kernel_legs(jas, reps=10):
+    """Configs 2 and 3 as per-kernel lines: HIP events on the library stream around `reps`
+    back-to-back launches of each kernel at the config's full shape (inputs resident)."""
+    import ctypes as C
+    import numpy as np
+    from jasmine_amd import expr as E
+    from jasmine_amd.timing import time_launches
+    lib, chk = jas.lib, jas.check
+    out = {}
+
+    # config 2: 8192 x 8192 fp32, A, B, C ~ N(0, 1) from seed 1
+    R = Cc = 8192
+    n = R * Cc
+    A, Bm, Cm = (jas.DeviceArray((R, Cc)) for _ in range(3))
+    for k, m in enumerate((A, Bm, Cm)):
+        chk(lib.jas_fill_normal(m.p, n, 1, k, 0.0, 1.0, None))
+    D, Y = jas.DeviceArray((R, Cc)), jas.DeviceArray((R, Cc))
+    tree = E.leaf(A) * E.leaf(Bm) + 0.5 * E.leaf(Cm) - E.un("tanh", E.leaf(A))
+    prog, leaves = E.lower(tree)
+    from jasmine_amd.capi import Ins, Leaf
+    pa = (Ins * len(prog))(*[Ins(o, d, a, 0, i) for o, d, a, i in prog])
+    la = (Leaf * len(leaves))(*leaves)
+    mb = n * 4
+
+    def line(name, ms, bytes_, bound="hbm", flops=None, peak=None):
+        if bound == "hbm":
+            ach = bytes_ / (ms * 1e-3) / 1e9
+            return {"kernel": name, "avg_launch_us": round(ms * 1e3, 2), "bound": "hbm", "bytes": bytes_,
+                    "achieved": round(ach, 1), "unit": "GB/s", "peak": HBM_PEAK_GBS, "frac": round(ach / HBM_PEAK_GBS, 4)}
+        ach = flops / (ms * 1e-3) / 1e12
+        return {"kernel": name, "avg_launch_us": round(ms * 1e3, 2), "bound": "mfma", "flops": flops,
+                "achieved": round(ach, 2), "unit": "TFLOP/s", "peak": peak, "frac": round(ach / peak, 4)}
+
+    ms = time_launches(lambda: chk(lib.jas_ew_eval(pa, len(prog), la, len(leaves), D.p, 0, R, Cc, None)), reps)
+    out["ew_cfg2"] = line("ew_eval_kernel: D = A*B + 0.5*C - tanh(A), 8192^2 fp32 (3 reads + 1 write)", ms, 4 * mb)
+    ms = time_launches(lambda: chk(lib.jas_softmax(D.p, Y.p, R, Cc, Cc, Cc, 1, None)), reps)
+    out["softmax_rows"] = line("row softmax, 8192 rows of 8192", ms, 2 * mb)
+    ms = time_launches(lambda: chk(lib.jas_layernorm(D.p, Y.p, R, Cc, Cc, Cc, 1, C.c_float(1e-5), None, None, None)),
+                       reps)
+    out["layernorm_rows"] = line("row LayerNorm eps 1e-5, 8192 rows of 8192", ms, 2 * mb)
+    ms = time_launches(lambda: chk(lib.jas_rmsnorm(D.p, Y.p, R, Cc, Cc, Cc, 1, C.c_float(1e-6), None, None)), reps)
+    out["rmsnorm_rows"] = line("row RMSNorm eps 1e-6, 8192 rows of 8192", ms, 2 * mb)
+    del A, Bm, Cm, D, Y
+
+    # config 3: causal attention B=8, H=12, S=1024, D=64, Q, K, V ~ N(0, 1) from seed 2
+    Bb, H, S, Dh = 8, 12, 1024, 64
+    shape, ne = (Bb, H, S, Dh), Bb * H * S * Dh
+    Q, K, V, O = (jas.DeviceArray(shape) for _ in range(4))
+    for k, m in enumerate((Q, K, V)):
+        chk(lib.jas_fill_normal(m.p, ne, 2, k, 0.0, 1.0, None))
+    st = (H * S * Dh, S * Dh, Dh)
+    causal_flops = 4.0 * Bb * H * S * S * Dh / 2
+
+    def prefill(q, k, v, o, dt):
+        chk(lib.jas_attn_prefill(q.p, k.p, v.p, o.p, Bb, H, S, S, Dh, *st, *st, *st, C.c_float(0.125), 1, dt, None))
+
+    ms = time_launches(lambda: prefill(Q, K, V, O, 0), reps)
+    out["attn_prefill_f32"] = line("flash_prefill_kernel<64> fp32 causal, B8 H12 S1024 D64", ms, None, "mfma",
+                                   causal_flops, FP32_MFMA_TFLOPS)
+
+    def bf(x):
+        u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    Qb, Kb, Vb = (jas.to_device(bf(m.numpy())) for m in (Q, K, V))
+    Ob = jas.DeviceArray(shape, np.uint16)
+    ms = time_launches(lambda: prefill(Qb, Kb, Vb, Ob, 3), reps)
+    out["attn_prefill_bf16"] = line("flash_prefill_kernel<64> bf16 in / fp32 accumulate, causal, same shape", ms, None,
+                                    "mfma", causal_flops, BF16_MFMA_TFLOPS)
+    del Qb, Kb, Vb, Ob
+
+    q = jas.DeviceArray((Bb, H, Dh))
+    chk(lib.jas_fill_normal(q.p, Bb * H * Dh, 2, 3, 0.0, 1.0, None))
+    o = jas.DeviceArray((Bb, H, Dh))
+    lens = jas.to_device(np.full(Bb, S, np.int32))
+    ws = jas.DeviceArray(max(lib.jas_attn_decode_workspace(Bb, H, Dh, S) // 4, 1))
+    ms = time_launches(lambda: chk(lib.jas_attn_decode(q.p, K.p, V.p, o.p, lens.p, Bb, H, Dh, S, st[0], st[1],
+                                                       C.c_float(0.125), ws.p, None)), reps * 5)
+    out["attn_decode_f32"] = line("attn_decode_kernel<64> + merge, 1 query over 1024 cached keys, B8 H12",
+                                  ms, 2 * ne * 4)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -107,6 +190,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--no-gpt2", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the config 2/3 kernel lines")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
@@ -119,6 +203,12 @@ def main():
 
     os.environ.setdefault("JAS_VERBOSE", "1")
     jas.check(jas.lib.jas_init(0))
+    kernels = None
+    if not args.no_kernels:
+        log("[bench] config 2/3 kernel lines")
+        kernels = run_kernel_legs(jas)
+        for k, v in kernels.items():
+            log(f"[bench]   {k}: {v['avg_launch_us']} us, {v['achieved']} {v['unit']} ({100 * v['frac']:.1f}% of peak)")
     B, P = args.batch, args.prompt
     L, d, H, F, V = 32, 4096, 32, 11008, 32000
     dh = d // H
@@ -216,6 +306,7 @@ def main():
         "prefill_tok_s": round(B * P / prefill_s, 1),
         "cpu_baseline": cpu,
         "gpt2_small": gpt2,
+        "kernels": kernels,
     }
     print(json.dumps(line), flush=True)
 

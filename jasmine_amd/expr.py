@@ -1,4 +1,4 @@
-"""Host-side lowering of jasmine expression trees to the jas_ew_eval postfix program.
+"""Host-side lowering of jasmine expression trees to the jas_ew_eval postfix program (Python mirror).
 
 Mirrors what the C++ header API does at a tree's evaluation point (clone / operator
 mat_t): node ele_types follow std::common_type over double > float > int

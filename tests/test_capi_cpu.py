@@ -52,7 +52,7 @@ def test_library_has_no_oracle_dependency():
 
 def test_lowering_stack_bound():
     # Sethi-Ullman ordering keeps a balanced 8-leaf tree within the 4-slot device stack
-    import ewexpr as E
+    from jasmine_amd import expr as E
 
     class FakeLeaf:
         vrows, vcols = 4, 4

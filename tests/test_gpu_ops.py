@@ -10,7 +10,7 @@ import math
 import numpy as np
 import pytest
 
-import ewexpr as E
+from jasmine_amd import expr as E
 from oracle_lib import orc, fp, normal
 
 pytestmark = pytest.mark.gpu
