@@ -115,6 +115,13 @@ typedef struct {
 jas_status jas_ew_eval(const jas_ew_ins *prog, int n_ins, const jas_leaf *leaves, int n_leaves,
                        void *d_out, int32_t out_dtype, int rows, int cols, jas_stream_t stream);
 
+/* How jas_ew_eval runs a program (no counterpart in the reference; a tuning switch):
+ * 0 = always the interpreter kernel, 1 = always a kernel specialised to the program
+ * (compiled once per program shape with hipRTC, cached for the process), 2 = specialise
+ * outputs of at least 2^20 elements (default).  Returns the previous mode; other values
+ * only query it.  Both paths give identical results. */
+int jas_ew_jit_mode(int mode);
+
 /* Reductions over a leaf (mat_express_t.hpp:511-628).  op: 0 sum, 1 max, 2 mean.
  * axis: 0 = per row (hsum/hmax/hmean -> [rows,1]), 1 = per column (vsum/vmean -> [1,cols]),
  * 2 = whole matrix (sum/max/mean -> one value).  Accumulation in out_dtype. */

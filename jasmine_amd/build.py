@@ -1,6 +1,6 @@
 """Build libjasmine_hip.so (gfx950) in-tree with hipcc.
 
-    python -m jasmine_amd.build          # or: python jasmine_amd/build.py
+    python jasmine_amd/build.py
 
 Every HIP/C++ source under csrc/ is compiled for gfx950 only, objects go to
 jasmine_amd/_build/, the shared library to jasmine_amd/libjasmine_hip.so.
@@ -60,7 +60,7 @@ def build(verbose=True, jobs=None):
             if verbose and err.strip():
                 print(err, file=sys.stderr)
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", tmp] + objs + ["-lhiprtc"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stderr)

@@ -8,7 +8,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libjasmine_hip.so")
 
 if not os.path.exists(LIB_PATH):
-    raise ImportError(f"{LIB_PATH} is missing: build it with `python -m jasmine_amd.build` "
+    raise ImportError(f"{LIB_PATH} is missing: build it with `python jasmine_amd/build.py` "
                       "(there is no CPU fallback)")
 
 lib = C.CDLL(LIB_PATH)
@@ -87,6 +87,8 @@ for _n, _a in _sigs.items():
 lib.jas_last_error.restype = C.c_char_p
 lib.jas_version.restype = C.c_char_p
 lib.jas_default_stream.restype = VP
+lib.jas_ew_jit_mode.restype = C.c_int
+lib.jas_ew_jit_mode.argtypes = [C.c_int]
 lib.jas_attn_decode_workspace.restype = C.c_size_t
 lib.jas_attn_decode_workspace.argtypes = [I, I, I, I]
 lib.jas_lm_position.restype = I
@@ -96,7 +98,7 @@ lib.jas_lm_stream.argtypes = [VP]
 
 # every symbol the C header declares (checked by the CPU test that the library exports them)
 EXPORTED = sorted(list(_sigs) + ["jas_last_error", "jas_version", "jas_default_stream",
-                                 "jas_attn_decode_workspace", "jas_lm_position", "jas_lm_stream"])
+                                 "jas_attn_decode_workspace", "jas_ew_jit_mode", "jas_lm_position", "jas_lm_stream"])
 
 
 def check(code):

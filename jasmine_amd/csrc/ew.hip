@@ -92,7 +92,7 @@ __device__ __forceinline__ double unop(int op, int dt, double x, double imm)
     case JAS_OP_EXP: return exp(x);
     case JAS_OP_SIGMOID: return 1.0 / (1.0 + exp(-x));
     case JAS_OP_TANH: return tanh(x);
-    case JAS_OP_GELU: return 0.5 * x * (1.0 + tanh(0.7978845608028654 * (x + 0.044715 * x * x * x)));
+    case JAS_OP_GELU: return gelu_d(x);
     case JAS_OP_SILU: return x / (1.0 + exp(-x));
     case JAS_OP_SQRT: return sqrt(x);
     case JAS_OP_POW: return round_to(pow(x, imm), dt);
@@ -275,6 +275,8 @@ extern "C" jas_status jas_ew_eval(const jas_ew_ins *prog, int n_ins, const jas_l
         if (A.leaf[k].kind == LK_CONTIG && ((uintptr_t)leaves[k].d_data % 16) != 0) vec = false;
     }
     A.contig_vec = vec ? 1 : 0;
+    if (ew_jit_wanted((long)rows * cols))
+        return ew_jit_launch(prog, n_ins, A.leaf, n_leaves, vec, d_out, out_dtype, rows, cols, stream_or_default(stream));
     long total = (long)rows * A.col_chunks;
     hipLaunchKernelGGL(ew_eval_kernel, dim3(ceil_div(total, 256)), dim3(256), 0, stream_or_default(stream), A);
     JAS_LAUNCH_CHECK();

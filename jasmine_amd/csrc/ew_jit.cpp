@@ -1,0 +1,318 @@
+// Specialised fused elementwise kernels for large expression evaluations.
+//
+// jas_ew_eval interprets the postfix program (ew_eval_kernel); interpretation costs a
+// few hundred instructions per element and leaves an 8192x8192 evaluation compute-bound
+// at a fraction of HBM bandwidth.  For large outputs the same program is instead turned
+// into straight-line HIP source -- one typed local per node, leaves loaded once per
+// element (float4 for dense row-major operands), constants as exact hex literals -- and
+// compiled once per distinct program shape with hipRTC for the current device, then
+// cached for the process.  The numerics are the interpreter's exactly: every node is
+// computed in its own type, rounded to it, with the same device math functions and no
+// contraction across nodes.
+#include "jas_leaf.hpp"
+
+#include <hip/hiprtc.h>
+
+#include <cstdlib>
+#include <mutex>
+#include <sstream>
+#include <unordered_map>
+#include <vector>
+
+namespace jas {
+
+// kernel argument block; the generated source declares the same layout
+struct JitLeaf {
+    const void *p;
+    long rs, cs;
+    int rows, cols, row_first, roff, coff, transposed;
+};
+struct JitArgs {
+    JitLeaf leaf[JAS_EW_MAX_LEAVES];
+    void *out;
+    int rows, cols, col_chunks;
+};
+
+static const char *kPrelude = R"JAS(
+struct JitLeaf { const void *p; long rs, cs; int rows, cols, row_first, roff, coff, transposed; };
+struct JitArgs { JitLeaf leaf[8]; void *out; int rows, cols, col_chunks; };
+__device__ __forceinline__ long gen_index(const JitLeaf &L, int i, int j)
+{
+    int a = L.transposed ? j + L.coff : i + L.roff;
+    int b = L.transposed ? i + L.roff : j + L.coff;
+    a %= L.rows;
+    b %= L.cols;
+    return L.row_first ? (long)a * L.cols + b : (long)b * L.rows + a;
+}
+__device__ __forceinline__ float gelu_f(float x)
+{
+#pragma clang fp contract(fast)
+    float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+    return 0.5f * x * (1.0f + tanhf(u));
+}
+__device__ __forceinline__ double gelu_d(double x)
+{
+#pragma clang fp contract(fast)
+    return 0.5 * x * (1.0 + tanh(0.7978845608028654 * (x + 0.044715 * x * x * x)));
+}
+__device__ __forceinline__ float silu_f(float x)
+{
+#pragma clang fp contract(fast)
+    return x / (1.0f + expf(-x));
+}
+)JAS";
+
+static int g_jit_mode = 2;  // 0 never, 1 always, 2 large outputs only
+static constexpr long kAutoMinElems = 1L << 20;
+
+static const char *ctype(int dt) { return dt == JAS_F64 ? "double" : dt == JAS_I32 ? "int" : "float"; }
+
+static std::string hexlit(double v)
+{
+    char buf[64];
+    std::snprintf(buf, sizeof buf, "%a", v);
+    std::string s(buf);
+    if (s == "inf") return "__builtin_inf()";
+    if (s == "-inf") return "(-__builtin_inf())";
+    if (s == "nan" || s == "-nan") return "__builtin_nan(\"\")";
+    return s;
+}
+
+struct Gen {
+    std::string src;
+    std::vector<int> leaf_slot;  // program leaf index -> deduplicated slot
+    int n_slots = 0;
+};
+
+static bool same_leaf(const LeafDev &a, const LeafDev &b)
+{
+    return a.p == b.p && a.kind == b.kind && a.dtype == b.dtype && a.rs == b.rs && a.cs == b.cs && a.rows == b.rows &&
+           a.cols == b.cols && a.row_first == b.row_first && a.roff == b.roff && a.coff == b.coff &&
+           a.transposed == b.transposed;
+}
+
+// Straight-line source for one program.  Every value is produced for VEC = 4 consecutive
+// columns of one output row (loop over e); node k becomes the local `T vk`.
+static Gen generate(const jas_ew_ins *prog, int n_ins, const LeafDev *leaves, int n_leaves, bool vec, int out_dtype,
+                    std::vector<int> &slot_src)
+{
+    Gen g;
+    g.leaf_slot.assign(n_leaves, -1);
+    slot_src.clear();
+    for (int k = 0; k < n_leaves; ++k) {
+        for (int s = 0; s < (int)slot_src.size(); ++s)
+            if (same_leaf(leaves[slot_src[s]], leaves[k])) g.leaf_slot[k] = s;
+        if (g.leaf_slot[k] < 0) {
+            g.leaf_slot[k] = (int)slot_src.size();
+            slot_src.push_back(k);
+        }
+    }
+    g.n_slots = (int)slot_src.size();
+    std::ostringstream o;
+    o << kPrelude;
+    // no contraction between nodes (each node rounds to its type, as in the interpreter);
+    // the math helpers above contract exactly like their twins in the library
+    o << "extern \"C\" __global__ void __launch_bounds__(256) jas_ew_jit(const JitArgs A)\n{\n"
+         "#pragma clang fp contract(off)\n"
+         "    long gid = (long)blockIdx.x * 256 + threadIdx.x;\n"
+         "    if (gid >= (long)A.rows * A.col_chunks) return;\n"
+         "    const int i = (int)(gid / A.col_chunks);\n"
+         "    const int j0 = (int)(gid % A.col_chunks) * 4;\n"
+         "    const long lin0 = (long)i * A.cols + j0;\n";
+    if (!vec) o << "    const int nv = min(4, A.cols - j0);\n";
+    // leaf loads (each distinct operand once)
+    for (int s = 0; s < g.n_slots; ++s) {
+        const LeafDev &L = leaves[slot_src[s]];
+        const char *T = ctype(L.dtype);
+        o << "    " << T << " l" << s << "[4];\n    {\n        const " << T << " *p = (const " << T << " *)A.leaf[" << s
+          << "].p;\n";
+        if (L.kind == LK_CONTIG && vec && L.dtype == JAS_F32) {
+            o << "        float4 v = *(const float4 *)(p + lin0);\n"
+                 "        l" << s << "[0] = v.x; l" << s << "[1] = v.y; l" << s << "[2] = v.z; l" << s << "[3] = v.w;\n";
+        } else {
+            o << "#pragma unroll\n        for (int e = 0; e < 4; ++e) {\n";
+            o << (vec ? "            const int ee = e;\n" : "            const int ee = e < nv ? e : 0;\n");
+            if (L.kind == LK_CONTIG)
+                o << "            l" << s << "[e] = p[lin0 + ee];\n";
+            else if (L.kind == LK_STRIDED)
+                o << "            l" << s << "[e] = p[(long)i * A.leaf[" << s << "].rs + (long)(j0 + ee) * A.leaf[" << s
+                  << "].cs];\n";
+            else
+                o << "            l" << s << "[e] = p[gen_index(A.leaf[" << s << "], i, j0 + ee)];\n";
+            o << "        }\n";
+        }
+        o << "    }\n";
+    }
+    // nodes
+    std::vector<int> stack;  // node ids on the evaluation stack
+    if (vec && out_dtype == JAS_F32) o << "    float ov[4];\n";
+    o << "#pragma unroll\n    for (int e = 0; e < 4; ++e) {\n";
+    for (int k = 0; k < n_ins; ++k) {
+        const jas_ew_ins &in = prog[k];
+        const int dt = in.dtype;
+        int vt = dt;
+        std::ostringstream rhs;
+        if (in.op == JAS_OP_LEAF) {
+            rhs << "(" << ctype(dt) << ")l" << g.leaf_slot[in.arg] << "[e]";
+        } else if (in.op == JAS_OP_CONST) {
+            rhs << "(" << ctype(dt) << ")" << hexlit(in.imm);
+        } else if (in.op >= JAS_OP_ADD && in.op <= JAS_OP_LT) {
+            int hi = stack.back();
+            stack.pop_back();
+            int lo = stack.back();
+            stack.pop_back();
+            int x = (in.arg & 1) ? hi : lo, y = (in.arg & 1) ? lo : hi;
+            std::string a = std::string("(") + ctype(dt) + ")v" + std::to_string(x);
+            std::string b = std::string("(") + ctype(dt) + ")v" + std::to_string(y);
+            static const char *sym[] = {"+", "-", "*", "/", ">", "<"};
+            const char *op = sym[in.op - JAS_OP_ADD];
+            if (in.op == JAS_OP_GT || in.op == JAS_OP_LT) {
+                vt = JAS_F64;  // the comparison result is exactly 1 or 0 in any type
+                rhs << "(" << a << " " << op << " " << b << ") ? 1.0 : 0.0";
+            } else if (in.op == JAS_OP_DIV && dt == JAS_I32) {
+                rhs << "(" << b << ") ? " << a << " / " << b << " : 0";
+            } else {
+                rhs << a << " " << op << " " << b;
+            }
+        } else {
+            int x = stack.back();
+            stack.pop_back();
+            std::string xs = "v" + std::to_string(x);
+            if (dt == JAS_F32) {
+                std::string a = "(float)" + xs;
+                switch (in.op) {
+                case JAS_OP_EXP: rhs << "expf(" << a << ")"; break;
+                case JAS_OP_SIGMOID: rhs << "(float)(1.0 / (1.0 + (double)expf(-" << a << ")))"; break;
+                case JAS_OP_TANH: rhs << "tanhf(" << a << ")"; break;
+                case JAS_OP_GELU: rhs << "gelu_f(" << a << ")"; break;
+                case JAS_OP_SILU: rhs << "silu_f(" << a << ")"; break;
+                case JAS_OP_SQRT: rhs << "sqrtf(" << a << ")"; break;
+                case JAS_OP_POW: rhs << "(float)pow((double)" << a << ", " << hexlit(in.imm) << ")"; break;
+                default: rhs << "-" << a; break;
+                }
+            } else {
+                // fp64 nodes (and int nodes, whose transcendental results stay unrounded)
+                std::string a = "(double)" + xs;
+                vt = JAS_F64;
+                switch (in.op) {
+                case JAS_OP_EXP: rhs << "exp(" << a << ")"; break;
+                case JAS_OP_SIGMOID: rhs << "1.0 / (1.0 + exp(-" << a << "))"; break;
+                case JAS_OP_TANH: rhs << "tanh(" << a << ")"; break;
+                case JAS_OP_GELU: rhs << "gelu_d(" << a << ")"; break;
+                case JAS_OP_SILU: rhs << a << " / (1.0 + exp(-" << a << "))"; break;
+                case JAS_OP_SQRT: rhs << "sqrt(" << a << ")"; break;
+                case JAS_OP_POW:
+                    vt = dt;
+                    rhs << "(" << ctype(dt) << ")pow(" << a << ", " << hexlit(in.imm) << ")";
+                    break;
+                default:
+                    vt = dt;
+                    rhs << "(" << ctype(dt) << ")(-" << a << ")";
+                    break;
+                }
+            }
+        }
+        o << "        const " << ctype(vt) << " v" << k << " = " << rhs.str() << ";\n";
+        stack.push_back(k);
+    }
+    const char *OT = ctype(out_dtype);
+    o << "        const " << OT << " res = (" << OT << ")v" << stack.back() << ";\n";
+    if (vec && out_dtype == JAS_F32) {
+        o << "        ov[e] = res;\n    }\n"
+             "    *(float4 *)((float *)A.out + lin0) = make_float4(ov[0], ov[1], ov[2], ov[3]);\n}\n";
+    } else {
+        o << "        if (" << (vec ? "true" : "e < nv") << ") ((" << OT << " *)A.out)[lin0 + e] = res;\n    }\n}\n";
+    }
+    g.src = o.str();
+    return g;
+}
+
+struct JitKernel {
+    hipModule_t mod = nullptr;
+    hipFunction_t fn = nullptr;
+};
+
+static std::mutex g_jit_mu;
+static std::unordered_map<std::string, JitKernel> g_jit_cache;
+
+static jas_status compile(const std::string &src, JitKernel &out)
+{
+    int dev = 0;
+    JAS_HIP(hipGetDevice(&dev));
+    hipDeviceProp_t prop;
+    JAS_HIP(hipGetDeviceProperties(&prop, dev));
+    std::string arch = std::string("--offload-arch=") + prop.gcnArchName;
+    hiprtcProgram prog;
+    if (hiprtcCreateProgram(&prog, src.c_str(), "jas_ew_jit.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+        return fail(JAS_ERR_RUNTIME, "jas_ew_eval: hiprtcCreateProgram failed");
+    // packed-FP32 instructions stay disabled, as for every other kernel of the library
+    const char *opts[] = {arch.c_str(), "-O3", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+    hiprtcResult rc = hiprtcCompileProgram(prog, (int)(sizeof opts / sizeof opts[0]), opts);
+    if (rc != HIPRTC_SUCCESS) {
+        size_t n = 0;
+        hiprtcGetProgramLogSize(prog, &n);
+        std::string log(n, '\0');
+        if (n) hiprtcGetProgramLog(prog, &log[0]);
+        hiprtcDestroyProgram(&prog);
+        return fail(JAS_ERR_RUNTIME, "jas_ew_eval: specialised kernel failed to compile: " + log);
+    }
+    size_t n = 0;
+    hiprtcGetCodeSize(prog, &n);
+    std::vector<char> code(n);
+    hiprtcGetCode(prog, code.data());
+    hiprtcDestroyProgram(&prog);
+    JAS_HIP(hipModuleLoadData(&out.mod, code.data()));
+    JAS_HIP(hipModuleGetFunction(&out.fn, out.mod, "jas_ew_jit"));
+    return JAS_OK;
+}
+
+bool ew_jit_wanted(long n_elems)
+{
+    if (g_jit_mode == 0) return false;
+    if (g_jit_mode == 1) return true;
+    return n_elems >= kAutoMinElems;
+}
+
+jas_status ew_jit_launch(const jas_ew_ins *prog, int n_ins, const LeafDev *leaves, int n_leaves, bool vec,
+                         void *out, int out_dtype, int rows, int cols, hipStream_t s)
+{
+    std::vector<int> slot_src;
+    Gen g = generate(prog, n_ins, leaves, n_leaves, vec, out_dtype, slot_src);
+    int dev = 0;
+    JAS_HIP(hipGetDevice(&dev));
+    const std::string key = std::to_string(dev) + "\n" + g.src;
+    hipFunction_t fn = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_jit_mu);
+        auto it = g_jit_cache.find(key);
+        if (it == g_jit_cache.end()) {
+            JitKernel k;
+            jas_status st = compile(g.src, k);
+            if (st != JAS_OK) return st;
+            it = g_jit_cache.emplace(key, k).first;
+        }
+        fn = it->second.fn;
+    }
+    JitArgs A{};
+    for (int sl = 0; sl < g.n_slots; ++sl) {
+        const LeafDev &L = leaves[slot_src[sl]];
+        A.leaf[sl] = JitLeaf{L.p, L.rs, L.cs, L.rows, L.cols, L.row_first, L.roff, L.coff, L.transposed};
+    }
+    A.out = out;
+    A.rows = rows;
+    A.cols = cols;
+    A.col_chunks = (cols + 3) / 4;
+    const long total = (long)rows * A.col_chunks;
+    void *params[] = {&A};
+    JAS_HIP(hipModuleLaunchKernel(fn, ceil_div(total, 256), 1, 1, 256, 1, 1, 0, s, params, nullptr));
+    return JAS_OK;
+}
+
+} // namespace jas
+
+extern "C" int jas_ew_jit_mode(int mode)
+{
+    const int prev = jas::g_jit_mode;
+    if (mode >= 0 && mode <= 2) jas::g_jit_mode = mode;
+    return prev;
+}

@@ -95,10 +95,20 @@ __device__ __forceinline__ float block_max(float v, float *red)
 // GPT-2 tanh GELU and SiLU in fp32
 __device__ __forceinline__ float gelu_f(float x)
 {
+#pragma clang fp contract(fast)
     float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
     return 0.5f * x * (1.0f + tanhf(u));
 }
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ double gelu_d(double x)
+{
+#pragma clang fp contract(fast)
+    return 0.5 * x * (1.0 + tanh(0.7978845608028654 * (x + 0.044715 * x * x * x)));
+}
+__device__ __forceinline__ float silu_f(float x)
+{
+#pragma clang fp contract(fast)
+    return x / (1.0f + expf(-x));
+}
 
 __device__ __forceinline__ float apply_act(float v, int act)
 {

@@ -73,4 +73,9 @@ static inline LeafDev classify(const jas_leaf &l, int rows, int cols)
     return d;
 }
 
+// specialised (hipRTC-compiled) evaluation of a validated program; ew_jit.cpp
+bool ew_jit_wanted(long n_elems);
+jas_status ew_jit_launch(const jas_ew_ins *prog, int n_ins, const LeafDev *leaves, int n_leaves, bool vec, void *out,
+                         int out_dtype, int rows, int cols, hipStream_t s);
+
 } // namespace jas

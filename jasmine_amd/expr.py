@@ -27,8 +27,9 @@ class Node:
     rows: int
     cols: int
     kids: list = field(default_factory=list)
-    leaf: Optional[object] = None  # (device array, jas_leaf kwargs)
+    leaf: Optional[object] = None  # jas_leaf descriptor
     imm: float = 0.0
+    owner: Optional[object] = None  # the device buffer a leaf points into, kept alive with the tree
 
     def __add__(self, o): return bin_("+", self, o)
     def __radd__(self, o): return bin_("+", o, self)
@@ -51,7 +52,7 @@ def const(v, dtype=None):
 def leaf(arr, dtype=F32, **kw):
     from jasmine_amd.capi import leaf as mk
     lf = mk(arr, **kw)
-    return Node("leaf", dtype, lf.vrows, lf.vcols, leaf=lf)
+    return Node("leaf", dtype, lf.vrows, lf.vcols, leaf=lf, owner=arr)
 
 
 def _wrap(x):

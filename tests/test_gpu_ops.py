@@ -43,7 +43,16 @@ GOLD_TREES = {
 }
 
 
-def test_ew_golden(jas):
+@pytest.fixture(params=[0, 1], ids=["interp", "jit"])
+def ew_mode(jas, request):
+    """Run an expression test through the interpreter kernel and through the specialised
+    (hipRTC) kernel; the library default picks by output size."""
+    prev = jas.lib.jas_ew_jit_mode(request.param)
+    yield request.param
+    jas.lib.jas_ew_jit_mode(prev)
+
+
+def test_ew_golden(jas, ew_mode):
     g = np.load(__import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "jasmine_golden.npz"))
     n = 0
     while f"expr{n}_id" in g:
@@ -63,7 +72,7 @@ def test_ew_golden(jas):
 
 
 @pytest.mark.parametrize("shape", [(64, 64), (33, 65), (1024, 1024), (8192, 1024)])
-def test_ew_cfg2(jas, shape):
+def test_ew_cfg2(jas, ew_mode, shape):
     R, Cc = shape
     a, b, c = normal(shape, 1, 0), normal(shape, 1, 1), normal(shape, 1, 2)
     want = np.zeros_like(a)
@@ -81,7 +90,7 @@ def test_ew_cfg2(jas, shape):
     assert bitfrac(part, want_part) == 1.0
 
 
-def test_ew_jasmine_view_and_modulo_semantics(jas):
+def test_ew_jasmine_view_and_modulo_semantics(jas, ew_mode):
     # jasmine views add offsets then the underlying mat_t wraps indices modulo its dims
     # (mat_view_t.hpp:28-38, mat_t.hpp:312-320), including the swapped offsets of a
     # transposed view with offsets.
@@ -103,7 +112,7 @@ def test_ew_jasmine_view_and_modulo_semantics(jas):
         assert bitfrac(got, want) == 1.0, (roff, coff, t)
 
 
-def test_ew_unary_and_pow(jas):
+def test_ew_unary_and_pow(jas, ew_mode):
     x = normal((37, 41), 3, 0)
     dx = jas.to_device(x)
     X = E.leaf(dx)
@@ -112,6 +121,47 @@ def test_ew_unary_and_pow(jas):
         close(E.evaluate(jas, E.un(op, X)), fn(x.astype(np.float64)).astype(np.float32), atol=2e-6, rtol=2e-6)
     sq = E.evaluate(jas, E.un("sqrt", E.un("pow", X, imm=2.0)))
     close(sq, np.abs(x), atol=1e-6, rtol=1e-6)
+
+
+def test_ew_jit_equals_interpreter(jas):
+    """The specialised kernel reproduces the interpreter bit for bit on mixed-type trees:
+    int / float / double nodes, comparisons, every unary op, broadcast and strided views."""
+    x = normal((67, 130), 4, 0)
+    y = (np.abs(normal((67, 130), 4, 1)) + 0.25).astype(np.float32)
+    r = normal((1, 130), 4, 2)
+    xd = normal((67, 130), 4, 3).astype(np.float64)
+    iv = (np.arange(67 * 130, dtype=np.int32).reshape(67, 130) % 11) - 5
+    dx, dy, dr, dxd, di = (jas.to_device(v) for v in (x, y, r, xd, iv))
+    X, Y, Rw, XD = E.leaf(dx), E.leaf(dy), E.leaf(dr), E.leaf(dxd, dtype=E.F64)
+    I = E.leaf(di, dtype=E.I32)
+    XT = E.leaf(dx, roff=3, coff=5, transposed=1, vrows=60, vcols=60)
+    trees = [
+        X * Y + 0.5 * Rw - E.un("tanh", X),
+        (X > Y) * X + (X < Y) * Y / 3,
+        E.un("exp", X - Rw) + E.un("sigmoid", X * 2.0) - E.un("silu", Y),
+        E.un("gelu", X) * E.un("sqrt", Y) + E.un("pow", Y, imm=1.5),
+        XD * X - E.un("exp", XD * 0.25) + E.un("neg", X),
+        I * 3 + I / 2 - (I > 0) * X,
+        E.un("gelu", XD) + E.un("tanh", XD) - E.un("sqrt", XD * XD),
+    ]
+    for k, t in enumerate(trees):
+        for out_dt in (E.F32, t.dtype):
+            jas.lib.jas_ew_jit_mode(0)
+            a = E.evaluate(jas, t, out_dtype=out_dt)
+            jas.lib.jas_ew_jit_mode(1)
+            b = E.evaluate(jas, t, out_dtype=out_dt)
+            jas.lib.jas_ew_jit_mode(2)
+            assert a.shape == b.shape and a.dtype == b.dtype
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), (k, out_dt)
+    # transposed-offset view (general modulo addressing) against a dense leaf
+    dsq = jas.to_device(np.ascontiguousarray(x[:60, :60]))  # keep the buffer alive while the leaf is used
+    t = XT * 2.0 + E.leaf(dsq)
+    jas.lib.jas_ew_jit_mode(0)
+    a = E.evaluate(jas, t)
+    jas.lib.jas_ew_jit_mode(1)
+    b = E.evaluate(jas, t)
+    jas.lib.jas_ew_jit_mode(2)
+    assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
 
 
 def test_ew_rejects_bad_programs(jas):
