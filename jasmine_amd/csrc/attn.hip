@@ -66,124 +66,244 @@ struct PrefillArgs {
     int causal;
 };
 
-constexpr int FA_BQ = 64, FA_BK = 64;
+constexpr int FA_NW = 8;    // waves per workgroup; 16 queries each
+constexpr int FA_BQ = 16 * FA_NW;
 
-template <int D, bool BF16>
-__global__ void __launch_bounds__(256) flash_prefill_kernel(const PrefillArgs p)
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// 2^x on the hardware exp unit (v_exp_f32): results below 2^-126 flush to zero.  Used for
+// softmax terms 2^(s - max) <= 1, where such terms cannot change a sum that contains 1.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+// a 16-byte chunk as a native vector (HIP's uint4 struct defeats register promotion)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// One workgroup = 64 queries of one (batch, head), 16 per wave.  Key/value tiles of 64
+// rows are double-staged: the global loads of tile t+1 are issued into registers before
+// tile t is computed from LDS, so HBM latency hides behind the matrix work.  Rows past
+// Sk are read clamped (finite data) and masked to probability 0.  fp32: S^T = K Q^T and
+// O^T += V^T P^T on v_mfma_f32_16x16x4_f32.  bf16: the same products on
+// v_mfma_f32_16x16x32_bf16 (fp32 accumulate, softmax in fp32, P rounded to bf16 for the
+// second product); the reduction index of each product is permuted identically in both
+// operands so that S lands in the P operand's registers with no shuffle.
+template <int D, bool BF16, int BK>
+__global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const PrefillArgs p)
 {
-    constexpr int KLD = D + 4;        // Ks row stride
-    constexpr int VLD = FA_BK + 4;    // Vt row stride
-    constexpr int NC = D / 16;        // 16-wide chunks of the head dim
-    __shared__ float Ks[FA_BK * KLD];
-    __shared__ float Vt[D * VLD];
+    constexpr int NT = 64 * FA_NW;
+    using T = typename std::conditional<BF16, uint16_t, float>::type;
+    constexpr int EPC = 16 / (int)sizeof(T);    // elements per 16-byte chunk
+    constexpr int KLD = D + (BF16 ? 8 : 4);    // padded row strides (elements)
+    constexpr int VLD = BK + (BF16 ? 8 : 4);
+    constexpr int CPR = D / EPC;                // 16-byte chunks per key row
+    constexpr int NCH = BK * CPR;            // 16-byte chunks per tile and tensor
+    constexpr int NLD = (NCH + NT - 1) / NT;    // chunks per thread per tensor and tile
+    constexpr int NC = D / 16;                  // 16-row blocks of the head dim (output)
+    constexpr int NJ = BK / 16;                 // 16-key blocks of a tile
+    static_assert(NCH % NT == 0 || NLD == 1, "tile/thread mismatch");
+    // two tile buffers: tile t+1 is written while tile t is read, one barrier per tile
+    __shared__ __attribute__((aligned(16))) T Ks[2][BK * KLD];
+    __shared__ __attribute__((aligned(16))) T Vt[2][D * VLD];
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, r16 = lane & 15, g = lane >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
+    // XCD-aware order: consecutive workgroup ids go to different XCDs (round robin over 8),
+    // so work item w = xcd * per + slot keeps the query blocks of one (batch, head) -- which
+    // share its K/V -- on one XCD's L2; within a head the heaviest causal blocks go first
     const int nqb = (p.Sq + FA_BQ - 1) / FA_BQ;
-    const int qb = nqb - 1 - (int)blockIdx.x;  // heaviest (causal) query blocks first
-    const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H;
+    const int total = nqb * p.B * p.H, per = (total + 7) / 8;
+    const int wi = ((int)blockIdx.x % 8) * per + (int)blockIdx.x / 8;
+    if (wi >= total) return;
+    const int bh = wi / nqb, qb = nqb - 1 - wi % nqb, b = bh / p.H, h = bh % p.H;
     const int q0 = qb * FA_BQ + w * 16;
     const int qi = q0 + r16;  // this lane's query (column of S^T)
     const int shift = p.Sk - p.Sq;
+    const int qq = qi < p.Sq ? qi : p.Sq - 1;
+    const long qbase = (long)b * p.q_sb + (long)h * p.q_sh + (long)qq * p.q_ss;
 
-    const char *Qb = (const char *)p.Q;
-    // Q fragment: lane holds Q[qi][16c + 4g .. +3], prescaled by scale*log2(e)
-    float4 qf[NC];
-    {
-        const int qq = qi < p.Sq ? qi : p.Sq - 1;
-        long base = (long)b * p.q_sb + (long)h * p.q_sh + (long)qq * p.q_ss;
+    const int q_last = min(qb * FA_BQ + FA_BQ - 1, p.Sq - 1);
+    const int k_end = p.causal ? min(p.Sk, q_last + shift + 1) : p.Sk;
+    // keys this wave can see at all (causal): [0, wave_kend)
+    const int wave_kend = p.causal ? min(p.Sk, min(q0 + 15, p.Sq - 1) + shift + 1) : p.Sk;
+    const long kbase = (long)b * p.k_sb + (long)h * p.k_sh;
+
+    // staging: chunk `it` of this thread is (key row, 16-byte column) of the 64-row tile
+    u32x4 kreg[NLD], vreg[NLD];
+    long goff[NLD];
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            float4 v = load4<BF16>(Qb, base + 16 * c + 4 * g);
-            qf[c] = make_float4(v.x * p.scale_log2, v.y * p.scale_log2, v.z * p.scale_log2, v.w * p.scale_log2);
-        }
+    for (int it = 0; it < NLD; ++it) {
+        const int idx = min(tid + it * NT, NCH - 1);
+        goff[it] = kbase + (long)(idx / CPR) * p.k_ss + (idx % CPR) * EPC;
+    }
+    // rows past Sk are read clamped to the last row (finite data, masked below)
+#define FA_GLOAD(KV0)                                                                        \
+    if ((KV0) + BK <= p.Sk) {                                                           \
+        const long o0 = (long)(KV0) * p.k_ss;                                              \
+        _Pragma("unroll") for (int it = 0; it < NLD; ++it)                                 \
+        {                                                                                  \
+            kreg[it] = *(const u32x4 *)((const T *)p.K + goff[it] + o0);                   \
+            vreg[it] = *(const u32x4 *)((const T *)p.V + goff[it] + o0);                   \
+        }                                                                                  \
+    } else {                                                                               \
+        _Pragma("unroll") for (int it = 0; it < NLD; ++it)                                 \
+        {                                                                                  \
+            const int idx = min(tid + it * NT, NCH - 1), key = idx / CPR, ch = idx % CPR; \
+            const long off = kbase + (long)min((KV0) + key, p.Sk - 1) * p.k_ss + ch * EPC; \
+            kreg[it] = *(const u32x4 *)((const T *)p.K + off);                             \
+            vreg[it] = *(const u32x4 *)((const T *)p.V + off);                             \
+        }                                                                                  \
     }
 
     floatx4 oacc[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) oacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -FLT_MAX, l_run = 0.f;
+    // running max (raw score units) and this lane's partial row sum: the lanes g = 0..3 of
+    // one query each sum their own keys; the four partials are combined once at the end
+    float m_run = -INFINITY, l_part = 0.f;
+    const float sl2 = p.scale_log2;
 
-    const int q_last = min(qb * FA_BQ + FA_BQ - 1, p.Sq - 1);
-    const int k_end = p.causal ? min(p.Sk, q_last + shift + 1) : p.Sk;
-    const long kbase = (long)b * p.k_sb + (long)h * p.k_sh;
-
-    for (int kv0 = 0; kv0 < k_end; kv0 += FA_BK) {
-        __syncthreads();
-        // stage K (row-major) and V (transposed) tiles: 64 keys x D
+    // Q fragments (B operand of S^T = K Q^T), raw (the scale is applied in the exponent)
+    float4 qf[BF16 ? 1 : NC];
+    bf16x8 qb16[BF16 ? D / 32 : 1];
+    if constexpr (BF16) {
 #pragma unroll
-        for (int it = 0; it < (FA_BK * D / 4) / 256; ++it) {
-            int idx = tid + it * 256;
-            int key = idx / (D / 4), d4 = (idx % (D / 4)) * 4;
-            int kk = kv0 + key;
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (kk < p.Sk) {
-                kv = load4<BF16>(p.K, kbase + (long)kk * p.k_ss + d4);
-                vv = load4<BF16>(p.V, kbase + (long)kk * p.k_ss + d4);
-            }
-            *(float4 *)(Ks + key * KLD + d4) = kv;
-            Vt[(d4 + 0) * VLD + key] = vv.x;
-            Vt[(d4 + 1) * VLD + key] = vv.y;
-            Vt[(d4 + 2) * VLD + key] = vv.z;
-            Vt[(d4 + 3) * VLD + key] = vv.w;
+        for (int c = 0; c < D / 32; ++c)
+            qb16[c] = *(const bf16x8 *)((const uint16_t *)p.Q + qbase + 32 * c + 8 * g);
+    } else {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) qf[c] = *(const float4 *)((const float *)p.Q + qbase + 16 * c + 4 * g);
+    }
+
+#define FA_LSTORE(BUF)                                                                       \
+    _Pragma("unroll") for (int it = 0; it < NLD; ++it)                                     \
+    {                                                                                      \
+        const int idx = tid + it * NT, key = idx / CPR, ch = idx % CPR;                    \
+        if (NCH % NT != 0 && idx >= NCH) break;                                            \
+        *(u32x4 *)(&Ks[BUF][key * KLD + ch * EPC]) = kreg[it];                             \
+        const u32x4 vw = vreg[it];                                                         \
+        _Pragma("unroll") for (int t = 0; t < EPC; ++t)                                    \
+        {                                                                                  \
+            if constexpr (BF16)                                                            \
+                Vt[BUF][(ch * EPC + t) * VLD + key] = (uint16_t)(vw[t / 2] >> (16 * (t & 1))); \
+            else                                                                           \
+                Vt[BUF][(ch * EPC + t) * VLD + key] = __uint_as_float(vw[t]);              \
+        }                                                                                  \
+    }
+
+    if (k_end > 0) {
+        FA_GLOAD(0)
+        FA_LSTORE(0)
+        if (BK < k_end) { FA_GLOAD(BK) }
+    }
+    __syncthreads();
+    int buf = 0;
+    for (int kv0 = 0; kv0 < k_end; kv0 += BK, buf ^= 1) {
+        // stage tile t+1 (loaded during the previous tile's math) and start loading t+2
+        if (kv0 + BK < k_end) {
+            FA_LSTORE(buf ^ 1)
+            if (kv0 + 2 * BK < k_end) { FA_GLOAD(kv0 + 2 * BK) }
         }
-        __syncthreads();
+        if (kv0 >= wave_kend) {  // wave-uniform: every key of this tile is masked for this wave
+            __syncthreads();
+            continue;
+        }
+        const T *Kc = Ks[buf], *Vc = Vt[buf];
 
-        // S^T tile: lane holds S^T[key = 16j + 4g + r][query = qi]
-        floatx4 s[4];
+        // S^T tile: lane holds S^T[key = kv0 + 16j + 4g + r][query = qi] (raw scores)
+        floatx4 s[NJ];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             s[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (BF16) {
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                float4 kf = *(const float4 *)(Ks + (16 * j + r16) * KLD + 16 * c + 4 * g);
-                s[j] = mfma4(kf.x, qf[c].x, s[j]);
-                s[j] = mfma4(kf.y, qf[c].y, s[j]);
-                s[j] = mfma4(kf.z, qf[c].z, s[j]);
-                s[j] = mfma4(kf.w, qf[c].w, s[j]);
+                for (int c = 0; c < D / 32; ++c) {
+                    bf16x8 kf = *(const bf16x8 *)(Kc + (16 * j + r16) * KLD + 32 * c + 8 * g);
+                    s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qb16[c], s[j], 0, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    float4 kf = *(const float4 *)(Kc + (16 * j + r16) * KLD + 16 * c + 4 * g);
+                    s[j] = mfma4(kf.x, qf[c].x, s[j]);
+                    s[j] = mfma4(kf.y, qf[c].y, s[j]);
+                    s[j] = mfma4(kf.z, qf[c].z, s[j]);
+                    s[j] = mfma4(kf.w, qf[c].w, s[j]);
+                }
             }
         }
-        // mask and tile max for this lane's query
-        float tmax = -FLT_MAX;
+        // masking only on tiles that reach past Sk or cross this wave's causal diagonal
+        const bool need_mask = kv0 + BK > p.Sk || (p.causal && kv0 + BK - 1 > q0 + shift);
+        if (need_mask) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < NJ; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                int kk = kv0 + 16 * j + 4 * g + r;
-                bool ok = kk < p.Sk && (!p.causal || kk <= qi + shift);
-                s[j][r] = ok ? s[j][r] : -FLT_MAX;
-                tmax = fmaxf(tmax, s[j][r]);
-            }
+                for (int r = 0; r < 4; ++r) {
+                    const int kk = kv0 + 16 * j + 4 * g + r;
+                    const bool ok = kk < p.Sk && (!p.causal || kk <= qi + shift);
+                    s[j][r] = ok ? s[j][r] : -INFINITY;
+                }
+        }
+        float tmax = s[0][0];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int r = (j == 0 ? 1 : 0); r < 4; ++r) tmax = fmaxf(tmax, s[j][r]);
         tmax = fmaxf(tmax, __shfl_xor(tmax, 16, WAVE));
         tmax = fmaxf(tmax, __shfl_xor(tmax, 32, WAVE));
         const float m_new = fmaxf(m_run, tmax);
-        const float corr = exp2f(m_run - m_new);
+        // p = 2^(scale*log2e * (s - m)); a query with every key masked so far keeps m = -inf
+        // and gets p = 0 from the -inf scores
+        const float mb = m_new == -INFINITY ? 0.f : m_new * sl2;
+        const float corr = exp2_fast(m_run * sl2 - mb);  // m_run = -inf on the first tile: 0
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[j][r] = exp2_fast(__builtin_fmaf(s[j][r], sl2, -mb));
         float psum = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float pv = s[j][r] == -FLT_MAX ? 0.f : exp2f(s[j][r] - m_new);
-                s[j][r] = pv;
-                psum += pv;
-            }
-        psum += __shfl_xor(psum, 16, WAVE);
-        psum += __shfl_xor(psum, 32, WAVE);
-        l_run = l_run * corr + psum;
+        for (int j = 0; j < NJ; ++j) psum += (s[j][0] + s[j][1]) + (s[j][2] + s[j][3]);
+        l_part = l_part * corr + psum;
         m_run = m_new;
+        // rescale the accumulator only when some query's max moved (wave-uniform test)
+        if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
 #pragma unroll
-        for (int c = 0; c < NC; ++c) oacc[c] *= corr;
-        // O^T[d = 16c + 4g + r][q] += sum_key V^T[d][key] P^T[key][q]
+            for (int c = 0; c < NC; ++c) oacc[c] *= corr;
+        }
+
+        if constexpr (BF16) {
+            // P^T operand for key block m (32 keys): slot t <-> key 32m + 16(t/4) + 4g + t%4,
+            // which are exactly s[2m][t] and s[2m+1][t-4] of this lane
+            bf16x8 pb[NJ / 2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+            for (int m = 0; m < NJ / 2; ++m)
+                pb[m] = bf16x8{(__bf16)s[2 * m][0], (__bf16)s[2 * m][1], (__bf16)s[2 * m][2], (__bf16)s[2 * m][3],
+                               (__bf16)s[2 * m + 1][0], (__bf16)s[2 * m + 1][1], (__bf16)s[2 * m + 1][2],
+                               (__bf16)s[2 * m + 1][3]};
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                float4 vf = *(const float4 *)(Vt + (16 * c + r16) * VLD + 16 * j + 4 * g);
-                oacc[c] = mfma4(vf.x, s[j][0], oacc[c]);
-                oacc[c] = mfma4(vf.y, s[j][1], oacc[c]);
-                oacc[c] = mfma4(vf.z, s[j][2], oacc[c]);
-                oacc[c] = mfma4(vf.w, s[j][3], oacc[c]);
-            }
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int m = 0; m < NJ / 2; ++m) {
+                    const uint16_t *vr = Vc + (16 * c + r16) * VLD + 32 * m + 4 * g;
+                    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                    const u32x2 lo = *(const u32x2 *)vr, hi = *(const u32x2 *)(vr + 16);
+                    const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
+                    oacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[m], oacc[c], 0, 0, 0);
+                }
+        } else {
+            // O^T[d = 16c + 4g + r][q] += sum_key V^T[d][key] P^T[key][q]
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    float4 vf = *(const float4 *)(Vc + (16 * c + r16) * VLD + 16 * j + 4 * g);
+                    oacc[c] = mfma4(vf.x, s[j][0], oacc[c]);
+                    oacc[c] = mfma4(vf.y, s[j][1], oacc[c]);
+                    oacc[c] = mfma4(vf.z, s[j][2], oacc[c]);
+                    oacc[c] = mfma4(vf.w, s[j][3], oacc[c]);
+                }
+        }
+        __syncthreads();  // every wave is done with buffer `buf` before it is restaged
     }
+    float l_run = l_part + __shfl_xor(l_part, 16, WAVE);
+    l_run += __shfl_xor(l_run, 32, WAVE);
 
     // lane holds O^T[d = 16c + 4g + r][query = qi], i.e. four consecutive dims of its query
     if (qi < p.Sq) {
@@ -194,6 +314,8 @@ __global__ void __launch_bounds__(256) flash_prefill_kernel(const PrefillArgs p)
             store4<BF16>(p.O, obase + 16 * c + 4 * g,
                          make_float4(oacc[c][0] * inv, oacc[c][1] * inv, oacc[c][2] * inv, oacc[c][3] * inv));
     }
+#undef FA_GLOAD
+#undef FA_LSTORE
 }
 
 // ---------------------------------------------------------------- decode
@@ -368,18 +490,24 @@ jas_status jas_attn_prefill(const void *Q, const void *K, const void *V, void *O
     JAS_CHECK(D == 32 || D == 64 || D == 128, JAS_ERR_INVALID, "jas_attn_prefill: head dim must be 32, 64 or 128");
     JAS_CHECK(dtype == JAS_F32 || dtype == JAS_BF16, JAS_ERR_INVALID, "jas_attn_prefill: dtype f32 or bf16");
     JAS_CHECK(!causal || Sk >= Sq, JAS_ERR_INVALID, "jas_attn_prefill: causal needs Sk >= Sq");
-    const long al = 4;  // every access is a 4-element vector (16 B f32, 8 B bf16)
+    // K/V/Q rows are read in 16-byte chunks (4 f32 / 8 bf16); O is written 4 elements at a time
+    const long al = dtype == JAS_BF16 ? 8 : 4;
     JAS_CHECK(q_ss % al == 0 && k_ss % al == 0 && o_ss % al == 0 && q_sh % al == 0 && k_sh % al == 0 &&
                   o_sh % al == 0 && q_sb % al == 0 && k_sb % al == 0 && o_sb % al == 0,
-              JAS_ERR_INVALID, "jas_attn_prefill: strides must be multiples of 4 elements");
+              JAS_ERR_INVALID, "jas_attn_prefill: strides must be multiples of 4 (f32) / 8 (bf16) elements");
+    JAS_CHECK((uintptr_t)Q % 16 == 0 && (uintptr_t)K % 16 == 0 && (uintptr_t)V % 16 == 0 && (uintptr_t)O % 16 == 0,
+              JAS_ERR_INVALID, "jas_attn_prefill: tensors must be 16-byte aligned");
     PrefillArgs p{Q, K, V, O, q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, o_sb, o_sh, o_ss, B, H, Sq, Sk,
                   scale * 1.4426950408889634f, causal};
-    dim3 grid(ceil_div(Sq, FA_BQ), B * H);
+    const int total = ceil_div(Sq, FA_BQ) * B * H;
+    dim3 grid((total + 7) / 8 * 8);
     hipStream_t s = stream_or_default(stream);
 #define JAS_FA(DD)                                                                                         \
     if (D == DD) {                                                                                         \
-        if (dtype == JAS_BF16) hipLaunchKernelGGL((flash_prefill_kernel<DD, true>), grid, dim3(256), 0, s, p); \
-        else hipLaunchKernelGGL((flash_prefill_kernel<DD, false>), grid, dim3(256), 0, s, p);               \
+        if (dtype == JAS_BF16)                                                                              \
+            hipLaunchKernelGGL((flash_prefill_kernel<DD, true, (DD <= 64 ? 128 : 64)>), grid, dim3(64 * FA_NW), 0, s, p); \
+        else                                                                                                \
+            hipLaunchKernelGGL((flash_prefill_kernel<DD, false, 64>), grid, dim3(64 * FA_NW), 0, s, p);      \
     }
     JAS_FA(32) JAS_FA(64) JAS_FA(128)
 #undef JAS_FA
