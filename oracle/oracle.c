@@ -493,9 +493,11 @@ int orc_argmax(const float *x, int n)
     return best;
 }
 
-/* y[out] = W[out][in] . x[in] (+ b), float sequential k */
+/* y[out] = W[out][in] . x[in] (+ b), float sequential k.  Rows are independent, so they
+ * are spread over threads when the caller is not already parallel (one sequence). */
 static void matvec(const float *W, const float *b, const float *x, int out, int in, float *y)
 {
+#pragma omp parallel for schedule(static) if (!omp_in_parallel() && (long)out * in > (1l << 20))
     for (int i = 0; i < out; ++i) {
         const float *w = W + (long)i * in;
         float s = 0.0f;
@@ -604,7 +606,7 @@ void orc_lm_generate(const orc_lm_cfg *cfg, const orc_lm_weights *w, int B, int 
 #else
     (void)nthreads;
 #endif
-#pragma omp parallel for schedule(dynamic)
+#pragma omp parallel for schedule(dynamic) if (B > 1)
     for (int b = 0; b < B; ++b) {
         float *hf = malloc(sizeof(float) * d), *lg = malloc(sizeof(float) * V);
         for (int t = 0; t < P - 1; ++t) lm_token(&st, b, prompt[(long)b * P + t], t, hf);
@@ -633,7 +635,7 @@ void orc_lm_last_logits(const orc_lm_cfg *cfg, const orc_lm_weights *w, int B, i
 #else
     (void)nthreads;
 #endif
-#pragma omp parallel for schedule(dynamic)
+#pragma omp parallel for schedule(dynamic) if (B > 1)
     for (int b = 0; b < B; ++b) {
         float *hf = malloc(sizeof(float) * d);
         for (int t = 0; t < T; ++t) lm_token(&st, b, ids[(long)b * T + t], t, hf);

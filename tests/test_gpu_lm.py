@@ -81,6 +81,21 @@ def test_gpt2_small_shape(jas):
     run_parity(jas, cfg, seed=3, B=2, P=24, steps=3, prompt_seed=3)
 
 
+def test_llama7b_width_two_layers(jas):
+    # config 5 width (d 4096, 32 heads of 128, SwiGLU 11008, RMSNorm 1e-6, RoPE 1e4, vocab
+    # 32000, seed 4) at 2 of its 32 layers: every per-layer kernel runs at its real shape;
+    # depth only repeats them (the oracle at 32 layers would take minutes per token)
+    cfg = jas.LmConfig(1, 2, 4096, 32, 11008, 32000, 64, 2, 1e-6, 10000.0)
+    run_parity(jas, cfg, seed=4, B=2, P=12, steps=3, prompt_seed=4)
+
+
+def test_llama7b_full_depth(jas):
+    # config 5 itself: all 32 layers of the LLaMA-7B shape, weights N(0, 0.02) from seed 4,
+    # one 16-token prompt (seed 4), 3 greedy steps -- 26 GB of weights read back for the oracle
+    cfg = jas.LmConfig(1, 32, 4096, 32, 11008, 32000, 32, 1, 1e-6, 10000.0)
+    run_parity(jas, cfg, seed=4, B=1, P=16, steps=3, prompt_seed=4)
+
+
 def test_kv_cache_equals_recompute(jas):
     # jasmine's decode (transformer_test.hpp:231-238) recomputes the whole prefix each step;
     # the KV-cache step must give the last column of that recompute.
