@@ -181,6 +181,81 @@ def run_kernel_legs(jas, reps=10):
     return out
 
 
+# ---------------------------------------------------------------- rocprofv3 summaries
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "llama7b_decode_b16_traffic.json")
+KCLASS = {"attention": ("attn_decode_kernel<128>", "attn_decode_merge_kernel<128>"), "weight_gemm": ("skinny_kernel<",)}
+
+
+def _pmc_per_kernel(csv_path, counter):
+    """{kernel name: [value per dispatch]} for one derived counter of a rocprofv3 --pmc run."""
+    import csv
+    per = {}
+    for r in csv.DictReader(open(csv_path)):
+        if r["Counter_Name"] != counter:
+            continue
+        per.setdefault(r["Kernel_Name"], {}).setdefault(r["Dispatch_Id"], 0.0)
+        per[r["Kernel_Name"]][r["Dispatch_Id"]] += float(r["Counter_Value"])
+    return {k: list(v.values()) for k, v in per.items()}
+
+
+def summarize_pmc(fetch_csv, write_csv, cfetch_csv, cwrite_csv, args):
+    """HBM traffic per decode launch from FETCH_SIZE / WRITE_SIZE runs of this bench,
+    calibrated by the same counters on a plain device copy of COPY_BYTES."""
+    import numpy as np
+    f, w = _pmc_per_kernel(fetch_csv, "FETCH_SIZE"), _pmc_per_kernel(write_csv, "WRITE_SIZE")
+    cf, cw = _pmc_per_kernel(cfetch_csv, "FETCH_SIZE"), _pmc_per_kernel(cwrite_csv, "WRITE_SIZE")
+    copy = [k for k in cf if "copyBuffer" in k or "copy" in k.lower()]
+    kib = COPY_BYTES / 1024.0
+    fcal = kib / np.median(cf[copy[0]]) if copy else 1.0
+    wcal = kib / np.median(cw[copy[0]]) if copy else 1.0
+    out = {"fetch_scale": fcal, "write_scale": wcal, "copy_bytes": COPY_BYTES, "classes": {}}
+    for cls, pats in KCLASS.items():
+        tot, n = 0.0, None
+        for k in f:
+            if any(pt in k for pt in pats):
+                fk, wk = f[k], w.get(k, [0.0])
+                tot += (np.mean(fk) * fcal + np.mean(wk) * wcal) * 1024.0 * len(fk)
+                if pats[0] in k:
+                    n = (n or 0) + len(fk)
+        if n:
+            out["classes"][cls] = {"bytes_per_launch": tot / n, "launches": n}
+    B, P, L, H, dh = args.batch, args.prompt, 32, 32, 128
+    first, last = P, P + args.warmup + 2 * args.steps - 1
+    mean_ctx = (first + 1 + last + 1) / 2.0
+    out["algorithmic"] = {"attention": B * H * mean_ctx * dh * 8, "weight_gemm": None}
+    out["run"] = {"batch": B, "prompt": P, "steps": args.steps, "warmup": args.warmup}
+    return out
+
+
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration():
+    """A plain device-to-device copy of COPY_BYTES (the copy-kernel reference for FETCH_SIZE /
+    WRITE_SIZE), five times."""
+    import jasmine_amd as jas
+    jas.check(jas.lib.jas_init(0))
+    a, b = jas.DeviceArray(COPY_BYTES // 4), jas.DeviceArray(COPY_BYTES // 4)
+    a.zero()
+    for _ in range(5):
+        jas.check(jas.lib.jas_memcpy_d2d(b.p, a.p, COPY_BYTES, None))
+    jas.check(jas.lib.jas_synchronize(None))
+    print(json.dumps({"copy_calibration_bytes": COPY_BYTES, "repeats": 5}))
+
+
+def load_traffic(args, dom_kernel_class):
+    """Measured HBM bytes per launch of the dominant class, if a summary for this exact
+    workload (batch, prompt, steps, warmup) was committed; else None."""
+    try:
+        t = json.load(open(TRAFFIC_FILE))
+    except (OSError, ValueError):
+        return None
+    if t.get("run") != {"batch": args.batch, "prompt": args.prompt, "steps": args.steps, "warmup": args.warmup}:
+        return None
+    c = t.get("classes", {}).get(dom_kernel_class)
+    return None if c is None else round(c["bytes_per_launch"])
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -191,7 +266,17 @@ def main():
     ap.add_argument("--no-gpt2", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true", help="skip the config 2/3 kernel lines")
+    ap.add_argument("--copy-calib", action="store_true", help="only run the copy used to calibrate PMC bytes")
+    ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV", "COPY_WRITE_CSV"),
+                    help="write the traffic summary from rocprofv3 --pmc counter_collection.csv files")
     args = ap.parse_args()
+    if args.copy_calib:
+        copy_calibration()
+        return
+    if args.summarize_pmc:
+        out = summarize_pmc(*args.summarize_pmc, args)
+        print(json.dumps(out, indent=1))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (run with --gpus 1)",
               file=sys.stderr)
@@ -252,14 +337,15 @@ def main():
     step_bytes = (w_bytes + kv_bytes) / args.steps
     classes = [
         {"kernel": "skinny_kernel (decode weight GEMMs: QKV+RoPE+KV append, O+residual, SwiGLU, down+residual, LM head)",
-         "achieved": gemm_gbs, "launches": cnt[0], "gpu_ms": ms[0], "bytes": w_bytes},
+         "achieved": gemm_gbs, "launches": cnt[0], "gpu_ms": ms[0], "bytes": w_bytes, "cls": "weight_gemm"},
         {"kernel": "attn_decode_kernel (split-K KV-cache attention + merge)",
-         "achieved": attn_gbs, "launches": cnt[1], "gpu_ms": ms[1], "bytes": kv_bytes},
+         "achieved": attn_gbs, "launches": cnt[1], "gpu_ms": ms[1], "bytes": kv_bytes, "cls": "attention"},
     ]
     dom = max(classes, key=lambda c: c["gpu_ms"])
     other = min(classes, key=lambda c: c["gpu_ms"])
     roof = {"bound": "hbm", "achieved": round(dom["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom["kernel"],
+            "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4), "traffic": load_traffic(args, dom["cls"]),
+            "kernel": dom["kernel"],
             "bytes_per_launch": dom["bytes"] / max(dom["launches"], 1),
             "avg_launch_us": 1e3 * dom["gpu_ms"] / max(dom["launches"], 1)}
     step_roofline_frac = (step_bytes_timed / (dt / args.steps)) / 1e9 / HBM_PEAK_GBS
