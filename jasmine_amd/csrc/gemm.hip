@@ -57,7 +57,7 @@ struct TileLoader {
                 int idx = tid + q * 256, i = idx >> 6, ln = idx & 63;
                 long rt = o0 / 16 + i;
                 float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (rt * 16 < O) v = *(const float4 *)(X + ((rt * (K >> 4) + (k0 >> 4)) * 64 + ln) * 4);
+                if (rt * 16 < O) v = *(const float4 *)(X + weight_tile_offset(rt, k0 >> 4, K >> 4, (O + 15) >> 4) + ln * 4);
                 r[4 * q] = v.x; r[4 * q + 1] = v.y; r[4 * q + 2] = v.z; r[4 * q + 3] = v.w;
             }
         } else if (MODE == LM_OC) {
@@ -276,13 +276,17 @@ skinny_kernel(const float *__restrict__ W, const float *__restrict__ W2, const f
     const int m0 = blockIdx.x * (DUAL ? 16 : NT * 16);
     const int K16 = K >> 4;
 
+    const long RG = (M + 15) >> 4;  // row tiles of the packed layout
     const float *wp[NT];
+    long wrt[NT];  // packed: this tile's row-tile index
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const float *base = (DUAL && t == 1) ? W2 : W;
         if (PACKED) {
-            const long rt = m0 / 16 + (DUAL ? 0 : t);
-            wp[t] = base + (rt * K16 * 64 + lane) * 4;
+            // tiles past the last row tile (M not a multiple of NT*16) re-read the last one;
+            // their rows are >= M and the epilogue discards them
+            wrt[t] = min((long)(m0 / 16 + (DUAL ? 0 : t)), RG - 1);
+            wp[t] = base + lane * 4;
         } else {
             int row = m0 + (DUAL ? 0 : t * 16) + r16;
             row = row < M ? row : M - 1;  // clamped rows are computed and discarded
@@ -313,7 +317,8 @@ skinny_kernel(const float *__restrict__ W, const float *__restrict__ W2, const f
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 if (PACKED)
-                    wv[t][q] = cin ? __builtin_nontemporal_load((const floatx4 *)(wp[t] + (long)(4 * c + q) * 256))
+                    wv[t][q] = cin ? __builtin_nontemporal_load(
+                                         (const floatx4 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG)))
                                    : floatx4{0.f, 0.f, 0.f, 0.f};
                 else
                     wv[t][q] = kin ? __builtin_nontemporal_load((const floatx4 *)(wp[t] + k + 16 * q))
@@ -490,6 +495,8 @@ jas_status skinny_gemm(const float *W, const float *W2, const float *X, long ldx
     // 1024-thread workgroups get 128 VGPRs: depth 4 would spill
     JAS_SK(1, 16, false, true, 2) JAS_SK(1, 16, false, true, 3) JAS_SK(1, 16, false, false, 2)
     JAS_SK(1, 16, false, false, 3)
+    // four row tiles per workgroup share each activation chunk (packed weights only)
+    JAS_SK(4, 4, false, true, 2) JAS_SK(4, 4, false, true, 3) JAS_SK(4, 8, false, true, 2)
 #undef JAS_SK_P
 #undef JAS_SK_D
 #undef JAS_SK
@@ -503,7 +510,7 @@ __global__ void weight_pack_kernel(const float *__restrict__ src, float *__restr
     long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= (long)Mp * K) return;
     int r, k;
-    weight_pack_coords(p, K, &r, &k);
+    weight_pack_coords(p, K, Mp >> 4, &r, &k);
     if (unpack) {
         if (r < M) dst[(long)r * K + k] = src[p];
     } else {
@@ -516,7 +523,7 @@ __global__ void fill_normal_packed_kernel(float *x, int M, int Mp, int K, uint64
     long stride = (long)gridDim.x * blockDim.x;
     for (long p = (long)blockIdx.x * blockDim.x + threadIdx.x; p < (long)Mp * K; p += stride) {
         int r, k;
-        weight_pack_coords(p, K, &r, &k);
+        weight_pack_coords(p, K, Mp >> 4, &r, &k);
         if (r >= M) {
             x[p] = 0.0f;
             continue;

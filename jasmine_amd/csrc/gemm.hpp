@@ -46,26 +46,35 @@ SkinnyTuning skinny_default_tuning(int M, int K, bool dual);
 // K splits (<= 8, all non-empty) for an EPI_PARTIAL launch of an [M][K] weight
 int skinny_pick_ksplit(int M, int K);
 
-// Packed weight layout for a [M][K] matrix (K % 16 == 0, rows padded to Mp = ceil16(M)
-// with zeros): element (r, k) lives at
-//   ((r/16 * K/16 + k/16) * 64 + lane) * 4 + k%4,  lane = r%16 + 16 * ((k%16)/4)
-// i.e. every 16x16 block is the 64 float4 A-operand registers of one MFMA wave, in lane
-// order, and the blocks of a 16-row tile follow each other along K.
-__host__ __device__ inline long weight_pack_offset(int r, int k, int K)
+// Packed (MFMA-native) weight layout of an [M][K] matrix, rows padded to RG = ceil(M/16)
+// row tiles, K % 16 == 0.  A 16 x 16 tile (row tile rt, K block kb) is 256 floats: lane
+// l = r%16 + 16*((k%16)/4) holds k%4 = 0..3 -- exactly the A-operand float4 of an MFMA wave,
+// one contiguous 1 KB load.  Tiles are ordered CHUNK-MAJOR: K is cut into chunks of 4 blocks
+// (64 columns); chunk c holds the tiles (rt, 4c..4c+3) of every row tile, row tile by row
+// tile.  Workgroups that stream neighbouring row tiles therefore read neighbouring addresses
+// at the same time, which keeps DRAM pages open (a row-tile-major layout, where every
+// workgroup streams its own distant range, reaches about half the bandwidth).
+__host__ __device__ inline long weight_tile_offset(long rt, int kb, int K16, long RG)
 {
-    const long blk = (long)(r >> 4) * (K >> 4) + (k >> 4);
-    const int lane = (r & 15) + 16 * ((k & 15) >> 2);
-    return (blk * 64 + lane) * 4 + (k & 3);
+    const int c = kb >> 2, q = kb & 3, nb = K16 - 4 * c < 4 ? K16 - 4 * c : 4;  // blocks in chunk c
+    return ((long)c * 4 * RG + rt * nb + q) * 256;
 }
-__host__ __device__ inline void weight_pack_coords(long p, int K, int *r, int *k)
+__host__ __device__ inline long weight_pack_offset(int r, int k, int K, long RG)
+{
+    const int lane = (r & 15) + 16 * ((k & 15) >> 2);
+    return weight_tile_offset(r >> 4, k >> 4, K >> 4, RG) + lane * 4 + (k & 3);
+}
+__host__ __device__ inline void weight_pack_coords(long p, int K, long RG, int *r, int *k)
 {
     const long blk = p >> 8;
     const int within = (int)(p & 255), lane = within >> 2, e = within & 3;
     const int K16 = K >> 4;
-    const long rt = blk / K16;
-    const int kc = (int)(blk - rt * K16);
+    const long c = blk / (4 * RG);  // chunk: full chunks hold 4*RG tiles, the last one fewer
+    const int nb = K16 - 4 * (int)c < 4 ? K16 - 4 * (int)c : 4;
+    const long in = blk - c * 4 * RG, rt = in / nb;
+    const int q = (int)(in - rt * nb);
     *r = (int)(rt * 16 + (lane & 15));
-    *k = kc * 16 + 4 * (lane >> 4) + e;
+    *k = ((int)c * 4 + q) * 16 + 4 * (lane >> 4) + e;
 }
 // Packed B-operand (activation) layout of a [16 tokens][K] matrix: element (n, k) at
 //   ((k/16) * 64 + lane) * 4 + k%4,  lane = n + 16 * ((k%16)/4)

@@ -76,12 +76,12 @@ __global__ void swiglu_kernel(const float *__restrict__ gate, const float *__res
 // token embedding gather from a packed [V][d] table (GPT-2 ties it to the LM head)
 __global__ void embed_packed_kernel(const float *__restrict__ wte, const float *__restrict__ wpe,
                                     const int32_t *__restrict__ ids, const int32_t *__restrict__ pos,
-                                    float *__restrict__ out, int n, int d)
+                                    float *__restrict__ out, int n, int d, int V)
 {
     long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= (long)n * d) return;
     int t = (int)(g / d), e = (int)(g % d);
-    float v = wte[weight_pack_offset(ids[t], e, d)];
+    float v = wte[weight_pack_offset(ids[t], e, d, (V + 15) >> 4)];
     if (wpe) v = v + wpe[(long)pos[t] * d + e];
     out[g] = v;
 }
@@ -240,7 +240,7 @@ jas_status embed(jas_lm *lm, const int32_t *ids, const int32_t *pos, float *out,
     TRY(prof_begin(lm, 2));
     if (c.kind == 0) {  // GPT-2: the tied, packed wte plus learned positions
         hipLaunchKernelGGL(embed_packed_kernel, dim3(ceil_div((long)n * c.d_model, 256)), dim3(256), 0, lm->stream,
-                           lm->W("wte"), lm->W("wpe"), ids, pos, out, n, c.d_model);
+                           lm->W("wte"), lm->W("wpe"), ids, pos, out, n, c.d_model, c.vocab);
         JAS_LAUNCH_CHECK();
     } else {
         TRY(jas_embed(lm->W("wte"), nullptr, ids, pos, out, n, c.d_model, lm->stream));
