@@ -437,21 +437,32 @@ static void launch_skinny(const float *W, const float *W2, const float *X, long 
 
 // geometry by row count: enough workgroups to cover the 256 CUs first, then more bytes per
 // wave (two row tiles) once the row groups outnumber the CUs several times over
+// Geometry per decode shape, from a cold-weight sweep on MI355X (16 tokens, packed weights):
+//  * two row tiles per workgroup everywhere except mid-size single matrices: each activation
+//    chunk read from L2 then feeds two weight tiles (the activation reads are otherwise as
+//    large as the weight reads and cost ~10% of the bandwidth);
+//  * 4-wave workgroups with a 3-deep chunk ring for the large matrices (SwiGLU pair, LM
+//    head), 8 waves x 2 deep for the split-K residual projection with K <= 4096.
 SkinnyTuning skinny_default_tuning(int M, int K, bool dual)
 {
     SkinnyTuning t;
     const int rt = (M + 15) / 16;
-    t.nt = (!dual && rt >= 1536) ? 2 : 1;
-    t.wpb = (dual || rt >= 1536) ? 8 : (rt >= 512 ? 4 : 8);
-    t.depth = rt >= 512 ? 2 : 3;
-    (void)K;
+    if (dual || rt >= 1536) {  // SwiGLU gate/up, LM head
+        t.nt = 2; t.wpb = 4; t.depth = 3;
+    } else if (rt >= 512) {    // QKV-sized: one tile, 4 waves
+        t.nt = 1; t.wpb = 4; t.depth = 2;
+    } else {                   // d-row residual projections (split-K)
+        t.nt = 2; t.wpb = K <= 4096 ? 8 : 4; t.depth = 2;
+    }
     return t;
 }
 
+// K splits for the split-K (partial-sum) residual projections: two for K <= 4096, four above
 int skinny_pick_ksplit(int M, int K)
 {
     const int rgroups = (M + 15) / 16, nchunk = (K + 63) / 64;
-    int ks = std::max(1, std::min({1024 / std::max(rgroups, 1), nchunk / 2, 8}));
+    int ks = rgroups >= 512 ? 1 : (K <= 4096 ? 2 : 4);
+    ks = std::max(1, std::min(ks, nchunk / 2));
     const int cpb = (nchunk + ks - 1) / ks;
     return (nchunk + cpb - 1) / cpb;  // every split non-empty
 }
