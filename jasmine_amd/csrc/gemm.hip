@@ -438,31 +438,33 @@ static void launch_skinny(const float *W, const float *W2, const float *X, long 
 // geometry by row count: enough workgroups to cover the 256 CUs first, then more bytes per
 // wave (two row tiles) once the row groups outnumber the CUs several times over
 // Geometry per decode shape, from a cold-weight sweep on MI355X (16 tokens, packed weights):
-//  * two row tiles per workgroup everywhere except mid-size single matrices: each activation
-//    chunk read from L2 then feeds two weight tiles (the activation reads are otherwise as
-//    large as the weight reads and cost ~10% of the bandwidth);
-//  * 4-wave workgroups with a 3-deep chunk ring for the large matrices (SwiGLU pair, LM
-//    head), 8 waves x 2 deep for the split-K residual projection with K <= 4096.
-SkinnyTuning skinny_default_tuning(int M, int K, bool dual)
+//  * two row tiles per workgroup for the large matrices (SwiGLU pair, LM head) and for the
+//    split-K residual projections: each activation chunk read from L2 then feeds two weight
+//    tiles (activation reads otherwise equal the weight reads and cost ~10% bandwidth);
+//  * 4-wave workgroups with a 3-deep chunk ring for the large matrices, 8 waves x 2 deep for
+//    the split-K projections; single-tile geometry where that would leave too few
+//    workgroups (mid-size and small matrices without a K split).
+SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split)
 {
     SkinnyTuning t;
     const int rt = (M + 15) / 16;
+    (void)K;
     if (dual || rt >= 1536) {  // SwiGLU gate/up, LM head
         t.nt = 2; t.wpb = 4; t.depth = 3;
-    } else if (rt >= 512) {    // QKV-sized: one tile, 4 waves
-        t.nt = 1; t.wpb = 4; t.depth = 2;
-    } else {                   // d-row residual projections (split-K)
-        t.nt = 2; t.wpb = K <= 4096 ? 8 : 4; t.depth = 2;
+    } else if (split) {        // split-K residual projections
+        t.nt = 2; t.wpb = 8; t.depth = 2;
+    } else {
+        t.nt = 1; t.wpb = rt >= 512 ? 4 : 8; t.depth = rt >= 512 ? 2 : 3;
     }
     return t;
 }
 
-// K splits for the split-K (partial-sum) residual projections: two for K <= 4096, four above
+// K splits of a split-K residual projection (two row tiles per workgroup): enough splits for
+// about 256 workgroups, at most 8 and at least two 64-wide chunks per split
 int skinny_pick_ksplit(int M, int K)
 {
-    const int rgroups = (M + 15) / 16, nchunk = (K + 63) / 64;
-    int ks = rgroups >= 512 ? 1 : (K <= 4096 ? 2 : 4);
-    ks = std::max(1, std::min(ks, nchunk / 2));
+    const int wgs = ((M + 15) / 16 + 1) / 2, nchunk = (K + 63) / 64;
+    int ks = std::max(1, std::min({(256 + wgs - 1) / wgs, nchunk / 2, 8}));
     const int cpb = (nchunk + ks - 1) / ks;
     return (nchunk + cpb - 1) / cpb;  // every split non-empty
 }
@@ -480,7 +482,7 @@ jas_status skinny_gemm(const float *W, const float *W2, const float *X, long ldx
     if (epi.mode == EPI_QKV)
         JAS_CHECK(epi.d % 16 == 0 && epi.dh % 4 == 0 && M == 3 * epi.d, JAS_ERR_INVALID, "skinny_gemm: bad QKV shape");
     if (dual) JAS_CHECK(W2 != nullptr, JAS_ERR_INVALID, "skinny_gemm: SwiGLU needs both weights");
-    SkinnyTuning tu = tune ? *tune : skinny_default_tuning(M, K, dual);
+    SkinnyTuning tu = tune ? *tune : skinny_default_tuning(M, K, dual, epi.mode == EPI_PARTIAL);
     const int nt = dual ? 2 : tu.nt;
     SkinnyEpiArgs ep = epi;
     const int nchunk = (K + 63) / 64;

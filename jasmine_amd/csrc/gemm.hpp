@@ -42,7 +42,7 @@ struct SkinnyEpiArgs {
 struct SkinnyTuning {
     int nt = 1, wpb = 8, depth = 2;  // depth: chunk buffers in the load pipeline
 };
-SkinnyTuning skinny_default_tuning(int M, int K, bool dual);
+SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split = false);
 // K splits (<= 8, all non-empty) for an EPI_PARTIAL launch of an [M][K] weight
 int skinny_pick_ksplit(int M, int K);
 
