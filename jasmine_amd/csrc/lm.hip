@@ -86,6 +86,27 @@ __global__ void embed_packed_kernel(const float *__restrict__ wte, const float *
     out[g] = v;
 }
 
+// graph-replay form of set_positions_kernel: the position comes from (and advances) state[0]
+__global__ void advance_position_kernel(int32_t *state, int32_t *pos, int32_t *seqlens, int B)
+{
+    const int p = state[0];
+    const int b = threadIdx.x;
+    if (b < B) {
+        pos[b] = p;
+        seqlens[b] = p + 1;
+    }
+    __syncthreads();
+    if (b == 0) state[0] = p + 1;
+}
+
+// hist[(pos - state[1]) * B + b] = ids[b] for the step at position pos[0] (graph replay)
+__global__ void record_ids_kernel(const int32_t *ids, int32_t *hist, const int32_t *pos, const int32_t *state, int B,
+                                  int cap)
+{
+    const int b = threadIdx.x, step = pos[0] - state[1];
+    if (b < B && step >= 0 && step < cap) hist[(long)step * B + b] = ids[b];
+}
+
 __global__ void copy_ids_kernel(const int32_t *src, int32_t *dst, int B)
 {
     int b = blockIdx.x * blockDim.x + threadIdx.x;
@@ -109,6 +130,13 @@ struct jas_lm {
     float *x = nullptr, *h = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr;
     int32_t *ids = nullptr, *pos = nullptr, *seqlens = nullptr, *hist = nullptr;
     int hist_cap = 0;
+    // device-side decode state for graph replay: [0] next position, [1] first position of
+    // the current jas_lm_generate call (its id history is indexed from there)
+    int32_t *dstate = nullptr;
+    // one decode step captured as a HIP graph (for this batch size and id-history buffer)
+    hipGraphExec_t graph = nullptr;
+    int graph_B = 0, graph_cap = 0;
+    const int32_t *graph_hist = nullptr;
     void *attn_ws = nullptr;
     float *part = nullptr;  // K-split partials of the residual projections [split][16][d]
     int ks_o = 1, ks_d = 1;
@@ -249,13 +277,21 @@ jas_status embed(jas_lm *lm, const int32_t *ids, const int32_t *pos, float *out,
 }
 
 // one decode step for lm->B sequences: d_ids in, argmax written back into d_ids
-jas_status decode_step(jas_lm *lm)
+// One decode step for the active batch.  device_pos: take the position from the device
+// state (graph capture/replay) instead of the host counter.  Attention is launched for the
+// full cache length (max_ctx) either way -- its splits past a sequence's length are empty --
+// so the launch shape, and the arithmetic, do not depend on the step.
+jas_status decode_step(jas_lm *lm, bool device_pos)
 {
     const jas_lm_config &c = lm->cfg;
     const int B = lm->B, d = c.d_model, F = c.d_ff, H = c.n_head, dh = lm->dh(), V = c.vocab;
-    JAS_CHECK(lm->position < c.max_ctx, JAS_ERR_RANGE, "jas_lm_decode: KV cache full (max_ctx reached)");
+    JAS_CHECK(device_pos || lm->position < c.max_ctx, JAS_ERR_RANGE,
+              "jas_lm_decode: KV cache full (max_ctx reached)");
     hipStream_t s = lm->stream;
-    hipLaunchKernelGGL(set_positions_kernel, dim3(1), dim3(256), 0, s, lm->pos, lm->seqlens, B, lm->position);
+    if (device_pos)
+        hipLaunchKernelGGL(advance_position_kernel, dim3(1), dim3(64), 0, s, lm->dstate, lm->pos, lm->seqlens, B);
+    else
+        hipLaunchKernelGGL(set_positions_kernel, dim3(1), dim3(256), 0, s, lm->pos, lm->seqlens, B, lm->position);
     TRY(embed(lm, lm->ids, lm->pos, lm->x, B));
     // The projections that feed the residual stream (O and down/proj) run K-split and leave
     // their partial sums in lm->part; the next norm kernel adds them (plus the bias) to x.
@@ -282,7 +318,7 @@ jas_status decode_step(jas_lm *lm)
         TRY(proj(lm, lm->LW("w_qkv", l), lm->h, B, 3 * d, d, eq));
         TRY(prof_begin(lm, 1));
         TRY(attn_decode_impl(lm->q, lm->kc + l * lm->kv_layer, lm->vc + l * lm->kv_layer, lm->att, lm->seqlens, B, H,
-                             dh, lm->position + 1, lm->kv_sb, lm->kv_sh, 1.0f / sqrtf((float)dh), lm->attn_ws, s, d));
+                             dh, c.max_ctx, lm->kv_sb, lm->kv_sh, 1.0f / sqrtf((float)dh), lm->attn_ws, s, d));
         TRY(prof_end(lm));
         SkinnyEpiArgs eo;
         eo.mode = EPI_PARTIAL;
@@ -334,7 +370,7 @@ jas_status decode_step(jas_lm *lm)
     TRY(prof_begin(lm, 2));
     TRY(jas_argmax(lm->logits, B, V, V, lm->ids, s));
     TRY(prof_end(lm));
-    lm->position += 1;
+    if (!device_pos) lm->position += 1;
     return JAS_OK;
 }
 
@@ -430,6 +466,7 @@ jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out)
     if (st == JAS_OK) st = jas_malloc((void **)&lm->ids, 64 * sizeof(int32_t));
     if (st == JAS_OK) st = jas_malloc((void **)&lm->pos, 64 * sizeof(int32_t));
     if (st == JAS_OK) st = jas_malloc((void **)&lm->seqlens, 64 * sizeof(int32_t));
+    if (st == JAS_OK) st = jas_malloc((void **)&lm->dstate, 2 * sizeof(int32_t));
     lm->attn_ws_bytes = jas_attn_decode_workspace(Bm, c.n_head, dh, c.max_ctx);
     for (int b = 1; b < Bm; ++b)  // workspace must cover every batch size actually used
         lm->attn_ws_bytes = std::max(lm->attn_ws_bytes, jas_attn_decode_workspace(b, c.n_head, dh, c.max_ctx));
@@ -451,7 +488,8 @@ jas_status jas_lm_destroy(jas_lm *lm)
 {
     if (!lm) return JAS_OK;
     if (lm->stream) (void)hipStreamSynchronize(lm->stream);
-    void *ptrs[] = {lm->arena, lm->kc, lm->vc, lm->x, lm->h, lm->q, lm->att, lm->ff, lm->logits, lm->ids, lm->pos,
+    if (lm->graph) (void)hipGraphExecDestroy(lm->graph);
+    void *ptrs[] = {lm->dstate, lm->arena, lm->kc, lm->vc, lm->x, lm->h, lm->q, lm->att, lm->ff, lm->logits, lm->ids, lm->pos,
                     lm->seqlens, lm->hist, lm->attn_ws, lm->part, lm->pX, lm->pH, lm->pQKV, lm->pATT, lm->pG, lm->pU, lm->pFF,
                     lm->pIds, lm->pPos};
     for (void *p : ptrs)
@@ -618,11 +656,49 @@ jas_status jas_lm_decode(jas_lm *lm, const int32_t *h_ids, int32_t *h_next, floa
             JAS_CHECK(h_ids[b] >= 0 && h_ids[b] < lm->cfg.vocab, JAS_ERR_INVALID, "jas_lm_decode: token id out of range");
         TRY(jas_memcpy_h2d(lm->ids, h_ids, lm->B * sizeof(int32_t), lm->stream));
     }
-    TRY(decode_step(lm));
+    TRY(decode_step(lm, false));
     if (h_next) TRY(jas_memcpy_d2h(h_next, lm->ids, lm->B * sizeof(int32_t), lm->stream));
     if (h_logits) TRY(jas_memcpy_d2h(h_logits, lm->logits, (size_t)lm->B * lm->cfg.vocab * sizeof(float), lm->stream));
     return JAS_OK;
 }
+
+namespace {
+// (Re)capture the graph-mode decode step plus its id recording when the batch size or the
+// id-history buffer changed.  No memset or allocation happens inside the captured region.
+jas_status capture_decode_graph(jas_lm *lm)
+{
+    // (a regrown history buffer can come back at the old address: compare its capacity too)
+    if (lm->graph && lm->graph_B == lm->B && lm->graph_hist == lm->hist && lm->graph_cap == lm->hist_cap)
+        return JAS_OK;
+    if (lm->graph) {
+        (void)hipGraphExecDestroy(lm->graph);
+        lm->graph = nullptr;
+    }
+    hipStream_t s = lm->stream;
+    JAS_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    jas_status st = decode_step(lm, true);
+    if (st == JAS_OK)
+        hipLaunchKernelGGL(record_ids_kernel, dim3(1), dim3(64), 0, s, lm->ids, lm->hist, lm->pos, lm->dstate, lm->B,
+                           lm->hist_cap);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(s, &g);  // always end the capture, also after a failure
+    if (st != JAS_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return st;
+    }
+    if (e != hipSuccess) return fail(JAS_ERR_HIP, std::string("jas_lm_generate: graph capture: ") + hipGetErrorString(e));
+    e = hipGraphInstantiate(&lm->graph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+        lm->graph = nullptr;
+        return fail(JAS_ERR_HIP, std::string("jas_lm_generate: graph instantiate: ") + hipGetErrorString(e));
+    }
+    lm->graph_B = lm->B;
+    lm->graph_hist = lm->hist;
+    lm->graph_cap = lm->hist_cap;
+    return JAS_OK;
+}
+} // namespace
 
 jas_status jas_lm_generate(jas_lm *lm, int steps, int32_t *h_ids)
 {
@@ -635,10 +711,20 @@ jas_status jas_lm_generate(jas_lm *lm, int steps, int32_t *h_ids)
         TRY(jas_malloc((void **)&lm->hist, (size_t)steps * 16 * sizeof(int32_t)));
         lm->hist_cap = steps;
     }
-    for (int st = 0; st < steps; ++st) {
-        TRY(decode_step(lm));
-        hipLaunchKernelGGL(copy_ids_kernel, dim3(1), dim3(64), 0, lm->stream, lm->ids, lm->hist + (long)st * lm->B,
-                           lm->B);
+    if (lm->prof) {  // per-launch events: run the step eagerly
+        for (int st = 0; st < steps; ++st) {
+            TRY(decode_step(lm, false));
+            hipLaunchKernelGGL(copy_ids_kernel, dim3(1), dim3(64), 0, lm->stream, lm->ids, lm->hist + (long)st * lm->B,
+                               lm->B);
+        }
+    } else if (steps > 0) {
+        // one decode step as a HIP graph, replayed `steps` times; the position lives on the
+        // device and advances inside the step, so the same graph serves every step
+        TRY(capture_decode_graph(lm));
+        const int32_t st0[2] = {lm->position, lm->position};
+        TRY(jas_memcpy_h2d(lm->dstate, st0, sizeof st0, lm->stream));
+        for (int st = 0; st < steps; ++st) JAS_HIP(hipGraphLaunch(lm->graph, lm->stream));
+        lm->position += steps;
     }
     if (h_ids && steps) TRY(jas_memcpy_d2h(h_ids, lm->hist, (size_t)steps * lm->B * sizeof(int32_t), lm->stream));
     JAS_HIP(hipStreamSynchronize(lm->stream));

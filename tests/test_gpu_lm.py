@@ -96,6 +96,40 @@ def test_llama7b_full_depth(jas):
     run_parity(jas, cfg, seed=4, B=1, P=16, steps=3, prompt_seed=4)
 
 
+@pytest.mark.parametrize("kind", [0, 1])
+def test_generate_graph_replay_matches_eager(jas, kind):
+    """jas_lm_generate replays one captured decode step as a HIP graph.  Every replay, also
+    after eager steps and host synchronisations in between, must reproduce the eager step
+    bit for bit: ids of every step and the logits that follow."""
+    cfg = jas.LmConfig(kind, 2, 128, 4, 256, 300, 64, 3, 1e-5 if kind == 0 else 1e-6, 10000.0)
+    prompt = randint((3, 11), 300, 11)
+
+    def fresh():
+        lm = jas.Lm(cfg)
+        lm.init_random(11, 0.02)
+        first, _ = lm.prefill(prompt)
+        return lm, first
+
+    g, first_g = fresh()
+    ids = [first_g[:, None]]
+    ids.append(g.generate(4, 3).T)                  # graph: 4 replays
+    ids.append(g.decode(None, B=3)[0][:, None])     # eager step in between
+    ids.append(g.generate(3, 3).T)                  # graph again (device position resynced)
+    ids.append(g.decode(None, B=3)[0][:, None])
+    ids.append(g.generate(5, 3).T)                  # longer run: history buffer regrown, re-captured
+    _, lg_g = g.decode(None, B=3, want_logits=True)
+    ids_g = np.concatenate(ids, 1)
+
+    e, first_e = fresh()
+    ids_e = [first_e]
+    for _ in range(ids_g.shape[1] - 1):
+        ids_e.append(e.decode(None, B=3)[0])
+    _, lg_e = e.decode(None, B=3, want_logits=True)
+    assert np.array_equal(ids_g, np.stack(ids_e, 1))
+    assert np.array_equal(lg_g, lg_e)
+    assert g.position == e.position
+
+
 def test_kv_cache_equals_recompute(jas):
     # jasmine's decode (transformer_test.hpp:231-238) recomputes the whole prefix each step;
     # the KV-cache step must give the last column of that recompute.
