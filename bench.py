@@ -83,12 +83,13 @@ def cpu_baseline(step_flops, B):
                       f"({step_flops / 1e9:.1f} GFLOP: all projections + attention + LM head)"}
 
 
-def run_gpt2(jas, steps=32, warmup=4):
+def run_gpt2(jas, steps=32, warmup=4, graph=True):
     """Config 4 shape: GPT-2-small, batch 8, 512-token prompts; returns decode tok/s."""
     from oracle_lib import randint
     B, P = 8, 512
     cfg = jas.LmConfig(0, 12, 768, 12, 3072, 50257, 1024, B, 1e-5, 10000.0)
     lm = jas.Lm(cfg)
+    lm.use_graph(graph)
     lm.init_random(3, 0.02)
     lm.prefill(randint((B, P), 50257, 3))
     lm.generate(warmup, B)
@@ -266,6 +267,8 @@ def main():
     ap.add_argument("--no-gpt2", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true", help="skip the config 2/3 kernel lines")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="decode with eager launches instead of graph replay (same kernels; for profilers)")
     ap.add_argument("--copy-calib", action="store_true", help="only run the copy used to calibrate PMC bytes")
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV", "COPY_WRITE_CSV"),
                     help="write the traffic summary from rocprofv3 --pmc counter_collection.csv files")
@@ -301,6 +304,8 @@ def main():
     cfg = llama_cfg(jas, B, ctx)
     log(f"[bench] creating LLaMA-7B-shape fp32 model, batch {B}, ctx {ctx}")
     lm = jas.Lm(cfg)
+    if args.no_graph:
+        lm.use_graph(False)
     t0 = time.perf_counter()
     lm.init_random(4, 0.02)
     log(f"[bench] weights initialised in {time.perf_counter() - t0:.1f} s")
@@ -357,7 +362,7 @@ def main():
     if not args.no_gpt2:
         lm.close()
         try:
-            g_tok, g_ms = run_gpt2(jas)
+            g_tok, g_ms = run_gpt2(jas, graph=not args.no_graph)
             gpt2 = {"decode_tok_s": round(g_tok, 1), "ms_per_step": round(g_ms, 3),
                     "workload": "config4: GPT-2-small fp32, batch 8, 512-token prompts, greedy decode"}
         except Exception as e:  # the headline number stands on its own

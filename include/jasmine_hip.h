@@ -268,6 +268,11 @@ jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_
 jas_status jas_lm_decode(jas_lm *lm, const int32_t *h_ids, int32_t *h_next, float *h_logits);
 /* Run `steps` greedy decode steps without host round trips; ids out [steps][B] (host). */
 jas_status jas_lm_generate(jas_lm *lm, int steps, int32_t *h_ids);
+/* jas_lm_generate replays one decode step captured as a HIP graph (default, enable = 1);
+ * enable = 0 launches the same kernels eagerly each step (identical results).  No
+ * counterpart in the reference: an execution-mode switch, e.g. for tools that cannot
+ * follow graph launches. */
+jas_status jas_lm_use_graph(jas_lm *lm, int enable);
 /* Current sequence length (tokens in the KV cache). */
 int jas_lm_position(jas_lm *lm);
 jas_stream_t jas_lm_stream(jas_lm *lm);

@@ -80,6 +80,7 @@ _sigs = {
     "jas_lm_decode": [VP, IP, IP, FP],
     "jas_lm_generate": [VP, I, IP],
     "jas_lm_profile": [VP, I, C.POINTER(C.c_double), C.POINTER(C.c_long)],
+    "jas_lm_use_graph": [VP, I],
 }
 for _n, _a in _sigs.items():
     getattr(lib, _n).argtypes = _a
@@ -230,6 +231,9 @@ class Lm:
     @property
     def position(self):
         return lib.jas_lm_position(self.h)
+
+    def use_graph(self, enable):
+        check(lib.jas_lm_use_graph(self.h, int(enable)))
 
     def profile(self, enable):
         ms = (C.c_double * 3)()

@@ -135,6 +135,7 @@ struct jas_lm {
     int32_t *dstate = nullptr;
     // one decode step captured as a HIP graph (for this batch size and id-history buffer)
     hipGraphExec_t graph = nullptr;
+    bool use_graph = true;
     int graph_B = 0, graph_cap = 0;
     const int32_t *graph_hist = nullptr;
     void *attn_ws = nullptr;
@@ -711,7 +712,7 @@ jas_status jas_lm_generate(jas_lm *lm, int steps, int32_t *h_ids)
         TRY(jas_malloc((void **)&lm->hist, (size_t)steps * 16 * sizeof(int32_t)));
         lm->hist_cap = steps;
     }
-    if (lm->prof) {  // per-launch events: run the step eagerly
+    if (lm->prof || !lm->use_graph) {  // per-launch events, or graphs switched off: eager steps
         for (int st = 0; st < steps; ++st) {
             TRY(decode_step(lm, false));
             hipLaunchKernelGGL(copy_ids_kernel, dim3(1), dim3(64), 0, lm->stream, lm->ids, lm->hist + (long)st * lm->B,
@@ -732,6 +733,13 @@ jas_status jas_lm_generate(jas_lm *lm, int steps, int32_t *h_ids)
 }
 
 int jas_lm_position(jas_lm *lm) { return lm ? lm->position : -1; }
+
+jas_status jas_lm_use_graph(jas_lm *lm, int enable)
+{
+    JAS_CHECK(lm, JAS_ERR_INVALID, "jas_lm_use_graph: null model");
+    lm->use_graph = enable != 0;
+    return JAS_OK;
+}
 jas_stream_t jas_lm_stream(jas_lm *lm) { return lm ? (jas_stream_t)lm->stream : nullptr; }
 
 jas_status jas_lm_profile(jas_lm *lm, int enable, double *ms_by_class, long *launches_by_class)
