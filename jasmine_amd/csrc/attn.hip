@@ -101,7 +101,9 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
     static_assert(NCH % NT == 0 || NLD == 1, "tile/thread mismatch");
     // two tile buffers: tile t+1 is written while tile t is read, one barrier per tile
     __shared__ __attribute__((aligned(16))) T Ks[2][BK * KLD];
-    __shared__ __attribute__((aligned(16))) T Vt[2][D * VLD];
+    // V: transposed [D][BK] for fp32; row-major [BK][D] for bf16, whose P.V operand is
+    // gathered with the LDS transpose read (ds_read_b64_tr_b16)
+    __shared__ __attribute__((aligned(16))) T Vt[2][BF16 ? BK * KLD : D * VLD];
 
     const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
@@ -178,12 +180,11 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
         const int idx = tid + it * NT, key = idx / CPR, ch = idx % CPR;                    \
         if (NCH % NT != 0 && idx >= NCH) break;                                            \
         *(u32x4 *)(&Ks[BUF][key * KLD + ch * EPC]) = kreg[it];                             \
-        const u32x4 vw = vreg[it];                                                         \
-        _Pragma("unroll") for (int t = 0; t < EPC; ++t)                                    \
-        {                                                                                  \
-            if constexpr (BF16)                                                            \
-                Vt[BUF][(ch * EPC + t) * VLD + key] = (uint16_t)(vw[t / 2] >> (16 * (t & 1))); \
-            else                                                                           \
+        if constexpr (BF16) {                                                              \
+            *(u32x4 *)(&Vt[BUF][key * KLD + ch * EPC]) = vreg[it];                         \
+        } else {                                                                           \
+            const u32x4 vw = vreg[it];                                                     \
+            _Pragma("unroll") for (int t = 0; t < EPC; ++t)                                \
                 Vt[BUF][(ch * EPC + t) * VLD + key] = __uint_as_float(vw[t]);              \
         }                                                                                  \
     }
@@ -209,15 +210,41 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
 
         // S^T tile: lane holds S^T[key = kv0 + 16j + 4g + r][query = qi] (raw scores)
         floatx4 s[NJ];
+        // bf16: every LDS fragment of the tile is requested up front -- K for S^T, and V for
+        // the second product, whose reads then complete behind the S products and the softmax
+        bf16x8 kfr[BF16 ? NJ : 1][BF16 ? D / 32 : 1];
+        bf16x8 vfr[BF16 ? NC : 1][BF16 ? NJ / 2 : 1];
+        if constexpr (BF16) {
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int c = 0; c < D / 32; ++c)
+                    kfr[j][c] = *(const bf16x8 *)(Kc + (16 * j + r16) * KLD + 32 * c + 8 * g);
+            // B operand of O = P V for key block m, head-dim block c: lane (n = l%16, g) needs
+            // V[key][16c + n] for keys 32m + 4g + 0..3 and 32m + 16 + 4g + 0..3.  The transpose
+            // read hands lane n of each 16-lane group element n%4 of the 4-element chunks that
+            // lanes n/4 + 4e address (e = 0..3), so lane i addresses row (key base + i/4),
+            // columns 16c + 4(i%4) .. +3.
+            typedef short s16x4 __attribute__((ext_vector_type(4)));
+            typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int m = 0; m < NJ / 2; ++m) {
+                    const uint16_t *v0 = Vc + (32 * m + 4 * g + (r16 >> 2)) * KLD + 16 * c + 4 * (r16 & 3);
+                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)v0);
+                    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(v0 + 16 * KLD));
+                    vfr[c][m] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                }
+        }
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
             s[j] = floatx4{0.f, 0.f, 0.f, 0.f};
             if constexpr (BF16) {
 #pragma unroll
-                for (int c = 0; c < D / 32; ++c) {
-                    bf16x8 kf = *(const bf16x8 *)(Kc + (16 * j + r16) * KLD + 32 * c + 8 * g);
-                    s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qb16[c], s[j], 0, 0, 0);
-                }
+                for (int c = 0; c < D / 32; ++c)
+                    s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kfr[j][c], qb16[c], s[j], 0, 0, 0);
             } else {
 #pragma unroll
                 for (int c = 0; c < NC; ++c) {
@@ -264,8 +291,18 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
         m_run = m_new;
         // rescale the accumulator only when some query's max moved (wave-uniform test)
         if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
+            if constexpr (BF16) {
+                // bf16 accumulates O (not O^T): oacc[c][r] is query 4g + r, whose factor lives
+                // in lane 4g + r (the lane that owns that query's scores)
+                floatx4 cr;
 #pragma unroll
-            for (int c = 0; c < NC; ++c) oacc[c] *= corr;
+                for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 4 * g + r, WAVE);
+#pragma unroll
+                for (int c = 0; c < NC; ++c) oacc[c] *= cr;
+            } else {
+#pragma unroll
+                for (int c = 0; c < NC; ++c) oacc[c] *= corr;
+            }
         }
 
         if constexpr (BF16) {
@@ -280,13 +317,8 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
 #pragma unroll
             for (int c = 0; c < NC; ++c)
 #pragma unroll
-                for (int m = 0; m < NJ / 2; ++m) {
-                    const uint16_t *vr = Vc + (16 * c + r16) * VLD + 32 * m + 4 * g;
-                    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-                    const u32x2 lo = *(const u32x2 *)vr, hi = *(const u32x2 *)(vr + 16);
-                    const bf16x8 vf = __builtin_bit_cast(bf16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
-                    oacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[m], oacc[c], 0, 0, 0);
-                }
+                for (int m = 0; m < NJ / 2; ++m)
+                    oacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb[m], vfr[c][m], oacc[c], 0, 0, 0);
         } else {
             // O^T[d = 16c + 4g + r][q] += sum_key V^T[d][key] P^T[key][q]
 #pragma unroll
@@ -305,8 +337,20 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
     float l_run = l_part + __shfl_xor(l_part, 16, WAVE);
     l_run += __shfl_xor(l_run, 32, WAVE);
 
-    // lane holds O^T[d = 16c + 4g + r][query = qi], i.e. four consecutive dims of its query
-    if (qi < p.Sq) {
+    if constexpr (BF16) {
+        // lane holds O[query = q0 + 4g + r][d = 16c + r16]; 1/l of query 4g + r from lane 4g + r
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float lr = __shfl(l_run, 4 * g + r, WAVE);
+            const int qo = q0 + 4 * g + r;
+            if (qo >= p.Sq) continue;
+            const float inv = lr > 0.f ? 1.0f / lr : 0.f;
+            uint16_t *orow = (uint16_t *)p.O + (long)b * p.o_sb + (long)h * p.o_sh + (long)qo * p.o_ss;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) orow[16 * c + r16] = __builtin_bit_cast(uint16_t, (__bf16)(oacc[c][r] * inv));
+        }
+    } else if (qi < p.Sq) {
+        // lane holds O^T[d = 16c + 4g + r][query = qi], i.e. four consecutive dims of its query
         const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
         long obase = (long)b * p.o_sb + (long)h * p.o_sh + (long)qi * p.o_ss;
 #pragma unroll
@@ -505,7 +549,7 @@ jas_status jas_attn_prefill(const void *Q, const void *K, const void *V, void *O
 #define JAS_FA(DD)                                                                                         \
     if (D == DD) {                                                                                         \
         if (dtype == JAS_BF16)                                                                              \
-            hipLaunchKernelGGL((flash_prefill_kernel<DD, true, (DD <= 64 ? 128 : 64)>), grid, dim3(64 * FA_NW), 0, s, p); \
+            hipLaunchKernelGGL((flash_prefill_kernel<DD, true, 64>), grid, dim3(64 * FA_NW), 0, s, p);       \
         else                                                                                                \
             hipLaunchKernelGGL((flash_prefill_kernel<DD, false, 64>), grid, dim3(64 * FA_NW), 0, s, p);      \
     }
