@@ -92,7 +92,6 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
     using T = typename std::conditional<BF16, uint16_t, float>::type;
     constexpr int EPC = 16 / (int)sizeof(T);    // elements per 16-byte chunk
     constexpr int KLD = D + (BF16 ? 8 : 4);    // padded row strides (elements)
-    constexpr int VLD = BK + (BF16 ? 8 : 4);
     constexpr int CPR = D / EPC;                // 16-byte chunks per key row
     constexpr int NCH = BK * CPR;            // 16-byte chunks per tile and tensor
     constexpr int NLD = (NCH + NT - 1) / NT;    // chunks per thread per tensor and tile
@@ -101,9 +100,9 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
     static_assert(NCH % NT == 0 || NLD == 1, "tile/thread mismatch");
     // two tile buffers: tile t+1 is written while tile t is read, one barrier per tile
     __shared__ __attribute__((aligned(16))) T Ks[2][BK * KLD];
-    // V: transposed [D][BK] for fp32; row-major [BK][D] for bf16, whose P.V operand is
-    // gathered with the LDS transpose read (ds_read_b64_tr_b16)
-    __shared__ __attribute__((aligned(16))) T Vt[2][BF16 ? BK * KLD : D * VLD];
+    // V row-major [BK][D] like K: the O = P V product reads its operand per key row (fp32:
+    // one float per lane and key; bf16: the LDS transpose read, ds_read_b64_tr_b16)
+    __shared__ __attribute__((aligned(16))) T Vt[2][BK * KLD];
 
     const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
@@ -180,13 +179,7 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
         const int idx = tid + it * NT, key = idx / CPR, ch = idx % CPR;                    \
         if (NCH % NT != 0 && idx >= NCH) break;                                            \
         *(u32x4 *)(&Ks[BUF][key * KLD + ch * EPC]) = kreg[it];                             \
-        if constexpr (BF16) {                                                              \
-            *(u32x4 *)(&Vt[BUF][key * KLD + ch * EPC]) = vreg[it];                         \
-        } else {                                                                           \
-            const u32x4 vw = vreg[it];                                                     \
-            _Pragma("unroll") for (int t = 0; t < EPC; ++t)                                \
-                Vt[BUF][(ch * EPC + t) * VLD + key] = __uint_as_float(vw[t]);              \
-        }                                                                                  \
+        *(u32x4 *)(&Vt[BUF][key * KLD + ch * EPC]) = vreg[it];                             \
     }
 
     if (k_end > 0) {
@@ -238,22 +231,30 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
                     vfr[c][m] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 }
         }
+        // the NJ key blocks are independent accumulators: the j loop is innermost so that
+        // consecutive matrix ops never wait on each other's result
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            s[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-            if constexpr (BF16) {
+        for (int j = 0; j < NJ; ++j) s[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (BF16) {
 #pragma unroll
-                for (int c = 0; c < D / 32; ++c)
+            for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
                     s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kfr[j][c], qb16[c], s[j], 0, 0, 0);
-            } else {
+        } else {
 #pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    float4 kf = *(const float4 *)(Kc + (16 * j + r16) * KLD + 16 * c + 4 * g);
-                    s[j] = mfma4(kf.x, qf[c].x, s[j]);
-                    s[j] = mfma4(kf.y, qf[c].y, s[j]);
-                    s[j] = mfma4(kf.z, qf[c].z, s[j]);
-                    s[j] = mfma4(kf.w, qf[c].w, s[j]);
-                }
+            for (int c = 0; c < NC; ++c) {
+                float4 kf[NJ];
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) kf[j] = *(const float4 *)(Kc + (16 * j + r16) * KLD + 16 * c + 4 * g);
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) s[j] = mfma4(kf[j].x, qf[c].x, s[j]);
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) s[j] = mfma4(kf[j].y, qf[c].y, s[j]);
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) s[j] = mfma4(kf[j].z, qf[c].z, s[j]);
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) s[j] = mfma4(kf[j].w, qf[c].w, s[j]);
             }
         }
         // masking only on tiles that reach past Sk or cross this wave's causal diagonal
@@ -291,18 +292,13 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
         m_run = m_new;
         // rescale the accumulator only when some query's max moved (wave-uniform test)
         if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
-            if constexpr (BF16) {
-                // bf16 accumulates O (not O^T): oacc[c][r] is query 4g + r, whose factor lives
-                // in lane 4g + r (the lane that owns that query's scores)
-                floatx4 cr;
+            // oacc[c][r] is query 4g + r (O, not O^T), whose factor lives in lane 4g + r, the
+            // lane that owns that query's scores
+            floatx4 cr;
 #pragma unroll
-                for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 4 * g + r, WAVE);
+            for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 4 * g + r, WAVE);
 #pragma unroll
-                for (int c = 0; c < NC; ++c) oacc[c] *= cr;
-            } else {
-#pragma unroll
-                for (int c = 0; c < NC; ++c) oacc[c] *= corr;
-            }
+            for (int c = 0; c < NC; ++c) oacc[c] *= cr;
         }
 
         if constexpr (BF16) {
@@ -320,16 +316,16 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
                 for (int m = 0; m < NJ / 2; ++m)
                     oacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb[m], vfr[c][m], oacc[c], 0, 0, 0);
         } else {
-            // O^T[d = 16c + 4g + r][q] += sum_key V^T[d][key] P^T[key][q]
+            // O[q][d = 16c + n] += sum_key P[q][key] V[key][d]: in product t of key block j the
+            // lanes of group g contribute key 16j + 4g + t -- their own score s[j][t] as A and
+            // V[16j + 4g + t][16c + n] (one float, consecutive across n) as B
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
 #pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    float4 vf = *(const float4 *)(Vc + (16 * c + r16) * VLD + 16 * j + 4 * g);
-                    oacc[c] = mfma4(vf.x, s[j][0], oacc[c]);
-                    oacc[c] = mfma4(vf.y, s[j][1], oacc[c]);
-                    oacc[c] = mfma4(vf.z, s[j][2], oacc[c]);
-                    oacc[c] = mfma4(vf.w, s[j][3], oacc[c]);
+                for (int t = 0; t < 4; ++t) {
+                    const float *vrow = Vc + (16 * j + 4 * g + t) * KLD + r16;
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) oacc[c] = mfma4(s[j][t], vrow[16 * c], oacc[c]);
                 }
         }
         __syncthreads();  // every wave is done with buffer `buf` before it is restaged
@@ -337,26 +333,22 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
     float l_run = l_part + __shfl_xor(l_part, 16, WAVE);
     l_run += __shfl_xor(l_run, 32, WAVE);
 
-    if constexpr (BF16) {
-        // lane holds O[query = q0 + 4g + r][d = 16c + r16]; 1/l of query 4g + r from lane 4g + r
+    // lane holds O[query = q0 + 4g + r][d = 16c + r16]; 1/l of query 4g + r from lane 4g + r
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float lr = __shfl(l_run, 4 * g + r, WAVE);
-            const int qo = q0 + 4 * g + r;
-            if (qo >= p.Sq) continue;
-            const float inv = lr > 0.f ? 1.0f / lr : 0.f;
-            uint16_t *orow = (uint16_t *)p.O + (long)b * p.o_sb + (long)h * p.o_sh + (long)qo * p.o_ss;
+    for (int r = 0; r < 4; ++r) {
+        const float lr = __shfl(l_run, 4 * g + r, WAVE);
+        const int qo = q0 + 4 * g + r;
+        if (qo >= p.Sq) continue;
+        const float inv = lr > 0.f ? 1.0f / lr : 0.f;
+        const long orow = (long)b * p.o_sb + (long)h * p.o_sh + (long)qo * p.o_ss;
 #pragma unroll
-            for (int c = 0; c < NC; ++c) orow[16 * c + r16] = __builtin_bit_cast(uint16_t, (__bf16)(oacc[c][r] * inv));
+        for (int c = 0; c < NC; ++c) {
+            const float v = oacc[c][r] * inv;
+            if constexpr (BF16)
+                ((uint16_t *)p.O)[orow + 16 * c + r16] = __builtin_bit_cast(uint16_t, (__bf16)v);
+            else
+                ((float *)p.O)[orow + 16 * c + r16] = v;
         }
-    } else if (qi < p.Sq) {
-        // lane holds O^T[d = 16c + 4g + r][query = qi], i.e. four consecutive dims of its query
-        const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
-        long obase = (long)b * p.o_sb + (long)h * p.o_sh + (long)qi * p.o_ss;
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-            store4<BF16>(p.O, obase + 16 * c + 4 * g,
-                         make_float4(oacc[c][0] * inv, oacc[c][1] * inv, oacc[c][2] * inv, oacc[c][3] * inv));
     }
 #undef FA_GLOAD
 #undef FA_LSTORE
