@@ -4,7 +4,8 @@
 // few hundred instructions per element and leaves an 8192x8192 evaluation compute-bound
 // at a fraction of HBM bandwidth.  For large outputs the same program is instead turned
 // into straight-line HIP source -- one typed local per node, leaves loaded once per
-// element (float4 for dense row-major operands), constants as exact hex literals -- and
+// element (16-byte non-temporal loads and stores for dense row-major operands, the fastest
+// streaming form measured on MI355X), constants as exact hex literals -- and
 // compiled once per distinct program shape with hipRTC for the current device, then
 // cached for the process.  The numerics are the interpreter's exactly: every node is
 // computed in its own type, rounded to it, with the same device math functions and no
@@ -34,6 +35,7 @@ struct JitArgs {
 };
 
 static const char *kPrelude = R"JAS(
+typedef float fx4 __attribute__((ext_vector_type(4)));
 struct JitLeaf { const void *p; long rs, cs; int rows, cols, row_first, roff, coff, transposed; };
 struct JitArgs { JitLeaf leaf[8]; void *out; int rows, cols, col_chunks; };
 __device__ __forceinline__ long gen_index(const JitLeaf &L, int i, int j)
@@ -127,8 +129,8 @@ static Gen generate(const jas_ew_ins *prog, int n_ins, const LeafDev *leaves, in
         o << "    " << T << " l" << s << "[4];\n    {\n        const " << T << " *p = (const " << T << " *)A.leaf[" << s
           << "].p;\n";
         if (L.kind == LK_CONTIG && vec && L.dtype == JAS_F32) {
-            o << "        float4 v = *(const float4 *)(p + lin0);\n"
-                 "        l" << s << "[0] = v.x; l" << s << "[1] = v.y; l" << s << "[2] = v.z; l" << s << "[3] = v.w;\n";
+            o << "        const fx4 v = __builtin_nontemporal_load((const fx4 *)(p + lin0));\n"
+                 "        l" << s << "[0] = v[0]; l" << s << "[1] = v[1]; l" << s << "[2] = v[2]; l" << s << "[3] = v[3];\n";
         } else {
             o << "#pragma unroll\n        for (int e = 0; e < 4; ++e) {\n";
             o << (vec ? "            const int ee = e;\n" : "            const int ee = e < nv ? e : 0;\n");
@@ -219,7 +221,7 @@ static Gen generate(const jas_ew_ins *prog, int n_ins, const LeafDev *leaves, in
     o << "        const " << OT << " res = (" << OT << ")v" << stack.back() << ";\n";
     if (vec && out_dtype == JAS_F32) {
         o << "        ov[e] = res;\n    }\n"
-             "    *(float4 *)((float *)A.out + lin0) = make_float4(ov[0], ov[1], ov[2], ov[3]);\n}\n";
+             "    __builtin_nontemporal_store(fx4{ov[0], ov[1], ov[2], ov[3]}, (fx4 *)((float *)A.out + lin0));\n}\n";
     } else {
         o << "        if (" << (vec ? "true" : "e < nv") << ") ((" << OT << " *)A.out)[lin0 + e] = res;\n    }\n}\n";
     }

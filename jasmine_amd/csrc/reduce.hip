@@ -13,6 +13,8 @@
 
 namespace jas {
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
 enum RowMode : int { RM_SOFTMAX = 0, RM_LN = 1, RM_RMS = 2 };
 
 template <int NT, int PER, int MODE, bool V4>
@@ -29,8 +31,10 @@ rowop_reg_kernel(const float *__restrict__ x, float *__restrict__ y, int len, lo
 #pragma unroll
         for (int k = 0; k < PER / 4; ++k) {
             int e = (k * NT + t) * 4;
-            float4 q = e < len ? *(const float4 *)(xr + e) : make_float4(0.f, 0.f, 0.f, 0.f);
-            v[4 * k] = q.x; v[4 * k + 1] = q.y; v[4 * k + 2] = q.z; v[4 * k + 3] = q.w;
+            // streaming access: non-temporal loads and stores measure ~10% faster than cached
+            // ones for an HBM-sized read+write pass on MI355X
+            floatx4 q = e < len ? __builtin_nontemporal_load((const floatx4 *)(xr + e)) : floatx4{0.f, 0.f, 0.f, 0.f};
+            v[4 * k] = q[0]; v[4 * k + 1] = q[1]; v[4 * k + 2] = q[2]; v[4 * k + 3] = q[3];
         }
     } else {
 #pragma unroll
@@ -89,7 +93,9 @@ rowop_reg_kernel(const float *__restrict__ x, float *__restrict__ y, int len, lo
 #pragma unroll
         for (int k = 0; k < PER / 4; ++k) {
             int e = (k * NT + t) * 4;
-            if (e < len) *(float4 *)(yr + e) = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+            if (e < len)
+                __builtin_nontemporal_store(floatx4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]},
+                                            (floatx4 *)(yr + e));
         }
     } else {
 #pragma unroll
