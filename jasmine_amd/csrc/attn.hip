@@ -159,6 +159,9 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
     // running max (raw score units) and this lane's partial row sum: the lanes g = 0..3 of
     // one query each sum their own keys; the four partials are combined once at the end
     float m_run = -INFINITY, l_part = 0.f;
+    // bf16: the row sums come out of the matrix core too (P times a ones operand), already in
+    // the accumulator's query layout -- no per-score adds, no final shuffles
+    floatx4 lacc = floatx4{0.f, 0.f, 0.f, 0.f};
     const float sl2 = p.scale_log2;
 
     // Q fragments (B operand of S^T = K Q^T), raw (the scale is applied in the exponent)
@@ -285,10 +288,12 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) s[j][r] = exp2_fast(__builtin_fmaf(s[j][r], sl2, -mb));
-        float psum = 0.f;
+        if constexpr (!BF16) {
+            float psum = 0.f;
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) psum += (s[j][0] + s[j][1]) + (s[j][2] + s[j][3]);
-        l_part = l_part * corr + psum;
+            for (int j = 0; j < NJ; ++j) psum += (s[j][0] + s[j][1]) + (s[j][2] + s[j][3]);
+            l_part = l_part * corr + psum;
+        }
         m_run = m_new;
         // rescale the accumulator only when some query's max moved (wave-uniform test)
         if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
@@ -299,6 +304,7 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
             for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 4 * g + r, WAVE);
 #pragma unroll
             for (int c = 0; c < NC; ++c) oacc[c] *= cr;
+            if constexpr (BF16) lacc *= cr;
         }
 
         if constexpr (BF16) {
@@ -315,6 +321,10 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
 #pragma unroll
                 for (int m = 0; m < NJ / 2; ++m)
                     oacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb[m], vfr[c][m], oacc[c], 0, 0, 0);
+            const bf16x8 ones = bf16x8{(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f,
+                                       (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
+#pragma unroll
+            for (int m = 0; m < NJ / 2; ++m) lacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb[m], ones, lacc, 0, 0, 0);
         } else {
             // O[q][d = 16c + n] += sum_key P[q][key] V[key][d]: in product t of key block j the
             // lanes of group g contribute key 16j + 4g + t -- their own score s[j][t] as A and
@@ -336,7 +346,7 @@ __global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const Prefill
     // lane holds O[query = q0 + 4g + r][d = 16c + r16]; 1/l of query 4g + r from lane 4g + r
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const float lr = __shfl(l_run, 4 * g + r, WAVE);
+        const float lr = BF16 ? lacc[r] : __shfl(l_run, 4 * g + r, WAVE);
         const int qo = q0 + 4 * g + r;
         if (qo >= p.Sq) continue;
         const float inv = lr > 0.f ? 1.0f / lr : 0.f;
