@@ -66,8 +66,9 @@ struct PrefillArgs {
     int causal;
 };
 
-constexpr int FA_NW = 8;    // waves per workgroup; 16 queries each
-constexpr int FA_BQ = 16 * FA_NW;
+// waves per workgroup (16 queries each), measured per type: 8 for bf16 (the tile staging is
+// shared by more waves), 4 for fp32 (more, smaller workgroups per CU)
+template <bool BF16> struct FaWaves { static constexpr int value = BF16 ? 8 : 4; };
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
@@ -86,8 +87,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // second product); the reduction index of each product is permuted identically in both
 // operands so that S lands in the P operand's registers with no shuffle.
 template <int D, bool BF16, int BK>
-__global__ void __launch_bounds__(64 * FA_NW) flash_prefill_kernel(const PrefillArgs p)
+__global__ void __launch_bounds__(64 * FaWaves<BF16>::value) flash_prefill_kernel(const PrefillArgs p)
 {
+    constexpr int FA_NW = FaWaves<BF16>::value, FA_BQ = 16 * FA_NW;
     constexpr int NT = 64 * FA_NW;
     using T = typename std::conditional<BF16, uint16_t, float>::type;
     constexpr int EPC = 16 / (int)sizeof(T);    // elements per 16-byte chunk
@@ -545,15 +547,19 @@ jas_status jas_attn_prefill(const void *Q, const void *K, const void *V, void *O
               JAS_ERR_INVALID, "jas_attn_prefill: tensors must be 16-byte aligned");
     PrefillArgs p{Q, K, V, O, q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, o_sb, o_sh, o_ss, B, H, Sq, Sk,
                   scale * 1.4426950408889634f, causal};
-    const int total = ceil_div(Sq, FA_BQ) * B * H;
-    dim3 grid((total + 7) / 8 * 8);
     hipStream_t s = stream_or_default(stream);
-#define JAS_FA(DD)                                                                                         \
-    if (D == DD) {                                                                                         \
-        if (dtype == JAS_BF16)                                                                              \
-            hipLaunchKernelGGL((flash_prefill_kernel<DD, true, 64>), grid, dim3(64 * FA_NW), 0, s, p);       \
-        else                                                                                                \
-            hipLaunchKernelGGL((flash_prefill_kernel<DD, false, 64>), grid, dim3(64 * FA_NW), 0, s, p);      \
+    // grid: one workgroup per (query block, batch x head), padded to a multiple of the 8 XCDs
+#define JAS_FA(DD)                                                                                     \
+    if (D == DD) {                                                                                     \
+        if (dtype == JAS_BF16) {                                                                       \
+            constexpr int nw = FaWaves<true>::value;                                                  \
+            const int total = ceil_div(Sq, 16 * nw) * B * H;                                           \
+            hipLaunchKernelGGL((flash_prefill_kernel<DD, true, 64>), dim3((total + 7) / 8 * 8), dim3(64 * nw), 0, s, p); \
+        } else {                                                                                       \
+            constexpr int nw = FaWaves<false>::value;                                                 \
+            const int total = ceil_div(Sq, 16 * nw) * B * H;                                           \
+            hipLaunchKernelGGL((flash_prefill_kernel<DD, false, 64>), dim3((total + 7) / 8 * 8), dim3(64 * nw), 0, s, p); \
+        }                                                                                              \
     }
     JAS_FA(32) JAS_FA(64) JAS_FA(128)
 #undef JAS_FA
