@@ -24,6 +24,10 @@ jas_status attn_decode_impl(const float *q, const float *K, const float *V, floa
                             int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, hipStream_t s,
                             int o_packed_d);
 
+// two-pass row argmax with caller-provided scratch of argmax_workspace_bytes(n, V) bytes
+size_t argmax_workspace_bytes(int n, int V);
+jas_status argmax_impl(const float *x, int n, int V, long ld, int32_t *out, void *work, hipStream_t s);
+
 #define JAS_HIP(expr)                                                                 \
     do {                                                                              \
         hipError_t e_ = (expr);                                                       \

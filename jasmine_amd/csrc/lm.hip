@@ -133,6 +133,7 @@ struct jas_lm {
     // device-side decode state for graph replay: [0] next position, [1] first position of
     // the current jas_lm_generate call (its id history is indexed from there)
     int32_t *dstate = nullptr;
+    void *argmax_ws = nullptr;  // scratch of the two-pass argmax (allocated once: graph-safe)
     // one decode step captured as a HIP graph (for this batch size and id-history buffer)
     hipGraphExec_t graph = nullptr;
     bool use_graph = true;
@@ -369,7 +370,7 @@ jas_status decode_step(jas_lm *lm, bool device_pos)
     eh.ldo = V;
     TRY(proj(lm, c.kind == 0 ? lm->W("wte") : lm->W("w_head"), lm->h, B, V, d, eh));
     TRY(prof_begin(lm, 2));
-    TRY(jas_argmax(lm->logits, B, V, V, lm->ids, s));
+    TRY(argmax_impl(lm->logits, B, V, V, lm->ids, lm->argmax_ws, s));
     TRY(prof_end(lm));
     if (!device_pos) lm->position += 1;
     return JAS_OK;
@@ -468,6 +469,7 @@ jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out)
     if (st == JAS_OK) st = jas_malloc((void **)&lm->pos, 64 * sizeof(int32_t));
     if (st == JAS_OK) st = jas_malloc((void **)&lm->seqlens, 64 * sizeof(int32_t));
     if (st == JAS_OK) st = jas_malloc((void **)&lm->dstate, 2 * sizeof(int32_t));
+    if (st == JAS_OK) st = jas_malloc(&lm->argmax_ws, argmax_workspace_bytes(std::max(Bm, 64), V));
     lm->attn_ws_bytes = jas_attn_decode_workspace(Bm, c.n_head, dh, c.max_ctx);
     for (int b = 1; b < Bm; ++b)  // workspace must cover every batch size actually used
         lm->attn_ws_bytes = std::max(lm->attn_ws_bytes, jas_attn_decode_workspace(b, c.n_head, dh, c.max_ctx));
@@ -490,7 +492,7 @@ jas_status jas_lm_destroy(jas_lm *lm)
     if (!lm) return JAS_OK;
     if (lm->stream) (void)hipStreamSynchronize(lm->stream);
     if (lm->graph) (void)hipGraphExecDestroy(lm->graph);
-    void *ptrs[] = {lm->dstate, lm->arena, lm->kc, lm->vc, lm->x, lm->h, lm->q, lm->att, lm->ff, lm->logits, lm->ids, lm->pos,
+    void *ptrs[] = {lm->argmax_ws, lm->dstate, lm->arena, lm->kc, lm->vc, lm->x, lm->h, lm->q, lm->att, lm->ff, lm->logits, lm->ids, lm->pos,
                     lm->seqlens, lm->hist, lm->attn_ws, lm->part, lm->pX, lm->pH, lm->pQKV, lm->pATT, lm->pG, lm->pU, lm->pFF,
                     lm->pIds, lm->pPos};
     for (void *p : ptrs)
@@ -641,7 +643,7 @@ jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_
     eh.out = lm->logits;
     eh.ldo = V;
     TRY(skinny_gemm(c.kind == 0 ? lm->W("wte") : lm->W("w_head"), nullptr, lm->h, d, V, B, d, eh, s, true));
-    TRY(jas_argmax(lm->logits, B, V, V, lm->ids, s));
+    TRY(argmax_impl(lm->logits, B, V, V, lm->ids, lm->argmax_ws, s));
     lm->position = P;
     if (h_next) TRY(jas_memcpy_d2h(h_next, lm->ids, B * sizeof(int32_t), s));
     if (h_logits) TRY(jas_memcpy_d2h(h_logits, lm->logits, (size_t)B * V * sizeof(float), s));

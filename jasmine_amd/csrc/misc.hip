@@ -90,32 +90,83 @@ __global__ void embed_kernel(const float *__restrict__ wte, const float *__restr
     out[g] = v;
 }
 
-// argmax of each row; ties go to the lowest index (the first maximum, like a forward scan)
-__global__ void __launch_bounds__(256) argmax_kernel(const float *__restrict__ x, int V, long ld, int32_t *out)
+// argmax of each row; ties go to the lowest index (the first maximum, like a forward scan).
+// Two passes: chunks of ARGMAX_CHUNK elements of every row are scanned by their own
+// workgroups (a 50257-long row is 13 of them, so the scan is not one workgroup's latency
+// chain), then one workgroup per row reduces the chunk winners.
+constexpr int ARGMAX_CHUNK = 4096;
+
+__device__ __forceinline__ void argmax_combine(float &bv, int &bi, float ov, int oi)
+{
+    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+}
+
+// block-wide (256 threads) first-maximum reduction; thread 0 gets the result
+__device__ __forceinline__ void argmax_block(float &bv, int &bi)
 {
     __shared__ float sv[4];
     __shared__ int si[4];
-    const float *row = x + (long)blockIdx.x * ld;
-    float bv = -FLT_MAX;
-    int bi = 0x7fffffff;
-    for (int e = threadIdx.x; e < V; e += 256) {
-        float v = row[e];
-        if (v > bv) { bv = v; bi = e; }
-    }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        float ov = __shfl_xor(bv, o, WAVE);
-        int oi = __shfl_xor(bi, o, WAVE);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
-    int w = threadIdx.x / WAVE;
+    for (int o = 32; o > 0; o >>= 1) argmax_combine(bv, bi, __shfl_xor(bv, o, WAVE), __shfl_xor(bi, o, WAVE));
+    const int w = threadIdx.x / WAVE;
     if (threadIdx.x % WAVE == 0) { sv[w] = bv; si[w] = bi; }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int k = 1; k < 4; ++k)
-            if (sv[k] > bv || (sv[k] == bv && si[k] < bi)) { bv = sv[k]; bi = si[k]; }
-        out[blockIdx.x] = bi == 0x7fffffff ? 0 : bi;
+    if (threadIdx.x == 0)
+        for (int k = 1; k < 4; ++k) argmax_combine(bv, bi, sv[k], si[k]);
+}
+
+__global__ void __launch_bounds__(256) argmax_chunk_kernel(const float *__restrict__ x, int V, long ld,
+                                                           float *__restrict__ pv, int *__restrict__ pi)
+{
+    const int row = blockIdx.y, c = blockIdx.x, nch = gridDim.x;
+    const float *r = x + (long)row * ld;
+    const int e0 = c * ARGMAX_CHUNK, e1 = min(V, e0 + ARGMAX_CHUNK);
+    float v[ARGMAX_CHUNK / 256];
+#pragma unroll
+    for (int k = 0; k < ARGMAX_CHUNK / 256; ++k) {  // all loads in flight before the scan
+        const int e = e0 + k * 256 + threadIdx.x;
+        v[k] = e < e1 ? r[e] : -INFINITY;
     }
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int k = 0; k < ARGMAX_CHUNK / 256; ++k) {
+        const int e = e0 + k * 256 + threadIdx.x;
+        if (e < e1 && v[k] > bv) { bv = v[k]; bi = e; }
+    }
+    argmax_block(bv, bi);
+    if (threadIdx.x == 0) {
+        pv[(long)row * nch + c] = bv;
+        pi[(long)row * nch + c] = bi;
+    }
+}
+
+__global__ void __launch_bounds__(256) argmax_final_kernel(const float *__restrict__ pv, const int *__restrict__ pi,
+                                                           int nch, int32_t *out)
+{
+    const int row = blockIdx.x;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int c = threadIdx.x; c < nch; c += 256) argmax_combine(bv, bi, pv[(long)row * nch + c], pi[(long)row * nch + c]);
+    argmax_block(bv, bi);
+    if (threadIdx.x == 0) out[row] = bi == 0x7fffffff ? 0 : bi;
+}
+
+size_t argmax_workspace_bytes(int n, int V)
+{
+    return (size_t)n * ((V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK) * (sizeof(float) + sizeof(int));
+}
+
+jas_status argmax_impl(const float *x, int n, int V, long ld, int32_t *out, void *work, hipStream_t s)
+{
+    if (!n) return JAS_OK;
+    const int nch = (V + ARGMAX_CHUNK - 1) / ARGMAX_CHUNK;
+    float *pv = (float *)work;
+    int *pi = (int *)(pv + (size_t)n * nch);
+    hipLaunchKernelGGL(argmax_chunk_kernel, dim3(nch, n), dim3(256), 0, s, x, V, ld, pv, pi);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(n), dim3(256), 0, s, pv, pi, nch, out);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
 }
 
 __global__ void fill_normal_kernel(float *x, size_t n, uint64_t key, float mean, float std)
@@ -173,9 +224,12 @@ jas_status jas_embed(const float *wte, const float *wpe, const int32_t *ids, con
 jas_status jas_argmax(const float *x, int n, int V, long ld, int32_t *out, jas_stream_t stream)
 {
     JAS_CHECK(x && out && n >= 0 && V > 0 && ld >= V, JAS_ERR_INVALID, "jas_argmax: bad arguments");
-    if (n) hipLaunchKernelGGL(argmax_kernel, dim3(n), dim3(256), 0, stream_or_default(stream), x, V, ld, out);
-    JAS_LAUNCH_CHECK();
-    return JAS_OK;
+    if (!n) return JAS_OK;
+    JAS_CHECK(n <= 65535, JAS_ERR_INVALID, "jas_argmax: at most 65535 rows");
+    hipStream_t s = stream_or_default(stream);
+    void *work = workspace(argmax_workspace_bytes(n, V), s);
+    JAS_CHECK(work, JAS_ERR_OOM, "jas_argmax: workspace allocation failed");
+    return argmax_impl(x, n, V, ld, out, work, s);
 }
 
 jas_status jas_fill_normal(float *x, size_t n, uint64_t seed, uint64_t stream_id, float mean, float std,

@@ -404,6 +404,25 @@ def test_embed_argmax_fill(jas):
     close(dn.numpy(), normal(100003, 9, 3, std=0.02), atol=1e-7, rtol=1e-6)
 
 
+@pytest.mark.parametrize("n,V,ld", [(1, 1, 1), (3, 4095, 4100), (16, 4097, 4097), (5, 32000, 32000), (16, 50257, 50260)])
+def test_argmax_two_pass(jas, n, V, ld):
+    """Ties resolve to the first index also when the tied values sit in different chunks
+    (4096 elements per chunk) or on a chunk's first/last element; -inf rows give 0."""
+    x = np.full((n, ld), np.nan, np.float32)
+    x[:, :V] = normal((n, V), 7, n)
+    if V > 4096:
+        x[0, 4095] = x[0, 4096] = 80.0      # tie across the chunk boundary
+    if n > 1:
+        x[1, :V] = -np.inf
+    if n > 2:
+        x[2, V - 1] = 90.0                  # last element
+    if n > 3:
+        x[3, :V] = 1.0                      # all equal
+    dx, da = jas.to_device(x), jas.DeviceArray(n, np.int32)
+    jas.check(jas.lib.jas_argmax(dx.p, n, V, ld, da.p, None))
+    assert list(da.numpy()) == [int(np.argmax(r[:V])) for r in x]
+
+
 # ---------------------------------------------------------------- API support kernels
 def test_leaf_assign_block_and_convert(jas):
     dst = np.zeros((7, 9), np.float32)
