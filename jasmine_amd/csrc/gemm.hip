@@ -293,41 +293,45 @@ skinny_kernel(const float *__restrict__ W, const float *__restrict__ W2, const f
             wp[t] = base + (long)row * K + 4 * g;
         }
     }
-    const bool xvalid = r16 < N;
-    const float *xp = PACKED ? X + (long)lane * 4 : X + (long)(xvalid ? r16 : 0) * ldx + 4 * g;
+    // token rows >= N feed only output columns >= N, which the epilogue discards, so the
+    // activation loads need no predicate (row 0 stands in for them)
+    const float *xp = PACKED ? X + (long)lane * 4 : X + (long)(r16 < N ? r16 : 0) * ldx + 4 * g;
 
     floatx4 acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    const int nchunk_all = (K + 63) / 64;
-    // K split (PARTIAL mode): this workgroup streams chunks [c_begin, nchunk)
+    // K split (PARTIAL mode): this workgroup owns chunks [c_begin, c_end).  The streaming
+    // loop covers the full 64-wide chunks; a partial last chunk (K % 64 != 0) is done once
+    // at the end with predicated loads.
     const int c_begin = blockIdx.y * epi.cpb;
-    const int nchunk = min(nchunk_all, c_begin + epi.cpb);
-    const bool ktail = (K & 63) != 0;
-    // DEPTH-deep ring of chunk buffers: chunk c+j*WPB is loading while chunk c computes
+    const int c_end = min((K + 63) >> 6, c_begin + epi.cpb);
+    const int c_full = min(K >> 6, c_end);
+    // chunk index of this wave's i-th chunk: cs + i * WPB.  w is made wave-uniform so every
+    // bound below is a scalar branch and the loads in the steady state carry no predicate
+    // (a predicated load puts a branch around it, and the wait before the MFMAs then drains
+    // the whole pipeline).
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    const int cs = c_begin + wu;
+    const int nw = cs < c_full ? (c_full - cs + WPB - 1) / WPB : 0;
     floatx4 wb[DEPTH][NT][4];
     float4 xb[DEPTH][4];
     auto load = [&](int c, floatx4 (&wv)[NT][4], float4 (&xv)[4]) {
         const int k = c * 64;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const bool kin = !ktail || (k + 16 * q + 4 * g) < K;
-            const bool cin = !ktail || (4 * c + q) < K16;  // packed: whole 16-wide block valid
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 if (PACKED)
-                    wv[t][q] = cin ? __builtin_nontemporal_load(
-                                         (const floatx4 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG)))
-                                   : floatx4{0.f, 0.f, 0.f, 0.f};
+                    wv[t][q] = __builtin_nontemporal_load(
+                        (const floatx4 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG)));
                 else
-                    wv[t][q] = kin ? __builtin_nontemporal_load((const floatx4 *)(wp[t] + k + 16 * q))
-                                   : floatx4{0.f, 0.f, 0.f, 0.f};
+                    wv[t][q] = __builtin_nontemporal_load((const floatx4 *)(wp[t] + k + 16 * q));
             }
-            if (PACKED)  // contiguous 1 KB per wave; token rows >= N only feed discarded columns
-                xv[q] = cin ? *(const float4 *)(xp + (long)(4 * c + q) * 256) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (PACKED)  // contiguous 1 KB per wave
+                xv[q] = *(const float4 *)(xp + (long)(4 * c + q) * 256);
             else
-                xv[q] = (xvalid && kin) ? *(const float4 *)(xp + k + 16 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+                xv[q] = *(const float4 *)(xp + k + 16 * q);
         }
     };
     auto compute = [&](const floatx4 (&wv)[NT][4], const float4 (&xv)[4]) {
@@ -343,14 +347,46 @@ skinny_kernel(const float *__restrict__ W, const float *__restrict__ W2, const f
     };
 #pragma unroll
     for (int j = 0; j < DEPTH - 1; ++j)
-        if (c_begin + w + j * WPB < nchunk) load(c_begin + w + j * WPB, wb[j], xb[j]);
-    for (int c = c_begin + w; c < nchunk; c += DEPTH * WPB) {
+        if (j < nw) load(cs + j * WPB, wb[j], xb[j]);
+    int i = 0;
+    // steady state: DEPTH chunks per trip, every load in range
+    for (; i + 2 * DEPTH - 2 < nw; i += DEPTH) {
 #pragma unroll
         for (int j = 0; j < DEPTH; ++j) {
-            const int cl = c + (j + DEPTH - 1) * WPB;
-            if (cl < nchunk) load(cl, wb[(j + DEPTH - 1) % DEPTH], xb[(j + DEPTH - 1) % DEPTH]);
-            if (c + j * WPB < nchunk) compute(wb[j], xb[j]);
+            load(cs + (i + j + DEPTH - 1) * WPB, wb[(j + DEPTH - 1) % DEPTH], xb[(j + DEPTH - 1) % DEPTH]);
+            compute(wb[j], xb[j]);
         }
+    }
+    // drain (i % DEPTH == 0 here, so the ring slots are compile-time indices)
+#pragma unroll
+    for (int j = 0; j < 2 * DEPTH - 1; ++j) {
+        if (i + j < nw) {
+            if (i + j + DEPTH - 1 < nw)
+                load(cs + (i + j + DEPTH - 1) * WPB, wb[(j + DEPTH - 1) % DEPTH], xb[(j + DEPTH - 1) % DEPTH]);
+            compute(wb[j % DEPTH], xb[j % DEPTH]);
+        }
+    }
+    // partial last chunk: the wave whose stride reaches it; blocks (packed) or lanes
+    // (row-major) past K read as zero
+    if (c_full < c_end && (c_full - c_begin) % WPB == wu) {
+        const int c = c_full, k = c * 64;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const bool in = PACKED ? (4 * c + q) < K16 : (k + 16 * q + 4 * g) < K;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                if (PACKED)
+                    wb[0][t][q] = in ? *(const floatx4 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG))
+                                     : floatx4{0.f, 0.f, 0.f, 0.f};
+                else
+                    wb[0][t][q] = in ? *(const floatx4 *)(wp[t] + k + 16 * q) : floatx4{0.f, 0.f, 0.f, 0.f};
+            }
+            if (PACKED)
+                xb[0][q] = in ? *(const float4 *)(xp + (long)(4 * c + q) * 256) : make_float4(0.f, 0.f, 0.f, 0.f);
+            else
+                xb[0][q] = in ? *(const float4 *)(xp + k + 16 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        compute(wb[0], xb[0]);
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) red[w][t][lane] = acc[t];
@@ -435,35 +471,38 @@ static void launch_skinny(const float *W, const float *W2, const float *X, long 
                        s, W, W2, X, ldx, M, N, K, epi);
 }
 
-// geometry by row count: enough workgroups to cover the 256 CUs first, then more bytes per
-// wave (two row tiles) once the row groups outnumber the CUs several times over
-// Geometry per decode shape, from a cold-weight sweep on MI355X (16 tokens, packed weights):
-//  * two row tiles per workgroup for the large matrices (SwiGLU pair, LM head) and for the
-//    split-K residual projections: each activation chunk read from L2 then feeds two weight
-//    tiles (activation reads otherwise equal the weight reads and cost ~10% bandwidth);
-//  * 4-wave workgroups with a 3-deep chunk ring for the large matrices, 8 waves x 2 deep for
-//    the split-K projections; single-tile geometry where that would leave too few
-//    workgroups (mid-size and small matrices without a K split).
+// Geometry per decode shape, from a cold-weight sweep on MI355X (16 tokens, packed weights).
+// More row tiles per workgroup amortise each activation chunk (read from L2) over more
+// weight bytes -- four tiles for the large matrices even though that leaves fewer
+// workgroups than CUs for the QKV projection; small matrices (GPT-2 widths) are
+// latency-bound and keep one tile and 8 waves so that more workgroups are in flight.
 SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split)
 {
     SkinnyTuning t;
     const int rt = (M + 15) / 16;
-    (void)K;
-    if (dual || rt >= 1536) {  // SwiGLU gate/up, LM head
+    if (dual) {                      // SwiGLU gate/up: one tile of each
         t.nt = 2; t.wpb = 4; t.depth = 3;
-    } else if (split) {        // split-K residual projections
-        t.nt = 2; t.wpb = 8; t.depth = 2;
+    } else if (split) {              // split-K residual projections
+        // (two tiles: four would need twice the K splits, and the norm kernel that sums
+        // the split partials then reads twice as much)
+        if (rt >= 256) { t.nt = 2; t.wpb = 4; t.depth = K >= 8192 ? 2 : 3; }
+        else { t.nt = 2; t.wpb = 8; t.depth = 2; }
+    } else if (rt >= 1536) {         // LM head
+        t.nt = 4; t.wpb = 4; t.depth = 3;
+    } else if (rt >= 512) {          // QKV at LLaMA-7B width
+        t.nt = 4; t.wpb = 4; t.depth = 2;
     } else {
-        t.nt = 1; t.wpb = rt >= 512 ? 4 : 8; t.depth = rt >= 512 ? 2 : 3;
+        t.nt = 1; t.wpb = 8; t.depth = 3;
     }
     return t;
 }
 
-// K splits of a split-K residual projection (two row tiles per workgroup): enough splits for
-// about 256 workgroups, at most 8 and at least two 64-wide chunks per split
+// K splits of a split-K residual projection: enough splits for about 256 workgroups with
+// the split geometry above, at most 8 and at least two 64-wide chunks per split
 int skinny_pick_ksplit(int M, int K)
 {
-    const int wgs = ((M + 15) / 16 + 1) / 2, nchunk = (K + 63) / 64;
+    const int nt = skinny_default_tuning(M, K, false, true).nt;
+    const int wgs = ((M + 15) / 16 + nt - 1) / nt, nchunk = (K + 63) / 64;
     int ks = std::max(1, std::min({(256 + wgs - 1) / wgs, nchunk / 2, 8}));
     const int cpb = (nchunk + ks - 1) / ks;
     return (nchunk + cpb - 1) / cpb;  // every split non-empty
@@ -483,6 +522,7 @@ jas_status skinny_gemm(const float *W, const float *W2, const float *X, long ldx
         JAS_CHECK(epi.d % 16 == 0 && epi.dh % 4 == 0 && M == 3 * epi.d, JAS_ERR_INVALID, "skinny_gemm: bad QKV shape");
     if (dual) JAS_CHECK(W2 != nullptr, JAS_ERR_INVALID, "skinny_gemm: SwiGLU needs both weights");
     SkinnyTuning tu = tune ? *tune : skinny_default_tuning(M, K, dual, epi.mode == EPI_PARTIAL);
+    if (!tune && !packed && tu.nt == 4) tu.nt = 2;  // four-tile geometry: packed weights only
     const int nt = dual ? 2 : tu.nt;
     SkinnyEpiArgs ep = epi;
     const int nchunk = (K + 63) / 64;

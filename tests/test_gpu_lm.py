@@ -74,6 +74,15 @@ def test_llama_architecture_small(jas):
     run_parity(jas, cfg, seed=4, B=3, P=20, steps=8, prompt_seed=4)
 
 
+@pytest.mark.parametrize("kind,d,H,F,V", [(1, 128, 4, 208, 333), (0, 192, 3, 336, 77)])
+def test_ragged_chunk_widths(jas, kind, d, H, F, V):
+    # FFN widths that are multiples of 16 but not of 64 (208 = 3*64 + 16, 336 = 5*64 + 16):
+    # the down/proj projection's last K chunk is partial, also under its K split; and
+    # vocabularies that are not a multiple of 16 rows (padded packed head)
+    cfg = jas.LmConfig(kind, 2, d, H, F, V, 40, 4, 1e-5 if kind == 0 else 1e-6, 10000.0)
+    run_parity(jas, cfg, seed=9, B=4, P=13, steps=6, prompt_seed=9)
+
+
 def test_gpt2_small_shape(jas):
     # config 4 shape (12 layers, d 768, 12 heads, FFN 3072, vocab 50257, ctx 1024, seed 3),
     # 2 sequences x 24-token prompts x 3 steps (the oracle is the bound here, not the GPU)

@@ -284,7 +284,7 @@ def test_gemm_epilogues(jas, bias_mode, act, acc, batch):
 
 
 @pytest.mark.parametrize("N", [1, 2, 5, 8, 16])
-@pytest.mark.parametrize("M,K", [(300, 64), (64, 100), (1000, 4096), (4096, 1024)])
+@pytest.mark.parametrize("M,K", [(300, 64), (64, 100), (1000, 4096), (4096, 1024), (8200, 80), (25000, 64)])
 def test_gemm_skinny(jas, M, N, K):
     # decode shape: W [M][K], tokens X [N][K] -> out [N][M] (token-major), via jas_gemm's skinny path
     W, X, b = normal((M, K), 20, 0), normal((N, K), 20, 1), normal(M, 20, 2)
