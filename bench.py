@@ -220,15 +220,53 @@ def summarize_pmc(fetch_csv, write_csv, cfetch_csv, cwrite_csv, args):
                     n = (n or 0) + len(fk)
         if n:
             out["classes"][cls] = {"bytes_per_launch": tot / n, "launches": n}
-    B, P, L, H, dh = args.batch, args.prompt, 32, 32, 128
-    first, last = P, P + args.warmup + 2 * args.steps - 1
-    mean_ctx = (first + 1 + last + 1) / 2.0
-    out["algorithmic"] = {"attention": B * H * mean_ctx * dh * 8, "weight_gemm": None}
-    out["run"] = {"batch": B, "prompt": P, "steps": args.steps, "warmup": args.warmup}
+    B, H, dh = args.batch, 32, 128
+    out["algorithmic"] = {"attention": B * H * profiled_mean_ctx(args) * dh * 8, "weight_gemm": None}
+    out["run"] = {"batch": B, "prompt": args.prompt, "steps": args.steps, "warmup": args.warmup}
     return out
 
 
 COPY_BYTES = 1 << 30
+
+
+def profiled_mean_ctx(args):
+    """Mean number of cached keys per decode step over the bench's profiled pass (positions
+    P + warmup + steps .. P + warmup + 2 steps - 1; step s attends to position + 1 keys)."""
+    pos1 = args.prompt + args.warmup + args.steps
+    return pos1 + (args.steps + 1) / 2.0
+
+
+def traffic_kernels(args):
+    """The dominant decode kernel alone for rocprofv3 --pmc: the split-K attention at the
+    LLaMA-7B shape (batch x 32 heads x 128) over the profiled pass's mean context (half the
+    sequences one key shorter when the mean is a half), five launches.  Same kernels, same
+    bytes per launch as inside the decode step; the runner itself is not profiled this way
+    because rocprofv3's counter collection dies in the runner's launch path (host SIGSEGV)."""
+    import ctypes as C
+    import numpy as np
+    import jasmine_amd as jas
+    lib = jas.lib
+    jas.check(lib.jas_init(0))
+    B, H, D = args.batch, 32, 128
+    mc = profiled_mean_ctx(args)
+    lo = int(mc)
+    lens_h = np.array([lo + (1 if (mc - lo) > 0 and b % 2 else 0) for b in range(B)], np.int32)
+    # the runner's K/V cache rows are max_len long and it launches over its full capacity
+    # (the splits past a sequence are empty): same strides and launch here
+    max_len = args.prompt + args.warmup + 2 * args.steps + 1
+    Kc, Vc = jas.DeviceArray((B, H, max_len, D)), jas.DeviceArray((B, H, max_len, D))
+    jas.check(lib.jas_fill_normal(Kc.p, B * H * max_len * D, 5, 0, 0.0, 1.0, None))
+    jas.check(lib.jas_fill_normal(Vc.p, B * H * max_len * D, 5, 1, 0.0, 1.0, None))
+    q, o = jas.DeviceArray((B, H, D)), jas.DeviceArray((B, H, D))
+    jas.check(lib.jas_fill_normal(q.p, B * H * D, 5, 2, 0.0, 1.0, None))
+    lens = jas.to_device(lens_h)
+    ws = jas.DeviceArray(max(lib.jas_attn_decode_workspace(B, H, D, max_len) // 4, 1))
+    for _ in range(5):
+        jas.check(lib.jas_attn_decode(q.p, Kc.p, Vc.p, o.p, lens.p, B, H, D, max_len, H * max_len * D, max_len * D,
+                                      C.c_float(D ** -0.5), ws.p, None))
+    jas.check(lib.jas_synchronize(None))
+    print(json.dumps({"traffic_kernels": "attn_decode", "batch": B, "heads": H, "head_dim": D,
+                      "mean_ctx": float(lens_h.mean()), "launches": 5}))
 
 
 def copy_calibration():
@@ -270,11 +308,16 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="decode with eager launches instead of graph replay (same kernels; for profilers)")
     ap.add_argument("--copy-calib", action="store_true", help="only run the copy used to calibrate PMC bytes")
+    ap.add_argument("--traffic-kernels", action="store_true",
+                    help="only run the dominant decode kernel at the profiled pass's shape (for rocprofv3 --pmc)")
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV", "COPY_WRITE_CSV"),
                     help="write the traffic summary from rocprofv3 --pmc counter_collection.csv files")
     args = ap.parse_args()
     if args.copy_calib:
         copy_calibration()
+        return
+    if args.traffic_kernels:
+        traffic_kernels(args)
         return
     if args.summarize_pmc:
         out = summarize_pmc(*args.summarize_pmc, args)
