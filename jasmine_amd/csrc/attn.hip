@@ -129,7 +129,8 @@ __global__ void __launch_bounds__(64 * FaWaves<BF16>::value) flash_prefill_kerne
     const long kbase = (long)b * p.k_sb + (long)h * p.k_sh;
 
     // staging: chunk `it` of this thread is (key row, 16-byte column) of the 64-row tile
-    u32x4 kreg[NLD], vreg[NLD];
+    // two register sets: tile t+1 is in one while tile t+2 is in flight in the other
+    u32x4 kra[NLD], vra[NLD], krb[NLD], vrb[NLD];
     long goff[NLD];
 #pragma unroll
     for (int it = 0; it < NLD; ++it) {
@@ -137,21 +138,21 @@ __global__ void __launch_bounds__(64 * FaWaves<BF16>::value) flash_prefill_kerne
         goff[it] = kbase + (long)(idx / CPR) * p.k_ss + (idx % CPR) * EPC;
     }
     // rows past Sk are read clamped to the last row (finite data, masked below)
-#define FA_GLOAD(KV0)                                                                        \
+#define FA_GLOAD(KV0, KR, VR)                                                                \
     if ((KV0) + BK <= p.Sk) {                                                           \
         const long o0 = (long)(KV0) * p.k_ss;                                              \
         _Pragma("unroll") for (int it = 0; it < NLD; ++it)                                 \
         {                                                                                  \
-            kreg[it] = *(const u32x4 *)((const T *)p.K + goff[it] + o0);                   \
-            vreg[it] = *(const u32x4 *)((const T *)p.V + goff[it] + o0);                   \
+            KR[it] = *(const u32x4 *)((const T *)p.K + goff[it] + o0);                     \
+            VR[it] = *(const u32x4 *)((const T *)p.V + goff[it] + o0);                     \
         }                                                                                  \
     } else {                                                                               \
         _Pragma("unroll") for (int it = 0; it < NLD; ++it)                                 \
         {                                                                                  \
             const int idx = min(tid + it * NT, NCH - 1), key = idx / CPR, ch = idx % CPR; \
             const long off = kbase + (long)min((KV0) + key, p.Sk - 1) * p.k_ss + ch * EPC; \
-            kreg[it] = *(const u32x4 *)((const T *)p.K + off);                             \
-            vreg[it] = *(const u32x4 *)((const T *)p.V + off);                             \
+            KR[it] = *(const u32x4 *)((const T *)p.K + off);                               \
+            VR[it] = *(const u32x4 *)((const T *)p.V + off);                               \
         }                                                                                  \
     }
 
@@ -178,32 +179,27 @@ __global__ void __launch_bounds__(64 * FaWaves<BF16>::value) flash_prefill_kerne
         for (int c = 0; c < NC; ++c) qf[c] = *(const float4 *)((const float *)p.Q + qbase + 16 * c + 4 * g);
     }
 
-#define FA_LSTORE(BUF)                                                                       \
+#define FA_LSTORE(BUF, KR, VR)                                                               \
     _Pragma("unroll") for (int it = 0; it < NLD; ++it)                                     \
     {                                                                                      \
         const int idx = tid + it * NT, key = idx / CPR, ch = idx % CPR;                    \
         if (NCH % NT != 0 && idx >= NCH) break;                                            \
-        *(u32x4 *)(&Ks[BUF][key * KLD + ch * EPC]) = kreg[it];                             \
-        *(u32x4 *)(&Vt[BUF][key * KLD + ch * EPC]) = vreg[it];                             \
+        *(u32x4 *)(&Ks[BUF][key * KLD + ch * EPC]) = KR[it];                               \
+        *(u32x4 *)(&Vt[BUF][key * KLD + ch * EPC]) = VR[it];                               \
     }
 
+    // Pipeline: tile t is computed from LDS buffer t%2 while tile t+1 waits in registers
+    // (staged into the other buffer at the top of step t) and tile t+2 is in flight from HBM
+    // into the other register set -- loads are issued two tiles ahead of their use.
+    // Register set A holds the odd tiles, B the even ones (after tile 0).
     if (k_end > 0) {
-        FA_GLOAD(0)
-        FA_LSTORE(0)
-        if (BK < k_end) { FA_GLOAD(BK) }
+        FA_GLOAD(0, kra, vra)
+        FA_LSTORE(0, kra, vra)
+        if (BK < k_end) { FA_GLOAD(BK, kra, vra) }
+        if (2 * BK < k_end) { FA_GLOAD(2 * BK, krb, vrb) }
     }
     __syncthreads();
-    int buf = 0;
-    for (int kv0 = 0; kv0 < k_end; kv0 += BK, buf ^= 1) {
-        // stage tile t+1 (loaded during the previous tile's math) and start loading t+2
-        if (kv0 + BK < k_end) {
-            FA_LSTORE(buf ^ 1)
-            if (kv0 + 2 * BK < k_end) { FA_GLOAD(kv0 + 2 * BK) }
-        }
-        if (kv0 >= wave_kend) {  // wave-uniform: every key of this tile is masked for this wave
-            __syncthreads();
-            continue;
-        }
+    auto tile = [&](const int kv0, const int buf) __attribute__((always_inline)) {
         const T *Kc = Ks[buf], *Vc = Vt[buf];
 
         // S^T tile: lane holds S^T[key = kv0 + 16j + 4g + r][query = qi] (raw scores)
@@ -340,8 +336,25 @@ __global__ void __launch_bounds__(64 * FaWaves<BF16>::value) flash_prefill_kerne
                     for (int c = 0; c < NC; ++c) oacc[c] = mfma4(s[j][t], vrow[16 * c], oacc[c]);
                 }
         }
-        __syncthreads();  // every wave is done with buffer `buf` before it is restaged
+    };
+    // step for tile kv0 in LDS buffer BUF: stage tile kv0+BK from (KR, VR) into the other
+    // buffer, refill (KR, VR) with tile kv0+3BK, compute, and wait until every wave is done
+    // with buffer BUF before it is restaged
+#define FA_STEP(KV0, BUF, KR, VR)                                                            \
+    {                                                                                        \
+        if ((KV0) + BK < k_end) {                                                            \
+            FA_LSTORE((BUF) ^ 1, KR, VR)                                                     \
+            if ((KV0) + 3 * BK < k_end) { FA_GLOAD((KV0) + 3 * BK, KR, VR) }                \
+        }                                                                                    \
+        if ((KV0) < wave_kend) tile(KV0, BUF); /* else every key is masked for this wave */  \
+        __syncthreads();                                                                     \
     }
+    for (int kv0 = 0; kv0 < k_end; kv0 += 2 * BK) {
+        FA_STEP(kv0, 0, kra, vra)
+        if (kv0 + BK >= k_end) break;
+        FA_STEP(kv0 + BK, 1, krb, vrb)
+    }
+#undef FA_STEP
     float l_run = l_part + __shfl_xor(l_part, 16, WAVE);
     l_run += __shfl_xor(l_run, 32, WAVE);
 
