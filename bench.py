@@ -83,21 +83,30 @@ def cpu_baseline(step_flops, B):
                       f"({step_flops / 1e9:.1f} GFLOP: all projections + attention + LM head)"}
 
 
-def run_gpt2(jas, steps=32, warmup=4, graph=True):
-    """Config 4 shape: GPT-2-small, batch 8, 512-token prompts; returns decode tok/s."""
+def gpt2_decode_bytes(L, d, F, V, B, ctx):
+    """HBM bytes of one GPT-2-style decode step: every weight matrix and bias once (the LM
+    head is the tied embedding), plus K and V of the `ctx` cached positions per sequence."""
+    weights = 4 * (L * (3 * d * d + d * d + 2 * d * F + 3 * d + d + F + d + 4 * d) + V * d + 2 * d)
+    return weights + B * L * 2 * d * 4 * ctx
+
+
+def run_gpt2(jas, cfg_args, B, P, seed, steps, warmup, graph=True):
+    """Greedy decode of a GPT-2-style LM (configs 1 and 4); returns (tok/s, ms per step,
+    HBM bytes per step at the timed steps' mean context)."""
     from oracle_lib import randint
-    B, P = 8, 512
-    cfg = jas.LmConfig(0, 12, 768, 12, 3072, 50257, 1024, B, 1e-5, 10000.0)
+    L, d, H, F, V, ctx = cfg_args
+    cfg = jas.LmConfig(0, L, d, H, F, V, ctx, B, 1e-5, 10000.0)
     lm = jas.Lm(cfg)
     lm.use_graph(graph)
-    lm.init_random(3, 0.02)
-    lm.prefill(randint((B, P), 50257, 3))
+    lm.init_random(seed, 0.02)
+    lm.prefill(randint((B, P), V, seed))
     lm.generate(warmup, B)
     t0 = time.perf_counter()
     lm.generate(steps, B)
     dt = time.perf_counter() - t0
     lm.close()
-    return B * steps / dt, 1e3 * dt / steps
+    mean_ctx = P + warmup + (steps + 1) / 2.0
+    return B * steps / dt, 1e3 * dt / steps, gpt2_decode_bytes(L, d, F, V, B, mean_ctx)
 
 
 def run_kernel_legs(jas, reps=10):
@@ -401,15 +410,32 @@ def main():
     step_flops = 2.0 * B * (L * (3 * d * d + d * d + 3 * d * F) + V * d) + 4.0 * B * L * H * (P + 64) * dh
     cpu = None if args.no_cpu else cpu_baseline(step_flops, B)
 
-    gpt2 = None
+    # prefill: all projections of every prompt token, causal attention, the LM head for the
+    # last position of each sequence
+    prefill_flops = (2.0 * B * P * L * (4 * d * d + 3 * d * F) + B * 4.0 * L * H * (P * P / 2.0) * dh
+                     + 2.0 * B * V * d)
+    gpt2 = tiny = None
     if not args.no_gpt2:
         lm.close()
         try:
-            g_tok, g_ms = run_gpt2(jas, graph=not args.no_graph)
+            g_tok, g_ms, g_bytes = run_gpt2(jas, (12, 768, 12, 3072, 50257, 1024), 8, 512, 3, 32, 4,
+                                            graph=not args.no_graph)
+            g_frac = g_bytes / (g_ms * 1e-3) / 1e9 / HBM_PEAK_GBS
             gpt2 = {"decode_tok_s": round(g_tok, 1), "ms_per_step": round(g_ms, 3),
-                    "workload": "config4: GPT-2-small fp32, batch 8, 512-token prompts, greedy decode"}
+                    "hbm_bytes_per_step": round(g_bytes), "step_hbm_frac": round(g_frac, 4),
+                    "workload": "config4: GPT-2-small fp32, batch 8, 512-token prompts, greedy decode "
+                                "(32 timed steps after 4 warm-up)"}
+            log(f"[bench] gpt2-small decode: {g_tok:.1f} tok/s, {g_ms:.3f} ms/step, {100 * g_frac:.1f}% of HBM peak")
+            t_tok, t_ms, t_bytes = run_gpt2(jas, (2, 128, 4, 512, 256, 64), 1, 32, 0, 31, 1,
+                                            graph=not args.no_graph)
+            tiny = {"decode_tok_s": round(t_tok, 1), "ms_per_step": round(t_ms, 4),
+                    "workload": "config1: tiny GPT-2 fp32 (2 layers, d 128), batch 1, 32-token prompt, "
+                                "32 greedy steps (31 timed after 1 warm-up)",
+                    "bound": "launch latency (about 8 kernels per layer; %.2f MB of weights and KV per step)"
+                             % (t_bytes / 1e6)}
+            log(f"[bench] tiny gpt2 decode: {t_tok:.1f} tok/s, {1e3 * t_ms:.1f} us/step")
         except Exception as e:  # the headline number stands on its own
-            log("[bench] gpt2 leg failed:", e)
+            log("[bench] gpt2 legs failed:", e)
 
     line = {
         "metric": "decode tok/s (GPT-2-small, LLaMA-7B shape); kernel % of HBM/MFMA peak",
@@ -438,8 +464,12 @@ def main():
                           "launches_by_class": {"weight_gemm": cnt[0], "attention": cnt[1], "other": cnt[2]},
                           "wall_s": round(dt_prof, 4)},
         "prefill_tok_s": round(B * P / prefill_s, 1),
+        "prefill_mfma": {"tflops": round(prefill_flops / prefill_s / 1e12, 2), "peak": 157.3,
+                         "frac": round(prefill_flops / prefill_s / 1e12 / 157.3, 4),
+                         "flops": prefill_flops, "note": "fp32 MFMA peak; wall time of the whole prefill"},
         "cpu_baseline": cpu,
         "gpt2_small": gpt2,
+        "tiny_gpt2": tiny,
         "kernels": kernels,
     }
     print(json.dumps(line), flush=True)
