@@ -241,6 +241,13 @@ typedef struct {
     int32_t kind;      /* 0 GPT-2 (pre-LN, GELU, learned positions, tied head), 1 LLaMA */
     int32_t n_layer, d_model, n_head, d_ff, vocab, max_ctx, max_batch;
     float eps, rope_theta;
+    /* Storage precision (0 = fp32, the reference's arithmetic; 1 = bf16, round to nearest
+     * even).  weight_bf16: the projection matrices and the LM head (GPT-2: the tied
+     * embedding) are stored as bf16 and widened to fp32 on load; norms, biases and
+     * embeddings stay fp32, every product accumulates in fp32.  kv_bf16: the KV cache holds
+     * bf16 keys/values; a prefill attends over the fp32 keys/values it has just computed
+     * and stores them rounded, every later step attends over the rounded cache. */
+    int32_t weight_bf16, kv_bf16;
 } jas_lm_config;
 
 typedef struct jas_lm jas_lm;

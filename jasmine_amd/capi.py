@@ -43,7 +43,7 @@ class Ins(C.Structure):
 class LmConfig(C.Structure):
     _fields_ = [("kind", C.c_int32), ("n_layer", C.c_int32), ("d_model", C.c_int32), ("n_head", C.c_int32),
                 ("d_ff", C.c_int32), ("vocab", C.c_int32), ("max_ctx", C.c_int32), ("max_batch", C.c_int32),
-                ("eps", C.c_float), ("rope_theta", C.c_float)]
+                ("eps", C.c_float), ("rope_theta", C.c_float), ("weight_bf16", C.c_int32), ("kv_bf16", C.c_int32)]
 
 
 _sigs = {

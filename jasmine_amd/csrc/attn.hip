@@ -23,11 +23,6 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c)
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float bf16_to_f32(uint16_t v)
-{
-    return __uint_as_float((uint32_t)v << 16);
-}
-
 template <bool BF16>
 __device__ __forceinline__ float4 load4(const void *base, long idx)
 {
@@ -381,7 +376,8 @@ __global__ void __launch_bounds__(64 * FaWaves<BF16>::value) flash_prefill_kerne
 
 // ---------------------------------------------------------------- decode
 struct DecodeArgs {
-    const float *q, *K, *V;
+    const float *q;
+    const void *K, *V;  // fp32 or (KB) bf16 elements
     float *O;
     const int32_t *seqlens;
     float *part;  // [B*H][nsplit][D + 2]
@@ -399,9 +395,11 @@ __device__ __forceinline__ long decode_out_index(const DecodeArgs &p, int bh, in
 }
 
 // TPK lanes per key (D/4 floats each); each group of TPK lanes walks its own keys.
-template <int D>
+// KB: the cache holds bf16 keys/values (8-byte loads, widened to fp32).
+template <int D, bool KB>
 __global__ void __launch_bounds__(256) attn_decode_kernel(const DecodeArgs p)
 {
+    using KT = typename std::conditional<KB, uint16_t, float>::type;
     constexpr int TPK = D / 4;              // lanes per key
     constexpr int GPW = WAVE / TPK;         // key groups per wave
     constexpr int NG = 4 * GPW;             // key groups per workgroup
@@ -417,8 +415,12 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(const DecodeArgs p)
 
     float4 q = *(const float4 *)(p.q + (long)bh * D + 4 * lig);
     q.x *= p.scale_log2; q.y *= p.scale_log2; q.z *= p.scale_log2; q.w *= p.scale_log2;
-    const float *Kb = p.K + (long)b * p.k_sb + (long)h * p.k_sh + 4 * lig;
-    const float *Vb = p.V + (long)b * p.k_sb + (long)h * p.k_sh + 4 * lig;
+    const KT *Kb = (const KT *)p.K + (long)b * p.k_sb + (long)h * p.k_sh + 4 * lig;
+    const KT *Vb = (const KT *)p.V + (long)b * p.k_sb + (long)h * p.k_sh + 4 * lig;
+    auto ldkv = [](const KT *a) -> floatx4 {
+        if constexpr (KB) return widen_bf16x4(__builtin_nontemporal_load((const u32x2 *)a));
+        else return __builtin_nontemporal_load((const floatx4 *)a);
+    };
 
     float m = -FLT_MAX, l = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -429,8 +431,8 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(const DecodeArgs p)
         for (int u = 0; u < U; ++u) {
             int key = kk + u * NG;
             bool ok = key < k1;
-            kv[u] = ok ? __builtin_nontemporal_load((const floatx4 *)(Kb + (long)key * D)) : floatx4{0.f, 0.f, 0.f, 0.f};
-            vv[u] = ok ? __builtin_nontemporal_load((const floatx4 *)(Vb + (long)key * D)) : floatx4{0.f, 0.f, 0.f, 0.f};
+            kv[u] = ok ? ldkv(Kb + (long)key * D) : floatx4{0.f, 0.f, 0.f, 0.f};
+            vv[u] = ok ? ldkv(Vb + (long)key * D) : floatx4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -509,9 +511,9 @@ static int decode_nsplit(int B, int H, int D, int max_len, int *chunk)
     return std::max(1, (max_len + ch - 1) / ch);
 }
 
-jas_status attn_decode_impl(const float *q, const float *K, const float *V, float *O, const int32_t *seqlens, int B,
+jas_status attn_decode_impl(const float *q, const void *K, const void *V, float *O, const int32_t *seqlens, int B,
                             int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, hipStream_t s,
-                            int o_packed_d)
+                            int o_packed_d, bool kv_bf16)
 {
     JAS_CHECK(q && K && V && O && seqlens, JAS_ERR_INVALID, "jas_attn_decode: null tensor");
     JAS_CHECK(B > 0 && H > 0 && max_len > 0, JAS_ERR_INVALID, "jas_attn_decode: empty shape");
@@ -526,7 +528,8 @@ jas_status attn_decode_impl(const float *q, const float *K, const float *V, floa
     dim3 grid(ns, B * H);
 #define JAS_DEC(DD)                                                                                  \
     if (D == DD) {                                                                                   \
-        hipLaunchKernelGGL((attn_decode_kernel<DD>), grid, dim3(256), 0, s, p);                      \
+        if (kv_bf16) hipLaunchKernelGGL((attn_decode_kernel<DD, true>), grid, dim3(256), 0, s, p);     \
+        else hipLaunchKernelGGL((attn_decode_kernel<DD, false>), grid, dim3(256), 0, s, p);          \
         if (ns > 1) hipLaunchKernelGGL((attn_decode_merge_kernel<DD>), dim3(B * H), dim3(DD), 0, s, p); \
     }
     JAS_DEC(32) JAS_DEC(64) JAS_DEC(128)

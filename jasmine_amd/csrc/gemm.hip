@@ -32,7 +32,9 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c)
 constexpr int TBM = 128, TBN = 128, TBK = 16, TLD = 20;  // LDS row stride (floats)
 
 // K-contiguous, outer-contiguous, generic strides, packed weights (weight_pack_offset)
-enum LoadMode : int { LM_KC = 0, LM_OC = 1, LM_GEN = 2, LM_PK = 3 };
+// and the packed layout with bf16 elements (widened on load)
+enum LoadMode : int { LM_KC = 0, LM_OC = 1, LM_GEN = 2, LM_PK = 3, LM_PKB = 4 };
+
 
 // Loads a [128 outer x 16 k] tile of X(o, k) = X[o*so + k*sk] into registers, then LDS
 // rows [o][k] (K-contiguous, padded stride TLD).
@@ -51,14 +53,18 @@ struct TileLoader {
                 if (go < O && gk < K) v = *(const float4 *)(X + (long)go * so + gk);
                 r[4 * q] = v.x; r[4 * q + 1] = v.y; r[4 * q + 2] = v.z; r[4 * q + 3] = v.w;
             }
-        } else if (MODE == LM_PK) {  // 8 row tiles x one 16-wide K block: 8 contiguous 1 KB blocks
+        } else if (MODE == LM_PK || MODE == LM_PKB) {  // 8 row tiles x one 16-wide K block: 8 contiguous blocks
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 int idx = tid + q * 256, i = idx >> 6, ln = idx & 63;
                 long rt = o0 / 16 + i;
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (rt * 16 < O) v = *(const float4 *)(X + weight_tile_offset(rt, k0 >> 4, K >> 4, (O + 15) >> 4) + ln * 4);
-                r[4 * q] = v.x; r[4 * q + 1] = v.y; r[4 * q + 2] = v.z; r[4 * q + 3] = v.w;
+                floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (rt * 16 < O) {
+                    const long off = weight_tile_offset(rt, k0 >> 4, K >> 4, (O + 15) >> 4) + ln * 4;
+                    if (MODE == LM_PKB) v = widen_bf16x4(*(const u32x2 *)((const uint16_t *)(const void *)X + off));
+                    else v = *(const floatx4 *)(X + off);
+                }
+                r[4 * q] = v[0]; r[4 * q + 1] = v[1]; r[4 * q + 2] = v[2]; r[4 * q + 3] = v[3];
             }
         } else if (MODE == LM_OC) {
 #pragma unroll
@@ -86,7 +92,7 @@ struct TileLoader {
                 int idx = tid + q * 256, o = idx >> 2, kq = (idx & 3) * 4;
                 *(float4 *)(lds + o * TLD + kq) = make_float4(r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]);
             }
-        } else if (MODE == LM_PK) {
+        } else if (MODE == LM_PK || MODE == LM_PKB) {
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 int idx = tid + q * 256, i = idx >> 6, ln = idx & 63;
@@ -231,22 +237,25 @@ static int pick_mode(const float *X, long so, long sk, int O, int K, long bstrid
     return LM_GEN;
 }
 
-jas_status gemm_general(int M, int N, int K, const float *A, long as0, long as1, const float *B, long bs0, long bs1,
+jas_status gemm_general(int M, int N, int K, const void *A, long as0, long as1, const float *B, long bs0, long bs1,
                         float *C, long cs0, long cs1, const float *bias, int bias_mode, int act, int accumulate,
-                        int batch, long abs_, long bbs, long cbs, long biasbs, hipStream_t s, bool a_packed)
+                        int batch, long abs_, long bbs, long cbs, long biasbs, hipStream_t s, bool a_packed,
+                        bool a_bf16)
 {
+    JAS_CHECK(!a_bf16 || a_packed, JAS_ERR_INVALID, "gemm: bf16 A only in the packed layout");
     TileArgs p;
-    p.A = A; p.B = B; p.C = C; p.bias = bias_mode ? bias : nullptr;
+    p.A = (const float *)A; p.B = B; p.C = C; p.bias = bias_mode ? bias : nullptr;
     p.as0 = as0; p.as1 = as1; p.bs0 = bs0; p.bs1 = bs1; p.cs0 = cs0; p.cs1 = cs1;
     p.abs_ = abs_; p.bbs = bbs; p.cbs = cbs; p.biasbs = biasbs;
     p.M = M; p.N = N; p.K = K;
     p.bias_mode = bias_mode; p.act = act; p.accumulate = accumulate;
     JAS_CHECK(!a_packed || (K % 16 == 0 && batch == 1), JAS_ERR_INVALID, "gemm: packed A needs K % 16 == 0");
-    int am = a_packed ? LM_PK : pick_mode(A, as0, as1, M, K, abs_);
+    int am = a_packed ? (a_bf16 ? LM_PKB : LM_PK) : pick_mode((const float *)A, as0, as1, M, K, abs_);
     int bm = pick_mode(B, bs1, bs0, N, K, bbs);
     bool c4 = cs0 == 1 && al16(C) && (cs1 % 4 == 0) && (cbs % 4 == 0);
     dim3 grid(ceil_div(N, TBN), ceil_div(M, TBM), batch);
-    if (am == LM_PK) launch_tile_b<LM_PK>(p, bm, c4, grid, s);
+    if (am == LM_PKB) launch_tile_b<LM_PKB>(p, bm, c4, grid, s);
+    else if (am == LM_PK) launch_tile_b<LM_PK>(p, bm, c4, grid, s);
     else if (am == LM_KC) launch_tile_b<LM_KC>(p, bm, c4, grid, s);
     else if (am == LM_OC) launch_tile_b<LM_OC>(p, bm, c4, grid, s);
     else launch_tile_b<LM_GEN>(p, bm, c4, grid, s);
@@ -264,11 +273,16 @@ jas_status gemm_general(int M, int N, int K, const float *A, long as0, long as1,
 // PACKED weights (weight_pack_offset): each wave-wide load is one contiguous 1 KB block
 // holding exactly the A-operand float4s of 64 lanes, so a workgroup streams its rows as
 // long contiguous runs instead of 16 rows x 64 B scattered 4*K bytes apart.
-template <int NT, int WPB, int DEPTH, bool DUAL, bool PACKED>
+//
+// WB (packed only): the weights are bf16 -- the same layout at 2 bytes per element, so one
+// wave-wide load is a contiguous 512-byte block, widened to fp32 in registers.
+template <int NT, int WPB, int DEPTH, bool DUAL, bool PACKED, bool WB>
 __global__ void __launch_bounds__(WPB * 64)
-skinny_kernel(const float *__restrict__ W, const float *__restrict__ W2, const float *__restrict__ X, long ldx, int M,
+skinny_kernel(const void *__restrict__ W, const void *__restrict__ W2, const float *__restrict__ X, long ldx, int M,
               int N, int K, const SkinnyEpiArgs epi)
 {
+    static_assert(!WB || PACKED, "bf16 weights are packed");
+    using WT = typename std::conditional<WB, uint16_t, float>::type;
     constexpr int ITEMS = NT * 64;
     __shared__ floatx4 red[WPB][NT][64];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -277,11 +291,11 @@ skinny_kernel(const float *__restrict__ W, const float *__restrict__ W2, const f
     const int K16 = K >> 4;
 
     const long RG = (M + 15) >> 4;  // row tiles of the packed layout
-    const float *wp[NT];
+    const WT *wp[NT];
     long wrt[NT];  // packed: this tile's row-tile index
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        const float *base = (DUAL && t == 1) ? W2 : W;
+        const WT *base = (const WT *)((DUAL && t == 1) ? W2 : W);
         if (PACKED) {
             // tiles past the last row tile (M not a multiple of NT*16) re-read the last one;
             // their rows are >= M and the epilogue discards them
@@ -322,7 +336,10 @@ skinny_kernel(const float *__restrict__ W, const float *__restrict__ W2, const f
         for (int q = 0; q < 4; ++q) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                if (PACKED)
+                if (WB)
+                    wv[t][q] = widen_bf16x4(__builtin_nontemporal_load(
+                        (const u32x2 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG))));
+                else if (PACKED)
                     wv[t][q] = __builtin_nontemporal_load(
                         (const floatx4 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG)));
                 else
@@ -375,7 +392,10 @@ skinny_kernel(const float *__restrict__ W, const float *__restrict__ W2, const f
             const bool in = PACKED ? (4 * c + q) < K16 : (k + 16 * q + 4 * g) < K;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                if (PACKED)
+                if (WB)
+                    wb[0][t][q] = in ? widen_bf16x4(*(const u32x2 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG)))
+                                     : floatx4{0.f, 0.f, 0.f, 0.f};
+                else if (PACKED)
                     wb[0][t][q] = in ? *(const floatx4 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG))
                                      : floatx4{0.f, 0.f, 0.f, 0.f};
                 else
@@ -452,23 +472,30 @@ skinny_kernel(const float *__restrict__ W, const float *__restrict__ W2, const f
                     v[2 * pr + 1] = (float)(x0 * sn + x1 * cs);
                 }
             }
-            float *dst;
-            if (sec == 0) dst = epi.q_out + (long)n * epi.d + e;
-            else dst = (sec == 1 ? epi.k_cache : epi.v_cache) + (long)n * epi.kv_sb + (long)h * epi.kv_sh +
-                       (long)pos * epi.dh + ee;
-            *(float4 *)dst = make_float4(v[0], v[1], v[2], v[3]);
+            if (sec == 0) {
+                *(float4 *)(epi.q_out + (long)n * epi.d + e) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+                const long ce = (long)n * epi.kv_sb + (long)h * epi.kv_sh + (long)pos * epi.dh + ee;
+                float *cache = sec == 1 ? epi.k_cache : epi.v_cache;
+                if (epi.kv_bf16)
+                    *(u32x2 *)((uint16_t *)cache + ce) =
+                        u32x2{(uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                              (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16)};
+                else
+                    *(float4 *)(cache + ce) = make_float4(v[0], v[1], v[2], v[3]);
+            }
         }
     }
 }
 
-template <int NT, int WPB, int DEPTH, bool DUAL, bool PACKED>
-static void launch_skinny(const float *W, const float *W2, const float *X, long ldx, int M, int N, int K,
+template <int NT, int WPB, int DEPTH, bool DUAL, bool PACKED, bool WB = false>
+static void launch_skinny(const void *W, const void *W2, const float *X, long ldx, int M, int N, int K,
                           const SkinnyEpiArgs &epi, hipStream_t s)
 {
     const int rows = DUAL ? 16 : NT * 16;
     const int ks = epi.mode == EPI_PARTIAL ? std::max(1, epi.ksplit) : 1;
-    hipLaunchKernelGGL((skinny_kernel<NT, WPB, DEPTH, DUAL, PACKED>), dim3((M + rows - 1) / rows, ks), dim3(WPB * 64), 0,
-                       s, W, W2, X, ldx, M, N, K, epi);
+    hipLaunchKernelGGL((skinny_kernel<NT, WPB, DEPTH, DUAL, PACKED, WB>), dim3((M + rows - 1) / rows, ks),
+                       dim3(WPB * 64), 0, s, W, W2, X, ldx, M, N, K, epi);
 }
 
 // Geometry per decode shape, from a cold-weight sweep on MI355X (16 tokens, packed weights).
@@ -508,9 +535,10 @@ int skinny_pick_ksplit(int M, int K)
     return (nchunk + cpb - 1) / cpb;  // every split non-empty
 }
 
-jas_status skinny_gemm(const float *W, const float *W2, const float *X, long ldx, int M, int N, int K,
-                       const SkinnyEpiArgs &epi, hipStream_t s, bool packed, const SkinnyTuning *tune)
+jas_status skinny_gemm(const void *W, const void *W2, const float *X, long ldx, int M, int N, int K,
+                       const SkinnyEpiArgs &epi, hipStream_t s, bool packed, const SkinnyTuning *tune, bool wbf16)
 {
+    JAS_CHECK(!wbf16 || packed, JAS_ERR_INVALID, "skinny_gemm: bf16 weights only in the packed layout");
     JAS_CHECK(N >= 1 && N <= 16 && M > 0 && K > 0 && K % 4 == 0 && ldx % 4 == 0, JAS_ERR_INVALID,
               "skinny_gemm: unsupported shape");
     JAS_CHECK(!packed || K % 16 == 0, JAS_ERR_INVALID, "skinny_gemm: packed weights need K % 16 == 0");
@@ -543,6 +571,19 @@ jas_status skinny_gemm(const float *W, const float *W2, const float *X, long ldx
     }
 #define JAS_SK_D(NTV, WPBV, DV, PV) JAS_SK(NTV, WPBV, DV, PV, 2) JAS_SK(NTV, WPBV, DV, PV, 3) JAS_SK(NTV, WPBV, DV, PV, 4)
 #define JAS_SK_P(NTV, WPBV, DV) JAS_SK_D(NTV, WPBV, DV, true) JAS_SK_D(NTV, WPBV, DV, false)
+    if (wbf16) {  // the geometries the default tuning picks
+#define JAS_SKB(NTV, WPBV, DV, DEP)                                                           \
+    if (nt == NTV && tu.wpb == WPBV && dual == DV && tu.depth == DEP) {                      \
+        launch_skinny<NTV, WPBV, DEP, DV, true, true>(W, W2, X, ldx, M, N, K, ep, s);         \
+        JAS_LAUNCH_CHECK();                                                                    \
+        return JAS_OK;                                                                         \
+    }
+        JAS_SKB(2, 4, true, 3) JAS_SKB(2, 4, true, 4) JAS_SKB(2, 4, false, 2) JAS_SKB(2, 4, false, 3)
+        JAS_SKB(2, 4, false, 4) JAS_SKB(2, 8, false, 2) JAS_SKB(2, 8, false, 3) JAS_SKB(4, 4, false, 2)
+        JAS_SKB(4, 4, false, 3) JAS_SKB(4, 4, false, 4) JAS_SKB(1, 8, false, 3) JAS_SKB(1, 8, false, 4)
+#undef JAS_SKB
+        return fail(JAS_ERR_INVALID, "skinny_gemm: unsupported tuning for bf16 weights");
+    }
     JAS_SK_P(1, 4, false) JAS_SK_P(1, 8, false) JAS_SK_P(2, 4, false) JAS_SK_P(2, 8, false) JAS_SK_P(2, 4, true)
     JAS_SK_P(2, 8, true)
     // 1024-thread workgroups get 128 VGPRs: depth 4 would spill
@@ -557,7 +598,8 @@ jas_status skinny_gemm(const float *W, const float *W2, const float *X, long ldx
 }
 
 // ---------------------------------------------------------------- packed weight layout
-__global__ void weight_pack_kernel(const float *__restrict__ src, float *__restrict__ dst, int M, int Mp, int K,
+template <bool BF>
+__global__ void weight_pack_kernel(const void *__restrict__ src, void *__restrict__ dst, int M, int Mp, int K,
                                    int unpack)
 {
     long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -565,49 +607,63 @@ __global__ void weight_pack_kernel(const float *__restrict__ src, float *__restr
     int r, k;
     weight_pack_coords(p, K, Mp >> 4, &r, &k);
     if (unpack) {
-        if (r < M) dst[(long)r * K + k] = src[p];
+        const float v = BF ? bf16_to_f32(((const uint16_t *)src)[p]) : ((const float *)src)[p];
+        if (r < M) ((float *)dst)[(long)r * K + k] = v;
     } else {
-        dst[p] = r < M ? src[(long)r * K + k] : 0.0f;
+        const float v = r < M ? ((const float *)src)[(long)r * K + k] : 0.0f;
+        if (BF) ((uint16_t *)dst)[p] = f32_to_bf16(v);
+        else ((float *)dst)[p] = v;
     }
 }
 
-__global__ void fill_normal_packed_kernel(float *x, int M, int Mp, int K, uint64_t key, float mean, float std)
+template <bool BF>
+__global__ void fill_normal_packed_kernel(void *x, int M, int Mp, int K, uint64_t key, float mean, float std)
 {
     long stride = (long)gridDim.x * blockDim.x;
     for (long p = (long)blockIdx.x * blockDim.x + threadIdx.x; p < (long)Mp * K; p += stride) {
         int r, k;
         weight_pack_coords(p, K, Mp >> 4, &r, &k);
-        if (r >= M) {
-            x[p] = 0.0f;
-            continue;
+        float v = 0.0f;
+        if (r < M) {
+            uint64_t i = (uint64_t)r * K + k;  // the row-major element index drives the generator
+            uint64_t a = splitmix64(key + 2 * i), b = splitmix64(key + 2 * i + 1);
+            double u1 = ((double)(a >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+            double u2 = (double)(b >> 11) * (1.0 / 9007199254740992.0);
+            double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+            v = (float)((double)mean + (double)std * z);
         }
-        uint64_t i = (uint64_t)r * K + k;  // the row-major element index drives the generator
-        uint64_t a = splitmix64(key + 2 * i), b = splitmix64(key + 2 * i + 1);
-        double u1 = ((double)(a >> 11) + 1.0) * (1.0 / 9007199254740992.0);
-        double u2 = (double)(b >> 11) * (1.0 / 9007199254740992.0);
-        double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
-        x[p] = (float)((double)mean + (double)std * z);
+        if (BF) ((uint16_t *)x)[p] = f32_to_bf16(v);
+        else ((float *)x)[p] = v;
     }
 }
 
-jas_status weight_pack(const float *src, float *dst, int M, int K, bool unpack, hipStream_t s)
+jas_status weight_pack(const void *src, void *dst, int M, int K, bool unpack, hipStream_t s, bool bf16)
 {
     JAS_CHECK(K % 16 == 0, JAS_ERR_INVALID, "weight_pack: K must be a multiple of 16");
     const int Mp = (M + 15) / 16 * 16;
     long n = (long)Mp * K;
-    hipLaunchKernelGGL(weight_pack_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, s, src, dst, M, Mp, K, unpack ? 1 : 0);
+    if (bf16)
+        hipLaunchKernelGGL(weight_pack_kernel<true>, dim3(ceil_div(n, 256)), dim3(256), 0, s, src, dst, M, Mp, K,
+                           unpack ? 1 : 0);
+    else
+        hipLaunchKernelGGL(weight_pack_kernel<false>, dim3(ceil_div(n, 256)), dim3(256), 0, s, src, dst, M, Mp, K,
+                           unpack ? 1 : 0);
     JAS_LAUNCH_CHECK();
     return JAS_OK;
 }
 
-jas_status fill_normal_packed(float *x, int M, int K, uint64_t seed, uint64_t stream_id, float mean, float std,
-                              hipStream_t s)
+jas_status fill_normal_packed(void *x, int M, int K, uint64_t seed, uint64_t stream_id, float mean, float std,
+                              hipStream_t s, bool bf16)
 {
     JAS_CHECK(K % 16 == 0, JAS_ERR_INVALID, "fill_normal_packed: K must be a multiple of 16");
     const int Mp = (M + 15) / 16 * 16;
     unsigned nb = (unsigned)std::min<long>(((long)Mp * K + 255) / 256, 65536);
-    hipLaunchKernelGGL(fill_normal_packed_kernel, dim3(nb), dim3(256), 0, s, x, M, Mp, K, stream_key(seed, stream_id),
-                       mean, std);
+    if (bf16)
+        hipLaunchKernelGGL(fill_normal_packed_kernel<true>, dim3(nb), dim3(256), 0, s, x, M, Mp, K,
+                           stream_key(seed, stream_id), mean, std);
+    else
+        hipLaunchKernelGGL(fill_normal_packed_kernel<false>, dim3(nb), dim3(256), 0, s, x, M, Mp, K,
+                           stream_key(seed, stream_id), mean, std);
     JAS_LAUNCH_CHECK();
     return JAS_OK;
 }

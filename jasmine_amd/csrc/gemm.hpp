@@ -30,6 +30,7 @@ struct SkinnyEpiArgs {
     float *q_out = nullptr;   // [n][d]
     float *k_cache = nullptr; // element (n, h, t, e) at n*kv_sb + h*kv_sh + t*dh + e
     float *v_cache = nullptr;
+    int kv_bf16 = 0;          // the caches hold bf16 elements (rounded to nearest even)
     const int32_t *pos = nullptr;
     long kv_sb = 0, kv_sh = 0;
     int d = 0, dh = 0;
@@ -83,20 +84,24 @@ __host__ __device__ inline long packed_b_offset(int n, int k)
 {
     return ((long)(k >> 4) * 64 + n + 16 * ((k & 15) >> 2)) * 4 + (k & 3);
 }
-jas_status weight_pack(const float *src, float *dst, int M, int K, bool unpack, hipStream_t s);
-jas_status fill_normal_packed(float *x, int M, int K, uint64_t seed, uint64_t stream_id, float mean, float std,
-                              hipStream_t s);
+// fp32 row-major [M][K] <-> packed (unpack: packed -> row-major); bf16: the packed side
+// holds bf16 elements (packing rounds to nearest even, unpacking widens exactly)
+jas_status weight_pack(const void *src, void *dst, int M, int K, bool unpack, hipStream_t s, bool bf16 = false);
+jas_status fill_normal_packed(void *x, int M, int K, uint64_t seed, uint64_t stream_id, float mean, float std,
+                              hipStream_t s, bool bf16 = false);
 
 // C(n, m) over N <= 16 tokens: acc = W[m, :] . X[n, :].  Row-major: W [M][K], X [N][ldx].
 // packed: W in weight_pack_offset layout and X in packed_b_offset layout (ldx ignored).
 // W2 (EPI_SWIGLU only) has the same shape and layout as W.
-jas_status skinny_gemm(const float *W, const float *W2, const float *X, long ldx, int M, int N, int K,
+// wbf16 (packed only): W/W2 hold bf16 elements in the packed layout, widened to fp32 on load.
+jas_status skinny_gemm(const void *W, const void *W2, const float *X, long ldx, int M, int N, int K,
                        const SkinnyEpiArgs &epi, hipStream_t s, bool packed = false,
-                       const SkinnyTuning *tune = nullptr);
+                       const SkinnyTuning *tune = nullptr, bool wbf16 = false);
 
 // General strided GEMM (see jas_gemm in jasmine_hip.h).
-jas_status gemm_general(int M, int N, int K, const float *A, long as0, long as1, const float *B, long bs0, long bs1,
+jas_status gemm_general(int M, int N, int K, const void *A, long as0, long as1, const float *B, long bs0, long bs1,
                         float *C, long cs0, long cs1, const float *bias, int bias_mode, int act, int accumulate,
-                        int batch, long abs_, long bbs, long cbs, long biasbs, hipStream_t s, bool a_packed = false);
+                        int batch, long abs_, long bbs, long cbs, long biasbs, hipStream_t s, bool a_packed = false,
+                        bool a_bf16 = false);
 
 } // namespace jas

@@ -20,9 +20,10 @@ jas_status resid_norm(float *x, const float *part, int ks, const float *bias, co
                       int N, int d, float eps, bool rms, hipStream_t s, bool y_packed = false);
 // decode attention with an optional packed-B output (o_packed_d = H*D features) for the
 // next packed GEMM; 0 = the jas_attn_decode layout O[b][h][D]
-jas_status attn_decode_impl(const float *q, const float *K, const float *V, float *O, const int32_t *seqlens, int B,
+// kv_bf16: K/V hold bf16 elements (same element strides)
+jas_status attn_decode_impl(const float *q, const void *K, const void *V, float *O, const int32_t *seqlens, int B,
                             int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, hipStream_t s,
-                            int o_packed_d);
+                            int o_packed_d, bool kv_bf16 = false);
 
 // two-pass row argmax with caller-provided scratch of argmax_workspace_bytes(n, V) bytes
 size_t argmax_workspace_bytes(int n, int V);
@@ -43,6 +44,31 @@ jas_status argmax_impl(const float *x, int n, int V, long ld, int32_t *out, void
 #define JAS_LAUNCH_CHECK() JAS_HIP(hipGetLastError())
 
 constexpr int WAVE = 64;
+
+// fp32 -> bf16, round to nearest even (NaN stays a quiet NaN of the same sign)
+__host__ __device__ inline uint16_t f32_to_bf16(float f)
+{
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)(((u >> 16) & 0x8000u) | 0x7fc0u);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+__host__ __device__ inline float bf16_to_f32(uint16_t v)
+{
+    const uint32_t u = (uint32_t)v << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// four consecutive bf16 elements (one 8-byte load) widened to fp32
+__device__ __forceinline__ floatx4 widen_bf16x4(u32x2 u)
+{
+    return floatx4{__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                   __uint_as_float(u.y & 0xffff0000u)};
+}
 
 // ---- wave64 reductions (DPP/permute lowered by the compiler from shfl_xor) ----
 __device__ __forceinline__ float wave_sum(float v)

@@ -10,7 +10,7 @@
 //   +residual)
 // with the decode GEMMs streaming the weights straight from HBM into the matrix cores.
 //
-// HBM layout (all fp32): one weight arena, matrices [out][in] row-major (K-contiguous for
+// HBM layout (fp32, or bf16 weights / KV cache when the config asks): one weight arena, matrices [out][in] row-major (K-contiguous for
 // both the weight-streaming decode GEMM and the tiled prefill GEMM); activations
 // token-major [token][feature]; KV cache [layer][seq][head][position][head_dim] so a
 // (seq, head) key range is one contiguous stream.
@@ -25,11 +25,17 @@ namespace jas {
 
 // A stacked weight tensor: `layers` matrices of [rows][cols]; packed matrices use the
 // MFMA-native layout of weight_pack_offset with rows padded to a multiple of 16.
+// bf16 (packed only): 2-byte elements; offsets and strides stay in float (4-byte) units of
+// the arena, so a bf16 layer occupies half as many of them (cols % 16 == 0: even counts).
 struct Tensor {
     size_t off = 0, count = 0;
     int layers = 1, rows = 1, cols = 1;
-    bool packed = false;
-    long lstride() const { return (long)(packed ? (rows + 15) / 16 * 16 : rows) * cols; }
+    bool packed = false, bf16 = false;
+    long lstride() const
+    {
+        const long elems = (long)(packed ? (rows + 15) / 16 * 16 : rows) * cols;
+        return bf16 ? elems / 2 : elems;
+    }
 };
 
 __global__ void set_positions_kernel(int32_t *pos, int32_t *seqlens, int B, int p)
@@ -49,7 +55,8 @@ __global__ void prefill_positions_kernel(int32_t *pos, int B, int P)
 
 // copy the k and v sections of the prefill QKV rows into the cache:
 // qkv[(b*P + t)*3d + sec*d + h*dh + e] -> cache[b][h][t][e]
-__global__ void kv_scatter_kernel(const float *__restrict__ qkv, float *kc, float *vc, int B, int P, int H, int dh,
+template <bool KB>
+__global__ void kv_scatter_kernel(const float *__restrict__ qkv, void *kc, void *vc, int B, int P, int H, int dh,
                                   int ctx)
 {
     long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -63,8 +70,16 @@ __global__ void kv_scatter_kernel(const float *__restrict__ qkv, float *kc, floa
     int d = H * dh;
     const float *row = qkv + n * 3L * d;
     long dst = (((long)b * H + h) * ctx + t) * dh + ee;
-    *(float4 *)(kc + dst) = *(const float4 *)(row + d + e);
-    *(float4 *)(vc + dst) = *(const float4 *)(row + 2 * d + e);
+    const float4 k = *(const float4 *)(row + d + e), v = *(const float4 *)(row + 2 * d + e);
+    if (KB) {  // bf16 cache, round to nearest even
+        *(u32x2 *)((uint16_t *)kc + dst) = u32x2{(uint32_t)f32_to_bf16(k.x) | ((uint32_t)f32_to_bf16(k.y) << 16),
+                                                 (uint32_t)f32_to_bf16(k.z) | ((uint32_t)f32_to_bf16(k.w) << 16)};
+        *(u32x2 *)((uint16_t *)vc + dst) = u32x2{(uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16),
+                                                 (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16)};
+    } else {
+        *(float4 *)((float *)kc + dst) = k;
+        *(float4 *)((float *)vc + dst) = v;
+    }
 }
 
 __global__ void swiglu_kernel(const float *__restrict__ gate, const float *__restrict__ up, float *out, long n)
@@ -74,14 +89,16 @@ __global__ void swiglu_kernel(const float *__restrict__ gate, const float *__res
 }
 
 // token embedding gather from a packed [V][d] table (GPT-2 ties it to the LM head)
-__global__ void embed_packed_kernel(const float *__restrict__ wte, const float *__restrict__ wpe,
+template <bool WB>
+__global__ void embed_packed_kernel(const void *__restrict__ wte, const float *__restrict__ wpe,
                                     const int32_t *__restrict__ ids, const int32_t *__restrict__ pos,
                                     float *__restrict__ out, int n, int d, int V)
 {
     long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= (long)n * d) return;
     int t = (int)(g / d), e = (int)(g % d);
-    float v = wte[weight_pack_offset(ids[t], e, d, (V + 15) >> 4)];
+    const long off = weight_pack_offset(ids[t], e, d, (V + 15) >> 4);
+    float v = WB ? bf16_to_f32(((const uint16_t *)wte)[off]) : ((const float *)wte)[off];
     if (wpe) v = v + wpe[(long)pos[t] * d + e];
     out[g] = v;
 }
@@ -124,8 +141,8 @@ struct jas_lm {
     size_t arena_count = 0;
     std::map<std::string, Tensor> tensors;
     // KV cache
-    float *kc = nullptr, *vc = nullptr;
-    long kv_layer = 0, kv_sb = 0, kv_sh = 0;
+    float *kc = nullptr, *vc = nullptr;  // bf16 elements when cfg.kv_bf16
+    long kv_layer = 0, kv_sb = 0, kv_sh = 0;  // in elements
     // decode buffers [max_batch][...]
     float *x = nullptr, *h = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr;
     int32_t *ids = nullptr, *pos = nullptr, *seqlens = nullptr, *hist = nullptr;
@@ -168,6 +185,10 @@ struct jas_lm {
         return arena + it->second.off + (long)l * it->second.lstride();
     }
     int dh() const { return cfg.d_model / cfg.n_head; }
+    bool wbf16() const { return cfg.weight_bf16 != 0; }
+    size_t kv_es() const { return cfg.kv_bf16 ? 2 : 4; }
+    // layer l of a KV cache (element type per cfg.kv_bf16)
+    float *kv_layer_ptr(float *base, int l) const { return (float *)((char *)base + (size_t)l * kv_layer * kv_es()); }
 };
 
 namespace {
@@ -180,6 +201,7 @@ void add_tensor(jas_lm *lm, const char *name, int layers, int rows, int cols, bo
     t.rows = rows;
     t.cols = cols;
     t.packed = packed;
+    t.bf16 = packed && lm->cfg.weight_bf16;
     t.count = (size_t)layers * t.lstride();
     lm->tensors[name] = t;
     cursor += (t.count + 63) & ~size_t(63);  // 256-byte aligned tensors
@@ -239,7 +261,7 @@ jas_status norm_rows(jas_lm *lm, const float *x, float *y, int n_vec, long vstri
 jas_status proj(jas_lm *lm, const float *Wt, const float *X, int N, int M, int K, const SkinnyEpiArgs &e)
 {
     TRY(prof_begin(lm, 0));
-    TRY(skinny_gemm(Wt, nullptr, X, K, M, N, K, e, lm->stream, true));
+    TRY(skinny_gemm(Wt, nullptr, X, K, M, N, K, e, lm->stream, true, nullptr, lm->wbf16()));
     return prof_end(lm);
 }
 
@@ -269,8 +291,12 @@ jas_status embed(jas_lm *lm, const int32_t *ids, const int32_t *pos, float *out,
     const jas_lm_config &c = lm->cfg;
     TRY(prof_begin(lm, 2));
     if (c.kind == 0) {  // GPT-2: the tied, packed wte plus learned positions
-        hipLaunchKernelGGL(embed_packed_kernel, dim3(ceil_div((long)n * c.d_model, 256)), dim3(256), 0, lm->stream,
-                           lm->W("wte"), lm->W("wpe"), ids, pos, out, n, c.d_model, c.vocab);
+        if (lm->wbf16())
+            hipLaunchKernelGGL(embed_packed_kernel<true>, dim3(ceil_div((long)n * c.d_model, 256)), dim3(256), 0,
+                               lm->stream, lm->W("wte"), lm->W("wpe"), ids, pos, out, n, c.d_model, c.vocab);
+        else
+            hipLaunchKernelGGL(embed_packed_kernel<false>, dim3(ceil_div((long)n * c.d_model, 256)), dim3(256), 0,
+                               lm->stream, lm->W("wte"), lm->W("wpe"), ids, pos, out, n, c.d_model, c.vocab);
         JAS_LAUNCH_CHECK();
     } else {
         TRY(jas_embed(lm->W("wte"), nullptr, ids, pos, out, n, c.d_model, lm->stream));
@@ -308,8 +334,9 @@ jas_status decode_step(jas_lm *lm, bool device_pos)
         eq.mode = EPI_QKV;
         eq.bias = lm->LW("b_qkv", l);
         eq.q_out = lm->q;
-        eq.k_cache = lm->kc + l * lm->kv_layer;
-        eq.v_cache = lm->vc + l * lm->kv_layer;
+        eq.k_cache = lm->kv_layer_ptr(lm->kc, l);
+        eq.v_cache = lm->kv_layer_ptr(lm->vc, l);
+        eq.kv_bf16 = c.kv_bf16;
         eq.pos = lm->pos;
         eq.kv_sb = lm->kv_sb;
         eq.kv_sh = lm->kv_sh;
@@ -319,8 +346,9 @@ jas_status decode_step(jas_lm *lm, bool device_pos)
         eq.theta = c.rope_theta;
         TRY(proj(lm, lm->LW("w_qkv", l), lm->h, B, 3 * d, d, eq));
         TRY(prof_begin(lm, 1));
-        TRY(attn_decode_impl(lm->q, lm->kc + l * lm->kv_layer, lm->vc + l * lm->kv_layer, lm->att, lm->seqlens, B, H,
-                             dh, c.max_ctx, lm->kv_sb, lm->kv_sh, 1.0f / sqrtf((float)dh), lm->attn_ws, s, d));
+        TRY(attn_decode_impl(lm->q, lm->kv_layer_ptr(lm->kc, l), lm->kv_layer_ptr(lm->vc, l), lm->att, lm->seqlens, B, H,
+                             dh, c.max_ctx, lm->kv_sb, lm->kv_sh, 1.0f / sqrtf((float)dh), lm->attn_ws, s, d,
+                             c.kv_bf16 != 0));
         TRY(prof_end(lm));
         SkinnyEpiArgs eo;
         eo.mode = EPI_PARTIAL;
@@ -353,7 +381,8 @@ jas_status decode_step(jas_lm *lm, bool device_pos)
             eg.ldo = F;
             eg.out_packed = 1;
             TRY(prof_begin(lm, 0));
-            TRY(skinny_gemm(lm->LW("w_gate", l), lm->LW("w_up", l), lm->h, d, F, B, d, eg, s, true));
+            TRY(skinny_gemm(lm->LW("w_gate", l), lm->LW("w_up", l), lm->h, d, F, B, d, eg, s, true, nullptr,
+                            lm->wbf16()));
             TRY(prof_end(lm));
             TRY(proj(lm, lm->LW("w_down", l), lm->ff, B, d, F, ed));
             pend_bias = nullptr;
@@ -383,13 +412,14 @@ namespace {
 // [layers*rows][cols] tensor; each packed layer is filled with its own slice of that stream
 jas_status fill_normal_packed_layers(jas_lm *lm, const Tensor &t, float *p, uint64_t seed, uint64_t sid, float std)
 {
-    if (t.layers == 1) return fill_normal_packed(p, t.rows, t.cols, seed, sid, 0.0f, std, lm->stream);
+    if (t.layers == 1) return fill_normal_packed(p, t.rows, t.cols, seed, sid, 0.0f, std, lm->stream, t.bf16);
     // per layer: generate row-major into a scratch buffer, then pack
     float *tmp = nullptr;
     TRY(jas_malloc((void **)&tmp, (size_t)t.rows * t.cols * t.layers * sizeof(float)));
     jas_status st = jas_fill_normal(tmp, (size_t)t.rows * t.cols * t.layers, seed, sid, 0.0f, std, lm->stream);
     for (int l = 0; l < t.layers && st == JAS_OK; ++l)
-        st = weight_pack(tmp + (long)l * t.rows * t.cols, p + (long)l * t.lstride(), t.rows, t.cols, false, lm->stream);
+        st = weight_pack(tmp + (long)l * t.rows * t.cols, p + (long)l * t.lstride(), t.rows, t.cols, false, lm->stream,
+                         t.bf16);
     (void)hipStreamSynchronize(lm->stream);
     (void)hipFree(tmp);
     return st;
@@ -415,6 +445,8 @@ jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out)
     // one 16-row packed tile never mixes two heads or the q/k/v sections
     JAS_CHECK((c.d_model / c.n_head) % 16 == 0, JAS_ERR_INVALID, "jas_lm_create: head dim must be a multiple of 16");
     JAS_CHECK(c.max_batch <= 16, JAS_ERR_INVALID, "jas_lm_create: max_batch above 16 is not supported");
+    JAS_CHECK((c.weight_bf16 == 0 || c.weight_bf16 == 1) && (c.kv_bf16 == 0 || c.kv_bf16 == 1), JAS_ERR_INVALID,
+              "jas_lm_create: weight_bf16 and kv_bf16 must be 0 or 1");
     TRY(jas_init(-1));
     jas_lm *lm = new jas_lm();
     lm->cfg = c;
@@ -456,8 +488,8 @@ jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out)
     lm->kv_sb = (long)c.n_head * lm->kv_sh;
     lm->kv_layer = (long)Bm * lm->kv_sb;
     size_t kvn = (size_t)L * lm->kv_layer;
-    st = jas_malloc((void **)&lm->kc, kvn * sizeof(float));
-    if (st == JAS_OK) st = jas_malloc((void **)&lm->vc, kvn * sizeof(float));
+    st = jas_malloc((void **)&lm->kc, kvn * lm->kv_es());
+    if (st == JAS_OK) st = jas_malloc((void **)&lm->vc, kvn * lm->kv_es());
     // decode activations span all 16 MFMA token columns (the packed B-operand layout)
     struct { float **p; size_t n; } fb[] = {{&lm->x, 16 * d}, {&lm->h, 16 * d}, {&lm->q, 16 * d}, {&lm->att, 16 * d},
                                             {&lm->ff, 16 * F}, {&lm->logits, Bm * V}};
@@ -559,8 +591,8 @@ static jas_status weight_copy(jas_lm *lm, const char *name, float *h, size_t cou
     const long lsz = (long)t.rows * t.cols;
     if (!to_host) st = jas_memcpy_h2d(tmp, h, n * sizeof(float), lm->stream);
     for (int l = 0; l < t.layers && st == JAS_OK; ++l)
-        st = to_host ? weight_pack(dev + l * t.lstride(), tmp + l * lsz, t.rows, t.cols, true, lm->stream)
-                     : weight_pack(tmp + l * lsz, dev + l * t.lstride(), t.rows, t.cols, false, lm->stream);
+        st = to_host ? weight_pack(dev + l * t.lstride(), tmp + l * lsz, t.rows, t.cols, true, lm->stream, t.bf16)
+                     : weight_pack(tmp + l * lsz, dev + l * t.lstride(), t.rows, t.cols, false, lm->stream, t.bf16);
     if (to_host && st == JAS_OK) st = jas_memcpy_d2h(h, tmp, n * sizeof(float), lm->stream);
     (void)hipStreamSynchronize(lm->stream);
     (void)hipFree(tmp);
@@ -605,32 +637,39 @@ jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_
         const float *bq = lm->LW("b_qkv", l);
         // QKV[n][m] = sum_k w_qkv[m][k] H[n][k] (+ b[m]); weights in the packed layout
         TRY(gemm_general(3 * d, (int)T, d, lm->LW("w_qkv", l), d, 1, lm->pH, 1, d, lm->pQKV, 1, 3L * d, bq,
-                         bq ? 1 : 0, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true));
+                         bq ? 1 : 0, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
         if (c.kind == 1)  // q and k sections are 2H consecutive heads of each row
             TRY(jas_rope_llama(lm->pQKV, lm->pPos, (int)T, 2 * H, dh, 3L * d, c.rope_theta, s));
-        float *kcl = lm->kc + l * lm->kv_layer, *vcl = lm->vc + l * lm->kv_layer;
-        hipLaunchKernelGGL(kv_scatter_kernel, dim3(ceil_div(T * (d / 4), 256)), dim3(256), 0, s, lm->pQKV, kcl, vcl,
-                           B, P, H, dh, c.max_ctx);
-        TRY(jas_attn_prefill(lm->pQKV, kcl, vcl, lm->pATT, B, H, P, P, dh, (long)P * 3 * d, dh, 3L * d, lm->kv_sb,
-                             lm->kv_sh, dh, (long)P * d, dh, d, 1.0f / sqrtf((float)dh), 1, JAS_F32, s));
+        float *kcl = lm->kv_layer_ptr(lm->kc, l), *vcl = lm->kv_layer_ptr(lm->vc, l);
+        if (c.kv_bf16)
+            hipLaunchKernelGGL(kv_scatter_kernel<true>, dim3(ceil_div(T * (d / 4), 256)), dim3(256), 0, s, lm->pQKV,
+                               kcl, vcl, B, P, H, dh, c.max_ctx);
+        else
+            hipLaunchKernelGGL(kv_scatter_kernel<false>, dim3(ceil_div(T * (d / 4), 256)), dim3(256), 0, s, lm->pQKV,
+                               kcl, vcl, B, P, H, dh, c.max_ctx);
+        // the prompt attends over the keys/values just computed (fp32, in the QKV rows);
+        // the cache keeps them for the decode steps (rounded when it is bf16)
+        const long qs = (long)P * 3 * d;
+        TRY(jas_attn_prefill(lm->pQKV, lm->pQKV + d, lm->pQKV + 2 * d, lm->pATT, B, H, P, P, dh, qs, dh, 3L * d, qs,
+                             dh, 3L * d, (long)P * d, dh, d, 1.0f / sqrtf((float)dh), 1, JAS_F32, s));
         const float *bo = lm->LW("b_o", l);
         TRY(gemm_general(d, (int)T, d, lm->LW("w_o", l), d, 1, lm->pATT, 1, d, lm->pX, 1, d, bo, bo ? 1 : 0,
-                         JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s, true));
+                         JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
         TRY(norm_rows(lm, lm->pX, lm->pH, (int)T, d, l, 2));
         if (c.kind == 0) {
             TRY(gemm_general(F, (int)T, d, lm->LW("w_fc", l), d, 1, lm->pH, 1, d, lm->pG, 1, F, lm->LW("b_fc", l), 1,
-                             JAS_ACT_GELU, 0, 1, 0, 0, 0, 0, s, true));
+                             JAS_ACT_GELU, 0, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
             TRY(gemm_general(d, (int)T, F, lm->LW("w_proj", l), F, 1, lm->pG, 1, F, lm->pX, 1, d,
-                             lm->LW("b_proj", l), 1, JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s, true));
+                             lm->LW("b_proj", l), 1, JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
         } else {
             TRY(gemm_general(F, (int)T, d, lm->LW("w_gate", l), d, 1, lm->pH, 1, d, lm->pG, 1, F, nullptr, 0,
-                             JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true));
+                             JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
             TRY(gemm_general(F, (int)T, d, lm->LW("w_up", l), d, 1, lm->pH, 1, d, lm->pU, 1, F, nullptr, 0,
-                             JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true));
+                             JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
             hipLaunchKernelGGL(swiglu_kernel, dim3(ceil_div(T * F, 256)), dim3(256), 0, s, lm->pG, lm->pU, lm->pFF,
                                T * F);
             TRY(gemm_general(d, (int)T, F, lm->LW("w_down", l), F, 1, lm->pFF, 1, F, lm->pX, 1, d, nullptr, 0,
-                             JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s, true));
+                             JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
         }
     }
     // final norm and LM head on the last position of every sequence (packed B operand)
@@ -642,7 +681,8 @@ jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_
     eh.mode = EPI_STORE;
     eh.out = lm->logits;
     eh.ldo = V;
-    TRY(skinny_gemm(c.kind == 0 ? lm->W("wte") : lm->W("w_head"), nullptr, lm->h, d, V, B, d, eh, s, true));
+    TRY(skinny_gemm(c.kind == 0 ? lm->W("wte") : lm->W("w_head"), nullptr, lm->h, d, V, B, d, eh, s, true, nullptr,
+                    lm->wbf16()));
     TRY(argmax_impl(lm->logits, B, V, V, lm->ids, lm->argmax_ws, s));
     lm->position = P;
     if (h_next) TRY(jas_memcpy_d2h(h_next, lm->ids, B * sizeof(int32_t), s));

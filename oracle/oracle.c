@@ -519,9 +519,34 @@ static float *kv_at(const lm_state *st, float *base, int b, int l, int h, int t)
     return base + ((((long)b * c->n_layer + l) * c->n_head + h) * c->max_ctx + t) * dh;
 }
 
+/* fp32 -> bf16 -> fp32, round to nearest even (the cache element of a bf16 KV cache) */
+static float round_bf16(float f)
+{
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return f;
+    u = ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16) << 16;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* Round every cached key/value of sequence b at positions [0, n) (bf16 KV cache). */
+static void lm_round_cache(const lm_state *st, int b, int n)
+{
+    const orc_lm_cfg *c = st->c;
+    int dh = c->d_model / c->n_head;
+    for (int l = 0; l < c->n_layer; ++l)
+        for (int h = 0; h < c->n_head; ++h)
+            for (int t = 0; t < n; ++t) {
+                float *k = kv_at(st, st->kc, b, l, h, t), *v = kv_at(st, st->vc, b, l, h, t);
+                for (int e = 0; e < dh; ++e) { k[e] = round_bf16(k[e]); v[e] = round_bf16(v[e]); }
+            }
+}
+
 /* Process token `tok` at position `pos` of sequence b through all layers, attending to
- * cache entries 0..pos; writes final-norm hidden into hout[d]. */
-static void lm_token(const lm_state *st, int b, int tok, int pos, float *hout)
+ * cache entries 0..pos; writes final-norm hidden into hout[d].  round_new: the token's own
+ * key/value enter the cache rounded to bf16 (a generated token under a bf16 KV cache). */
+static void lm_token(const lm_state *st, int b, int tok, int pos, float *hout, int round_new)
 {
     const orc_lm_cfg *c = st->c;
     const orc_lm_weights *w = st->w;
@@ -546,8 +571,11 @@ static void lm_token(const lm_state *st, int b, int tok, int pos, float *hout)
                 orc_rope_llama(q, dh, pos, c->rope_theta);
                 orc_rope_llama(k, dh, pos, c->rope_theta);
             }
-            memcpy(kv_at(st, st->kc, b, l, hh, pos), k, sizeof(float) * dh);
-            memcpy(kv_at(st, st->vc, b, l, hh, pos), v, sizeof(float) * dh);
+            float *kd = kv_at(st, st->kc, b, l, hh, pos), *vd = kv_at(st, st->vc, b, l, hh, pos);
+            for (int e = 0; e < dh; ++e) {
+                kd[e] = round_new ? round_bf16(k[e]) : k[e];
+                vd[e] = round_new ? round_bf16(v[e]) : v[e];
+            }
             double scale = 1.0 / sqrt((double)dh), m = -INFINITY;
             for (int t = 0; t <= pos; ++t) {
                 const float *kt = kv_at(st, st->kc, b, l, hh, t);
@@ -609,10 +637,12 @@ void orc_lm_generate(const orc_lm_cfg *cfg, const orc_lm_weights *w, int B, int 
 #pragma omp parallel for schedule(dynamic) if (B > 1)
     for (int b = 0; b < B; ++b) {
         float *hf = malloc(sizeof(float) * d), *lg = malloc(sizeof(float) * V);
-        for (int t = 0; t < P - 1; ++t) lm_token(&st, b, prompt[(long)b * P + t], t, hf);
+        for (int t = 0; t < P - 1; ++t) lm_token(&st, b, prompt[(long)b * P + t], t, hf, 0);
         int tok = prompt[(long)b * P + P - 1];
         for (int s = 0; s < steps; ++s) {
-            lm_token(&st, b, tok, P - 1 + s, hf);
+            /* step 0 is the prompt's last token: part of the prefill */
+            lm_token(&st, b, tok, P - 1 + s, hf, s > 0 && cfg->kv_bf16);
+            if (s == 0 && cfg->kv_bf16) lm_round_cache(&st, b, P);
             lm_logits(&st, hf, lg);
             int nx = orc_argmax(lg, V);
             out_ids[(long)b * steps + s] = nx;
@@ -638,7 +668,7 @@ void orc_lm_last_logits(const orc_lm_cfg *cfg, const orc_lm_weights *w, int B, i
 #pragma omp parallel for schedule(dynamic) if (B > 1)
     for (int b = 0; b < B; ++b) {
         float *hf = malloc(sizeof(float) * d);
-        for (int t = 0; t < T; ++t) lm_token(&st, b, ids[(long)b * T + t], t, hf);
+        for (int t = 0; t < T; ++t) lm_token(&st, b, ids[(long)b * T + t], t, hf, 0);
         lm_logits(&st, hf, logits + (long)b * cfg->vocab);
         free(hf);
     }

@@ -123,6 +123,11 @@ typedef struct {
     int n_layer, d_model, n_head, d_ff, vocab, max_ctx;
     float eps;       /* 1e-5 GPT-2 LN, 1e-6 LLaMA RMSNorm */
     float rope_theta;
+    /* 1: the KV cache stores keys/values rounded to bf16 (nearest even).  The prompt's
+     * tokens attend over the unrounded keys/values of the prompt (a prefill computes them in
+     * one pass); every generated token attends over the rounded cache, its own entry
+     * included. */
+    int kv_bf16;
 } orc_lm_cfg;
 /* Weight pointers; layer tensors are stacked [n_layer][...].  Matrices are [out][in].
  * GPT-2: wte[V][d], wpe[ctx][d], ln1_g/b, w_qkv[3d][d], b_qkv[3d], w_o[d][d], b_o[d],

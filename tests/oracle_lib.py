@@ -78,7 +78,7 @@ if orc is not None:
 class LmCfg(C.Structure):
     _fields_ = [("kind", C.c_int), ("n_layer", C.c_int), ("d_model", C.c_int), ("n_head", C.c_int),
                 ("d_ff", C.c_int), ("vocab", C.c_int), ("max_ctx", C.c_int),
-                ("eps", C.c_float), ("rope_theta", C.c_float)]
+                ("eps", C.c_float), ("rope_theta", C.c_float), ("kv_bf16", C.c_int)]
 
 
 LM_WEIGHT_FIELDS = ["wte", "wpe", "ln1_g", "ln1_b", "w_qkv", "b_qkv", "w_o", "b_o", "ln2_g", "ln2_b",

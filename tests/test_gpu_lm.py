@@ -25,7 +25,7 @@ def close(a, b, atol=ATOL, rtol=RTOL):
 def oracle_for(jas, lm, cfg):
     w = {n: lm.weight(n) for n in LM_WEIGHT_FIELDS}
     ocfg = LmCfg(cfg.kind, cfg.n_layer, cfg.d_model, cfg.n_head, cfg.d_ff, cfg.vocab, cfg.max_ctx, cfg.eps,
-                 cfg.rope_theta)
+                 cfg.rope_theta, cfg.kv_bf16)
     ow = LmWeights(*[fp(w[n]) if w[n] is not None else None for n in LM_WEIGHT_FIELDS])
     return ocfg, ow, w
 
@@ -81,6 +81,55 @@ def test_ragged_chunk_widths(jas, kind, d, H, F, V):
     # vocabularies that are not a multiple of 16 rows (padded packed head)
     cfg = jas.LmConfig(kind, 2, d, H, F, V, 40, 4, 1e-5 if kind == 0 else 1e-6, 10000.0)
     run_parity(jas, cfg, seed=9, B=4, P=13, steps=6, prompt_seed=9)
+
+
+def bf16_round(a):
+    """fp32 -> bf16 -> fp32, round to nearest even (finite inputs)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return u.astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("kind,wb,kb", [(1, 1, 1), (0, 1, 1), (1, 1, 0), (0, 0, 1)])
+def test_bf16_storage(jas, kind, wb, kb):
+    """bf16 weights and/or KV cache: the oracle runs the same model (the rounded weights read
+    back from the device, the cache rounded as the runner rounds it), so the fp32 tolerance
+    holds; FFN width 208 also exercises a partial K chunk of the bf16 weight stream."""
+    cfg = jas.LmConfig(kind, 2, 128, 4, 208, 333, 48, 4, 1e-5 if kind == 0 else 1e-6, 10000.0, wb, kb)
+    run_parity(jas, cfg, seed=12, B=4, P=11, steps=6, prompt_seed=12)
+
+
+def test_bf16_weight_roundtrip(jas):
+    # set_weight rounds to bf16 (nearest even) and get_weight widens exactly; fp32 tensors
+    # (norm gains, biases, positions) are untouched
+    cfg = jas.LmConfig(0, 2, 64, 2, 128, 50, 8, 1, 1e-5, 1e4, 1, 1)
+    lm = jas.Lm(cfg)
+    rng = np.random.default_rng(1)
+    for name, packed in (("wte", True), ("w_qkv", True), ("w_proj", True), ("b_qkv", False), ("wpe", False)):
+        l, r, c = lm.weight_shape(name)
+        a = rng.standard_normal(l * r * c).astype(np.float32)
+        lm.set_weight(name, a)
+        want = bf16_round(a) if packed else a
+        assert np.array_equal(lm.weight(name), want), name
+
+
+def test_bf16_graph_replay_matches_eager(jas):
+    cfg = jas.LmConfig(1, 2, 128, 4, 256, 300, 64, 3, 1e-6, 10000.0, 1, 1)
+    prompt = randint((3, 9), 300, 13)
+
+    def fresh():
+        lm = jas.Lm(cfg)
+        lm.init_random(13, 0.02)
+        first, _ = lm.prefill(prompt)
+        return lm, first
+
+    g, first = fresh()
+    ids_g = np.concatenate([first[:, None], g.generate(6, 3).T], 1)
+    e, first_e = fresh()
+    ids_e = [first_e]
+    for _ in range(6):
+        ids_e.append(e.decode(None, B=3)[0])
+    assert np.array_equal(ids_g, np.stack(ids_e, 1))
 
 
 def test_gpt2_small_shape(jas):

@@ -269,8 +269,18 @@ def make_lm(kind, L=2, d=64, H=2, F=128, V=97, ctx=24, seed=11):
     return cfg, w, lw
 
 
-def _np_lm_logits(kind, cfg, w, ids):
-    """Cache-free numpy (fp64) forward of one sequence, logits of the last position."""
+def _bf16(a):
+    """round to bf16 (nearest even) and back, elementwise, in fp64"""
+    f = np.asarray(a, np.float64).astype(np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def _np_lm_logits(kind, cfg, w, ids, kv_round_from=None):
+    """Cache-free numpy (fp64) forward of one sequence, logits of the last position.
+    kv_round_from = P: query positions >= P see every key/value rounded to bf16 (a bf16 KV
+    cache after a P-token prefill); positions < P see them unrounded."""
     L, d, H = cfg.n_layer, cfg.d_model, cfg.n_head
     dh = d // H
     T = len(ids)
@@ -302,11 +312,15 @@ def _np_lm_logits(kind, cfg, w, ids):
         q, k, v = (qkv[:, i * d:(i + 1) * d].reshape(T, H, dh) for i in range(3))
         if kind == 1:
             q, k = rope(q), rope(k)
-        s = np.einsum("thd,uhd->htu", q, k) / math.sqrt(dh)
-        s[:, np.triu(np.ones((T, T), bool), 1)] = -np.inf
-        p = np.exp(s - s.max(-1, keepdims=True))
-        p /= p.sum(-1, keepdims=True)
-        a = np.einsum("htu,uhd->thd", p, v).reshape(T, d)
+        def attend(kk, vv):
+            s = np.einsum("thd,uhd->htu", q, kk) / math.sqrt(dh)
+            s[:, np.triu(np.ones((T, T), bool), 1)] = -np.inf
+            p = np.exp(s - s.max(-1, keepdims=True))
+            p /= p.sum(-1, keepdims=True)
+            return np.einsum("htu,uhd->thd", p, vv).reshape(T, d)
+        a = attend(k, v)
+        if kv_round_from is not None and T > kv_round_from:
+            a[kv_round_from:] = attend(_bf16(k), _bf16(v))[kv_round_from:]
         x = x + a @ w["w_o"][l].T + (w["b_o"][l] if kind == 0 else 0)
         h = norm(x, "ln2_g", "ln2_b", l)
         if kind == 0:
@@ -319,6 +333,32 @@ def _np_lm_logits(kind, cfg, w, ids):
     hf = norm(x[-1:], "lnf_g", "lnf_b", None)
     head = w["wte"] if kind == 0 else w["w_head"]
     return (hf @ head.T)[0]
+
+
+@pytest.mark.parametrize("kind", [0, 1])
+def test_lm_oracle_bf16_kv_cache(kind):
+    """kv_bf16: the oracle's cache rounding equals the parallel numpy form (queries from the
+    prompt see unrounded keys/values, generated ones see them all rounded); the first step
+    (the prompt's last token) is unchanged, later steps move by about the bf16 rounding."""
+    cfg, w, lw = make_lm(kind)
+    cfg_r, _, _ = make_lm(kind)
+    cfg_r.kv_bf16 = 1
+    B, P, steps = 2, 5, 5
+    prompt = randint((B, P), cfg.vocab, 3)
+    ids, ids_r = np.zeros((B, steps), np.int32), np.zeros((B, steps), np.int32)
+    lg, lg_r = np.zeros((steps, B, cfg.vocab), np.float32), np.zeros((steps, B, cfg.vocab), np.float32)
+    orc.orc_lm_generate(cfg, lw, B, P, ip(prompt), steps, None, ip(ids), fp(lg), 1)
+    force = np.ascontiguousarray(ids)  # same token stream for both
+    orc.orc_lm_generate(cfg_r, lw, B, P, ip(prompt), steps, ip(force), ip(ids_r), fp(lg_r), 1)
+    assert np.array_equal(lg[0], lg_r[0])
+    assert not np.array_equal(lg[1:], lg_r[1:])
+    assert np.abs(lg - lg_r).max() < 5e-3
+    for b in range(B):
+        seq = list(prompt[b])
+        for s in range(steps):
+            ref_l = _np_lm_logits(kind, cfg, w, np.array(seq), kv_round_from=P)
+            assert np.allclose(lg_r[s, b], ref_l, atol=1e-4), (b, s)
+            seq.append(int(force[b, s]))
 
 
 @pytest.mark.parametrize("kind", [0, 1])
