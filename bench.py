@@ -36,8 +36,52 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def llama_cfg(jas, B, ctx):
-    return jas.LmConfig(1, 32, 4096, 32, 11008, 32000, ctx, B, 1e-6, 10000.0)
+def llama_cfg(jas, B, ctx, bf16=False):
+    return jas.LmConfig(1, 32, 4096, 32, 11008, 32000, ctx, B, 1e-6, 10000.0, int(bf16), int(bf16))
+
+
+def run_llama_bf16(jas, args):
+    """The config-5 shape with bf16 weight and KV-cache storage (fp32 activations and
+    accumulation; the survey's first 'next' item).  Same prompt, warm-up and timed steps as
+    the fp32 headline; returns its own line (not the headline value)."""
+    from oracle_lib import randint
+    B, P = args.batch, args.prompt
+    L, d, H, F, V = 32, 4096, 32, 11008, 32000
+    dh = d // H
+    ctx = P + args.warmup + 2 * args.steps + 1
+    lm = jas.Lm(llama_cfg(jas, B, ctx, bf16=True))
+    if args.no_graph:
+        lm.use_graph(False)
+    lm.init_random(4, 0.02)
+    lm.prefill(randint((B, P), V, 4))
+    lm.generate(args.warmup, B)
+    pos0 = lm.position
+    jas.check(jas.lib.jas_synchronize(lm.stream))
+    t0 = time.perf_counter()
+    lm.generate(args.steps, B)
+    dt = time.perf_counter() - t0
+    pos1 = lm.position
+    lm.profile(True)
+    lm.generate(args.steps, B)
+    ms, cnt = lm.profile(False)
+    lm.close()
+    w_step = 2 * (L * (4 * d * d + 3 * d * F) + V * d) + 4 * (2 * L + 1) * d
+    kv_timed = sum(B * L * H * (pos0 + st + 1) * dh * 2 * 2 for st in range(args.steps)) / args.steps
+    kv_prof = sum(B * L * H * (pos1 + st + 1) * dh * 2 * 2 for st in range(args.steps))
+    step_bytes = w_step + kv_timed
+    tok_s = B * args.steps / dt
+    frac = step_bytes / (dt / args.steps) / 1e9 / HBM_PEAK_GBS
+    gemm_gbs = (w_step - 4 * (2 * L + 1) * d) * args.steps / (ms[0] * 1e-3) / 1e9
+    attn_gbs = kv_prof / (ms[1] * 1e-3) / 1e9
+    log(f"[bench] llama bf16 storage: {tok_s:.1f} tok/s, {1e3 * dt / args.steps:.3f} ms/step, "
+        f"{100 * frac:.1f}% of HBM peak (attention {attn_gbs:.0f} GB/s, weight GEMMs {gemm_gbs:.0f} GB/s)")
+    return {"decode_tok_s": round(tok_s, 2), "ms_per_step": round(1e3 * dt / args.steps, 3),
+            "step_bytes": step_bytes, "step_hbm_frac": round(frac, 4),
+            "attention_gbs": round(attn_gbs, 1), "attention_frac": round(attn_gbs / HBM_PEAK_GBS, 4),
+            "weight_gemm_gbs": round(gemm_gbs, 1), "weight_gemm_frac": round(gemm_gbs / HBM_PEAK_GBS, 4),
+            "workload": f"config5 shape with bf16 weights and bf16 KV cache (fp32 activations and accumulation), "
+                        f"batch {B}, {P}-token prompts, timed positions {pos0}..{pos0 + args.steps - 1}",
+            "dtype": "bf16 storage / f32 compute"}
 
 
 def weight_bytes_per_step(L, d, F, V):
@@ -313,6 +357,7 @@ def main():
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--no-gpt2", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-bf16", action="store_true", help="skip the bf16-storage LLaMA leg")
     ap.add_argument("--no-kernels", action="store_true", help="skip the config 2/3 kernel lines")
     ap.add_argument("--no-graph", action="store_true",
                     help="decode with eager launches instead of graph replay (same kernels; for profilers)")
@@ -414,9 +459,15 @@ def main():
     # last position of each sequence
     prefill_flops = (2.0 * B * P * L * (4 * d * d + 3 * d * F) + B * 4.0 * L * H * (P * P / 2.0) * dh
                      + 2.0 * B * V * d)
+    lm.close()
+    llama_bf16 = None
+    if not args.no_bf16:
+        try:
+            llama_bf16 = run_llama_bf16(jas, args)
+        except Exception as e:  # the headline number stands on its own
+            log("[bench] bf16 leg failed:", e)
     gpt2 = tiny = None
     if not args.no_gpt2:
-        lm.close()
         try:
             g_tok, g_ms, g_bytes = run_gpt2(jas, (12, 768, 12, 3072, 50257, 1024), 8, 512, 3, 32, 4,
                                             graph=not args.no_graph)
@@ -468,6 +519,7 @@ def main():
                          "frac": round(prefill_flops / prefill_s / 1e12 / 157.3, 4),
                          "flops": prefill_flops, "note": "fp32 MFMA peak; wall time of the whole prefill"},
         "cpu_baseline": cpu,
+        "llama7b_bf16_storage": llama_bf16,
         "gpt2_small": gpt2,
         "tiny_gpt2": tiny,
         "kernels": kernels,

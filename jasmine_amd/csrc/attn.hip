@@ -400,7 +400,8 @@ template <int D, bool KB>
 __global__ void __launch_bounds__(256) attn_decode_kernel(const DecodeArgs p)
 {
     using KT = typename std::conditional<KB, uint16_t, float>::type;
-    constexpr int TPK = D / 4;              // lanes per key
+    constexpr int EPL = KB ? 8 : 4;         // elements per lane and key: one 16-byte load
+    constexpr int TPK = D / EPL;            // lanes per key
     constexpr int GPW = WAVE / TPK;         // key groups per wave
     constexpr int NG = 4 * GPW;             // key groups per workgroup
     constexpr int U = 4;                    // keys per group per iteration (loads in flight)
@@ -413,30 +414,39 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(const DecodeArgs p)
     const int len = p.seqlens[b];
     const int k0 = split * p.chunk, k1 = min(len, k0 + p.chunk);
 
-    float4 q = *(const float4 *)(p.q + (long)bh * D + 4 * lig);
-    q.x *= p.scale_log2; q.y *= p.scale_log2; q.z *= p.scale_log2; q.w *= p.scale_log2;
-    const KT *Kb = (const KT *)p.K + (long)b * p.k_sb + (long)h * p.k_sh + 4 * lig;
-    const KT *Vb = (const KT *)p.V + (long)b * p.k_sb + (long)h * p.k_sh + 4 * lig;
-    auto ldkv = [](const KT *a) -> floatx4 {
-        if constexpr (KB) return widen_bf16x4(__builtin_nontemporal_load((const u32x2 *)a));
-        else return __builtin_nontemporal_load((const floatx4 *)a);
+    float q[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) q[e] = p.q[(long)bh * D + EPL * lig + e] * p.scale_log2;
+    const KT *Kb = (const KT *)p.K + (long)b * p.k_sb + (long)h * p.k_sh + EPL * lig;
+    const KT *Vb = (const KT *)p.V + (long)b * p.k_sb + (long)h * p.k_sh + EPL * lig;
+    // one 16-byte load per key row and lane, kept raw until it is used (bf16: eight elements
+    // widened on use, so the registers in flight are the same as for fp32)
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    auto ld16 = [](const KT *a) { return __builtin_nontemporal_load((const u32x4_t *)a); };
+    auto elem = [](const u32x4_t &u, int e) -> float {  // element e (compile-time) of a row chunk
+        if constexpr (KB) return __uint_as_float(e & 1 ? u[e >> 1] & 0xffff0000u : u[e >> 1] << 16);
+        else return __uint_as_float(u[e]);
     };
 
     float m = -FLT_MAX, l = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float acc[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
     for (int kk = k0 + grp; kk < k1; kk += NG * U) {
-        floatx4 kv[U], vv[U];
+        u32x4_t kv[U], vv[U];
         float sc[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             int key = kk + u * NG;
             bool ok = key < k1;
-            kv[u] = ok ? ldkv(Kb + (long)key * D) : floatx4{0.f, 0.f, 0.f, 0.f};
-            vv[u] = ok ? ldkv(Vb + (long)key * D) : floatx4{0.f, 0.f, 0.f, 0.f};
+            kv[u] = ok ? ld16(Kb + (long)key * D) : u32x4_t{0u, 0u, 0u, 0u};
+            vv[u] = ok ? ld16(Vb + (long)key * D) : u32x4_t{0u, 0u, 0u, 0u};
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float d = q.x * kv[u][0] + q.y * kv[u][1] + q.z * kv[u][2] + q.w * kv[u][3];
+            float d = q[0] * elem(kv[u], 0);
+#pragma unroll
+            for (int e = 1; e < EPL; ++e) d += q[e] * elem(kv[u], e);
 #pragma unroll
             for (int o = TPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, WAVE);
             sc[u] = (kk + u * NG) < k1 ? d : -FLT_MAX;
@@ -446,18 +456,22 @@ __global__ void __launch_bounds__(256) attn_decode_kernel(const DecodeArgs p)
         for (int u = 0; u < U; ++u) mx = fmaxf(mx, sc[u]);
         float corr = exp2f(m - mx);
         l *= corr;
-        acc.x *= corr; acc.y *= corr; acc.z *= corr; acc.w *= corr;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] *= corr;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             float pv = sc[u] == -FLT_MAX ? 0.f : exp2f(sc[u] - mx);
             l += pv;
-            acc.x += pv * vv[u][0]; acc.y += pv * vv[u][1]; acc.z += pv * vv[u][2]; acc.w += pv * vv[u][3];
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[e] += pv * elem(vv[u], e);
         }
         m = mx;
     }
     // merge the key groups of this workgroup
     if (lig == 0) { sm[grp] = m; sl[grp] = l; }
-    *(float4 *)(&sacc[grp][4 * lig]) = acc;
+#pragma unroll
+    for (int e = 0; e < EPL; e += 4)
+        *(float4 *)(&sacc[grp][EPL * lig + e]) = make_float4(acc[e], acc[e + 1], acc[e + 2], acc[e + 3]);
     __syncthreads();
     if (tid < D) {
         float M = -FLT_MAX;
@@ -502,9 +516,12 @@ __global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p
 // max_len only adds empty trailing splits (whose zero weights leave the merge bit-identical).
 // 2*B*H keys per split (at least 192): many splits when few (sequence, head) pairs must fill
 // the chip, about three 1K-key splits per pair at the LLaMA-7B batch-16 shape (measured best).
-static int decode_nsplit(int B, int H, int D, int max_len, int *chunk)
+// bf16 caches take twice the keys per step (8 elements per lane), so their chunk is never
+// shorter and their split count never larger than the fp32 one: the fp32 workspace size
+// covers both.
+static int decode_nsplit(int B, int H, int D, int max_len, int *chunk, bool kv_bf16 = false)
 {
-    const int keys_per_step = 4 * (WAVE / (D / 4)) * 4;  // NG * U
+    const int keys_per_step = 4 * (WAVE / (D / (kv_bf16 ? 8 : 4))) * 4;  // NG * U
     int ch = std::max(2 * B * H, 192);
     ch = (ch + keys_per_step - 1) / keys_per_step * keys_per_step;
     *chunk = ch;
@@ -520,7 +537,7 @@ jas_status attn_decode_impl(const float *q, const void *K, const void *V, float 
     JAS_CHECK(D == 32 || D == 64 || D == 128, JAS_ERR_INVALID, "jas_attn_decode: head dim must be 32, 64 or 128");
     JAS_CHECK(k_sb % 4 == 0 && k_sh % 4 == 0, JAS_ERR_INVALID, "jas_attn_decode: strides must be multiples of 4");
     int chunk;
-    int ns = decode_nsplit(B, H, D, max_len, &chunk);
+    int ns = decode_nsplit(B, H, D, max_len, &chunk, kv_bf16);
     JAS_CHECK(ns == 1 || work, JAS_ERR_INVALID, "jas_attn_decode: workspace required");
     JAS_CHECK(o_packed_d <= 0 || (B <= 16 && o_packed_d == H * D), JAS_ERR_INVALID, "attn_decode: bad packed output");
     DecodeArgs p{q, K, V, O, seqlens, (float *)work, k_sb, k_sh, B, H, ns, chunk, scale * 1.4426950408889634f,

@@ -22,6 +22,7 @@
 namespace jas {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c)
 {
@@ -275,7 +276,15 @@ jas_status gemm_general(int M, int N, int K, const void *A, long as0, long as1, 
 // long contiguous runs instead of 16 rows x 64 B scattered 4*K bytes apart.
 //
 // WB (packed only): the weights are bf16 -- the same layout at 2 bytes per element, so one
-// wave-wide load is a contiguous 512-byte block, widened to fp32 in registers.
+// wave-wide load is a contiguous 512-byte block.  They feed v_mfma_f32_16x16x32_bf16
+// directly: the activations are split exactly into three bf16 parts (x = hi + mid + lo,
+// 8 significant bits each, so every bf16 x bf16 product is exact in fp32) and each weight
+// fragment is multiplied by all three, accumulating in fp32.  The K order within a 32-wide
+// step is permuted identically in both operands: slot j of lane group g is k = 16q + 4g + j
+// for j < 4 (block q) and 16(q+1) + 4g + j - 4 for j >= 4 (block q+1) -- exactly what the
+// packed weight and activation layouts put in that lane.  One such MFMA does the work of
+// eight fp32 16x16x4 ones, so halving the weight bytes does not make the kernel
+// matrix-core bound.
 template <int NT, int WPB, int DEPTH, bool DUAL, bool PACKED, bool WB>
 __global__ void __launch_bounds__(WPB * 64)
 skinny_kernel(const void *__restrict__ W, const void *__restrict__ W2, const float *__restrict__ X, long ldx, int M,
@@ -283,6 +292,7 @@ skinny_kernel(const void *__restrict__ W, const void *__restrict__ W2, const flo
 {
     static_assert(!WB || PACKED, "bf16 weights are packed");
     using WT = typename std::conditional<WB, uint16_t, float>::type;
+    using WR = typename std::conditional<WB, u32x2, floatx4>::type;  // one lane's weights of a block
     constexpr int ITEMS = NT * 64;
     __shared__ floatx4 red[WPB][NT][64];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -328,17 +338,17 @@ skinny_kernel(const void *__restrict__ W, const void *__restrict__ W2, const flo
     const int wu = __builtin_amdgcn_readfirstlane(w);
     const int cs = c_begin + wu;
     const int nw = cs < c_full ? (c_full - cs + WPB - 1) / WPB : 0;
-    floatx4 wb[DEPTH][NT][4];
+    WR wb[DEPTH][NT][4];
     float4 xb[DEPTH][4];
-    auto load = [&](int c, floatx4 (&wv)[NT][4], float4 (&xv)[4]) {
+    auto load = [&](int c, WR (&wv)[NT][4], float4 (&xv)[4]) {
         const int k = c * 64;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                if (WB)
-                    wv[t][q] = widen_bf16x4(__builtin_nontemporal_load(
-                        (const u32x2 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG))));
+                if constexpr (WB)
+                    wv[t][q] = __builtin_nontemporal_load(
+                        (const u32x2 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG)));
                 else if (PACKED)
                     wv[t][q] = __builtin_nontemporal_load(
                         (const floatx4 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG)));
@@ -351,16 +361,44 @@ skinny_kernel(const void *__restrict__ W, const void *__restrict__ W2, const flo
                 xv[q] = *(const float4 *)(xp + k + 16 * q);
         }
     };
-    auto compute = [&](const floatx4 (&wv)[NT][4], const float4 (&xv)[4]) {
+    auto compute = [&](const WR (&wv)[NT][4], const float4 (&xv)[4]) {
+        if constexpr (WB) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+            for (int pr = 0; pr < 2; ++pr) {  // blocks 2pr, 2pr+1: one 32-wide MFMA step
+                const float4 a = xv[2 * pr], b = xv[2 * pr + 1];
+                const float x8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                bf16x8 xh, xm, xl;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                acc[t] = mfma4(wv[t][q][0], xv[q].x, acc[t]);
-                acc[t] = mfma4(wv[t][q][1], xv[q].y, acc[t]);
-                acc[t] = mfma4(wv[t][q][2], xv[q].z, acc[t]);
-                acc[t] = mfma4(wv[t][q][3], xv[q].w, acc[t]);
+                for (int j = 0; j < 8; ++j) {
+                    const __bf16 h = (__bf16)x8[j];
+                    const float r1 = x8[j] - (float)h;   // exact
+                    const __bf16 m = (__bf16)r1;
+                    const float r2 = r1 - (float)m;      // exact, at most 8 significant bits
+                    xh[j] = h;
+                    xm[j] = m;
+                    xl[j] = (__bf16)r2;                  // exact
+                }
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const u32x2 w0 = wv[t][2 * pr], w1 = wv[t][2 * pr + 1];
+                    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+                    const bf16x8 wf = __builtin_bit_cast(bf16x8, u32x4_t{w0.x, w0.y, w1.x, w1.y});
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xl, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xm, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xh, acc[t], 0, 0, 0);
+                }
             }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    acc[t] = mfma4(wv[t][q][0], xv[q].x, acc[t]);
+                    acc[t] = mfma4(wv[t][q][1], xv[q].y, acc[t]);
+                    acc[t] = mfma4(wv[t][q][2], xv[q].z, acc[t]);
+                    acc[t] = mfma4(wv[t][q][3], xv[q].w, acc[t]);
+                }
+        }
     };
 #pragma unroll
     for (int j = 0; j < DEPTH - 1; ++j)
@@ -392,9 +430,9 @@ skinny_kernel(const void *__restrict__ W, const void *__restrict__ W2, const flo
             const bool in = PACKED ? (4 * c + q) < K16 : (k + 16 * q + 4 * g) < K;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                if (WB)
-                    wb[0][t][q] = in ? widen_bf16x4(*(const u32x2 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG)))
-                                     : floatx4{0.f, 0.f, 0.f, 0.f};
+                if constexpr (WB)
+                    wb[0][t][q] = in ? *(const u32x2 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG))
+                                     : u32x2{0u, 0u};
                 else if (PACKED)
                     wb[0][t][q] = in ? *(const floatx4 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG))
                                      : floatx4{0.f, 0.f, 0.f, 0.f};
@@ -503,10 +541,21 @@ static void launch_skinny(const void *W, const void *W2, const float *X, long ld
 // weight bytes -- four tiles for the large matrices even though that leaves fewer
 // workgroups than CUs for the QKV projection; small matrices (GPT-2 widths) are
 // latency-bound and keep one tile and 8 waves so that more workgroups are in flight.
-SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split)
+SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split, bool wbf16)
 {
     SkinnyTuning t;
     const int rt = (M + 15) / 16;
+    if (wbf16) {  // bf16 weights (cold-weight sweep): half the bytes per tile, deeper rings
+        if (dual) { t.nt = 2; t.wpb = 4; t.depth = 3; }
+        else if (split && rt >= 256) {
+            if (K >= 8192) { t.nt = 4; t.wpb = 4; t.depth = 4; }
+            else { t.nt = 2; t.wpb = 8; t.depth = 2; }
+        } else if (split) { t.nt = 2; t.wpb = 8; t.depth = 2; }
+        else if (rt >= 1536) { t.nt = 4; t.wpb = 4; t.depth = 2; }
+        else if (rt >= 512) { t.nt = 4; t.wpb = 4; t.depth = 4; }
+        else { t.nt = 1; t.wpb = 8; t.depth = 3; }
+        return t;
+    }
     if (dual) {                      // SwiGLU gate/up: one tile of each
         t.nt = 2; t.wpb = 4; t.depth = 3;
     } else if (split) {              // split-K residual projections
@@ -526,9 +575,9 @@ SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split)
 
 // K splits of a split-K residual projection: enough splits for about 256 workgroups with
 // the split geometry above, at most 8 and at least two 64-wide chunks per split
-int skinny_pick_ksplit(int M, int K)
+int skinny_pick_ksplit(int M, int K, bool wbf16)
 {
-    const int nt = skinny_default_tuning(M, K, false, true).nt;
+    const int nt = skinny_default_tuning(M, K, false, true, wbf16).nt;
     const int wgs = ((M + 15) / 16 + nt - 1) / nt, nchunk = (K + 63) / 64;
     int ks = std::max(1, std::min({(256 + wgs - 1) / wgs, nchunk / 2, 8}));
     const int cpb = (nchunk + ks - 1) / ks;
@@ -549,7 +598,7 @@ jas_status skinny_gemm(const void *W, const void *W2, const float *X, long ldx, 
     if (epi.mode == EPI_QKV)
         JAS_CHECK(epi.d % 16 == 0 && epi.dh % 4 == 0 && M == 3 * epi.d, JAS_ERR_INVALID, "skinny_gemm: bad QKV shape");
     if (dual) JAS_CHECK(W2 != nullptr, JAS_ERR_INVALID, "skinny_gemm: SwiGLU needs both weights");
-    SkinnyTuning tu = tune ? *tune : skinny_default_tuning(M, K, dual, epi.mode == EPI_PARTIAL);
+    SkinnyTuning tu = tune ? *tune : skinny_default_tuning(M, K, dual, epi.mode == EPI_PARTIAL, wbf16);
     if (!tune && !packed && tu.nt == 4) tu.nt = 2;  // four-tile geometry: packed weights only
     const int nt = dual ? 2 : tu.nt;
     SkinnyEpiArgs ep = epi;

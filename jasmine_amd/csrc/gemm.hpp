@@ -43,9 +43,9 @@ struct SkinnyEpiArgs {
 struct SkinnyTuning {
     int nt = 1, wpb = 8, depth = 2;  // depth: chunk buffers in the load pipeline
 };
-SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split = false);
+SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split = false, bool wbf16 = false);
 // K splits (<= 8, all non-empty) for an EPI_PARTIAL launch of an [M][K] weight
-int skinny_pick_ksplit(int M, int K);
+int skinny_pick_ksplit(int M, int K, bool wbf16 = false);
 
 // Packed (MFMA-native) weight layout of an [M][K] matrix, rows padded to RG = ceil(M/16)
 // row tiles, K % 16 == 0.  A 16 x 16 tile (row tile rt, K block kb) is 256 floats: lane

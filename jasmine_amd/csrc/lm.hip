@@ -507,8 +507,8 @@ jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out)
         lm->attn_ws_bytes = std::max(lm->attn_ws_bytes, jas_attn_decode_workspace(b, c.n_head, dh, c.max_ctx));
     if (st == JAS_OK && lm->attn_ws_bytes) st = jas_malloc(&lm->attn_ws, lm->attn_ws_bytes);
     // K splits of the d-row residual projections: enough workgroups to cover the chip
-    lm->ks_o = skinny_pick_ksplit(c.d_model, c.d_model);
-    lm->ks_d = skinny_pick_ksplit(c.d_model, c.d_ff);
+    lm->ks_o = skinny_pick_ksplit(c.d_model, c.d_model, lm->wbf16());
+    lm->ks_d = skinny_pick_ksplit(c.d_model, c.d_ff, lm->wbf16());
     if (st == JAS_OK)
         st = jas_malloc((void **)&lm->part, sizeof(float) * (size_t)std::max(lm->ks_o, lm->ks_d) * 16 * c.d_model);
     if (st != JAS_OK) {
