@@ -61,9 +61,13 @@ struct TileLoader {
                 long rt = o0 / 16 + i;
                 floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
                 if (rt * 16 < O) {
-                    const long off = weight_tile_offset(rt, k0 >> 4, K >> 4, (O + 15) >> 4) + ln * 4;
-                    if (MODE == LM_PKB) v = widen_bf16x4(*(const u32x2 *)((const uint16_t *)(const void *)X + off));
-                    else v = *(const floatx4 *)(X + off);
+                    if (MODE == LM_PKB) {  // half (k0/16)%2 of the pair tile: 4 of the lane's 8 elements
+                        const int kb = k0 >> 4;
+                        const long off = weight_tile_offset_b(rt, kb >> 1, k32_of(K), (O + 15) >> 4) + ln * 8 + 4 * (kb & 1);
+                        v = widen_bf16x4(*(const u32x2 *)((const uint16_t *)(const void *)X + off));
+                    } else {
+                        v = *(const floatx4 *)(X + weight_tile_offset(rt, k0 >> 4, K >> 4, (O + 15) >> 4) + ln * 4);
+                    }
                 }
                 r[4 * q] = v[0]; r[4 * q + 1] = v[1]; r[4 * q + 2] = v[2]; r[4 * q + 3] = v[3];
             }
@@ -292,7 +296,8 @@ skinny_kernel(const void *__restrict__ W, const void *__restrict__ W2, const flo
 {
     static_assert(!WB || PACKED, "bf16 weights are packed");
     using WT = typename std::conditional<WB, uint16_t, float>::type;
-    using WR = typename std::conditional<WB, u32x2, floatx4>::type;  // one lane's weights of a block
+    // one lane's weights of a 16-wide block (fp32) or of a 32-wide pair tile (bf16, slots 0-1)
+    using WR = typename std::conditional<WB, u32x4, floatx4>::type;
     constexpr int ITEMS = NT * 64;
     __shared__ floatx4 red[WPB][NT][64];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -310,7 +315,7 @@ skinny_kernel(const void *__restrict__ W, const void *__restrict__ W2, const flo
             // tiles past the last row tile (M not a multiple of NT*16) re-read the last one;
             // their rows are >= M and the epilogue discards them
             wrt[t] = min((long)(m0 / 16 + (DUAL ? 0 : t)), RG - 1);
-            wp[t] = base + lane * 4;
+            wp[t] = base + lane * (WB ? 8 : 4);
         } else {
             int row = m0 + (DUAL ? 0 : t * 16) + r16;
             row = row < M ? row : M - 1;  // clamped rows are computed and discarded
@@ -340,16 +345,18 @@ skinny_kernel(const void *__restrict__ W, const void *__restrict__ W2, const flo
     const int nw = cs < c_full ? (c_full - cs + WPB - 1) / WPB : 0;
     WR wb[DEPTH][NT][4];
     float4 xb[DEPTH][4];
+    const int K32 = k32_of(K);
     auto load = [&](int c, WR (&wv)[NT][4], float4 (&xv)[4]) {
         const int k = c * 64;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                if constexpr (WB)
-                    wv[t][q] = __builtin_nontemporal_load(
-                        (const u32x2 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG)));
-                else if (PACKED)
+                if constexpr (WB) {
+                    if (q < 2)  // pair tiles 2c, 2c+1
+                        wv[t][q] = __builtin_nontemporal_load(
+                            (const u32x4 *)(wp[t] + weight_tile_offset_b(wrt[t], 2 * c + q, K32, RG)));
+                } else if (PACKED)
                     wv[t][q] = __builtin_nontemporal_load(
                         (const floatx4 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG)));
                 else
@@ -380,9 +387,7 @@ skinny_kernel(const void *__restrict__ W, const void *__restrict__ W2, const flo
                 }
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    const u32x2 w0 = wv[t][2 * pr], w1 = wv[t][2 * pr + 1];
-                    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-                    const bf16x8 wf = __builtin_bit_cast(bf16x8, u32x4_t{w0.x, w0.y, w1.x, w1.y});
+                    const bf16x8 wf = __builtin_bit_cast(bf16x8, wv[t][pr]);
                     acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xl, acc[t], 0, 0, 0);
                     acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xm, acc[t], 0, 0, 0);
                     acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, xh, acc[t], 0, 0, 0);
@@ -430,10 +435,11 @@ skinny_kernel(const void *__restrict__ W, const void *__restrict__ W2, const flo
             const bool in = PACKED ? (4 * c + q) < K16 : (k + 16 * q + 4 * g) < K;
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                if constexpr (WB)
-                    wb[0][t][q] = in ? *(const u32x2 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG))
-                                     : u32x2{0u, 0u};
-                else if (PACKED)
+                if constexpr (WB) {
+                    if (q % 2 == 0)  // a pair tile whose first block is in range (its padding is zero)
+                        wb[0][t][q / 2] = in ? *(const u32x4 *)(wp[t] + weight_tile_offset_b(wrt[t], 2 * c + q / 2, K32, RG))
+                                             : u32x4{0u, 0u, 0u, 0u};
+                } else if (PACKED)
                     wb[0][t][q] = in ? *(const floatx4 *)(wp[t] + weight_tile_offset(wrt[t], 4 * c + q, K16, RG))
                                      : floatx4{0.f, 0.f, 0.f, 0.f};
                 else
@@ -647,19 +653,22 @@ jas_status skinny_gemm(const void *W, const void *W2, const float *X, long ldx, 
 }
 
 // ---------------------------------------------------------------- packed weight layout
+// BF: the bf16 pair-tile layout (weight_pack_offset_b), K padded to a multiple of 32
 template <bool BF>
 __global__ void weight_pack_kernel(const void *__restrict__ src, void *__restrict__ dst, int M, int Mp, int K,
                                    int unpack)
 {
     long p = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (p >= (long)Mp * K) return;
+    if (p >= (long)Mp * (BF ? k32_of(K) : K)) return;
     int r, k;
-    weight_pack_coords(p, K, Mp >> 4, &r, &k);
+    if (BF) weight_pack_coords_b(p, K, Mp >> 4, &r, &k);
+    else weight_pack_coords(p, K, Mp >> 4, &r, &k);
+    const bool real = r < M && k < K;
     if (unpack) {
         const float v = BF ? bf16_to_f32(((const uint16_t *)src)[p]) : ((const float *)src)[p];
-        if (r < M) ((float *)dst)[(long)r * K + k] = v;
+        if (real) ((float *)dst)[(long)r * K + k] = v;
     } else {
-        const float v = r < M ? ((const float *)src)[(long)r * K + k] : 0.0f;
+        const float v = real ? ((const float *)src)[(long)r * K + k] : 0.0f;
         if (BF) ((uint16_t *)dst)[p] = f32_to_bf16(v);
         else ((float *)dst)[p] = v;
     }
@@ -669,11 +678,12 @@ template <bool BF>
 __global__ void fill_normal_packed_kernel(void *x, int M, int Mp, int K, uint64_t key, float mean, float std)
 {
     long stride = (long)gridDim.x * blockDim.x;
-    for (long p = (long)blockIdx.x * blockDim.x + threadIdx.x; p < (long)Mp * K; p += stride) {
+    for (long p = (long)blockIdx.x * blockDim.x + threadIdx.x; p < (long)Mp * (BF ? k32_of(K) : K); p += stride) {
         int r, k;
-        weight_pack_coords(p, K, Mp >> 4, &r, &k);
+        if (BF) weight_pack_coords_b(p, K, Mp >> 4, &r, &k);
+        else weight_pack_coords(p, K, Mp >> 4, &r, &k);
         float v = 0.0f;
-        if (r < M) {
+        if (r < M && k < K) {
             uint64_t i = (uint64_t)r * K + k;  // the row-major element index drives the generator
             uint64_t a = splitmix64(key + 2 * i), b = splitmix64(key + 2 * i + 1);
             double u1 = ((double)(a >> 11) + 1.0) * (1.0 / 9007199254740992.0);
@@ -690,7 +700,7 @@ jas_status weight_pack(const void *src, void *dst, int M, int K, bool unpack, hi
 {
     JAS_CHECK(K % 16 == 0, JAS_ERR_INVALID, "weight_pack: K must be a multiple of 16");
     const int Mp = (M + 15) / 16 * 16;
-    long n = (long)Mp * K;
+    long n = (long)Mp * (bf16 ? k32_of(K) : K);
     if (bf16)
         hipLaunchKernelGGL(weight_pack_kernel<true>, dim3(ceil_div(n, 256)), dim3(256), 0, s, src, dst, M, Mp, K,
                            unpack ? 1 : 0);
@@ -706,7 +716,7 @@ jas_status fill_normal_packed(void *x, int M, int K, uint64_t seed, uint64_t str
 {
     JAS_CHECK(K % 16 == 0, JAS_ERR_INVALID, "fill_normal_packed: K must be a multiple of 16");
     const int Mp = (M + 15) / 16 * 16;
-    unsigned nb = (unsigned)std::min<long>(((long)Mp * K + 255) / 256, 65536);
+    unsigned nb = (unsigned)std::min<long>(((long)Mp * (bf16 ? k32_of(K) : K) + 255) / 256, 65536);
     if (bf16)
         hipLaunchKernelGGL(fill_normal_packed_kernel<true>, dim3(nb), dim3(256), 0, s, x, M, Mp, K,
                            stream_key(seed, stream_id), mean, std);

@@ -80,6 +80,38 @@ __host__ __device__ inline void weight_pack_coords(long p, int K, long RG, int *
 // Packed B-operand (activation) layout of a [16 tokens][K] matrix: element (n, k) at
 //   ((k/16) * 64 + lane) * 4 + k%4,  lane = n + 16 * ((k%16)/4)
 // so one 16-wide K block is the 64 float4 B-operand registers of an MFMA wave in lane order.
+// bf16 packed layout: the same chunk-major order, but the unit is a 16-row x 32-column
+// "pair tile" (two 16-wide K blocks, 512 elements, 1 KB) in which lane
+// l = r%16 + 16*((k%16)/4) holds 8 consecutive elements, slot 4*((k%32)/16) + k%4 -- exactly
+// one lane's operand of a 32-wide v_mfma_f32_16x16x32_bf16 step (with the K order of both
+// operands permuted alike), one 16-byte load.  K is padded to a multiple of 32 with zeros;
+// a 64-column chunk holds two pair tiles of every row tile (the last chunk one, when the
+// padded K is an odd number of pairs).
+__host__ __device__ inline int k32_of(int K) { return (K + 31) / 32 * 32; }
+__host__ __device__ inline long weight_tile_offset_b(long rt, int kp, int K32, long RG)
+{
+    const int c = kp >> 1, qp = kp & 1, npairs = K32 >> 5, np = npairs - 2 * c < 2 ? npairs - 2 * c : 2;
+    return ((long)c * 2 * RG + rt * np + qp) * 512;
+}
+__host__ __device__ inline long weight_pack_offset_b(int r, int k, int K, long RG)
+{
+    const int lane = (r & 15) + 16 * ((k & 15) >> 2), slot = 4 * ((k >> 4) & 1) + (k & 3);
+    return weight_tile_offset_b(r >> 4, k >> 5, k32_of(K), RG) + lane * 8 + slot;
+}
+// inverse over the padded range p < RG*16*K32: (r, k) may be a padding position (k >= K)
+__host__ __device__ inline void weight_pack_coords_b(long p, int K, long RG, int *r, int *k)
+{
+    const long blk = p >> 9;
+    const int within = (int)(p & 511), lane = within >> 3, slot = within & 7;
+    const int npairs = k32_of(K) >> 5;
+    const long c = blk / (2 * RG);
+    const int np = npairs - 2 * (int)c < 2 ? npairs - 2 * (int)c : 2;
+    const long in = blk - c * 2 * RG, rt = in / np;
+    const int qp = (int)(in - rt * np);
+    *r = (int)(rt * 16 + (lane & 15));
+    *k = ((int)c * 2 + qp) * 32 + 16 * (slot >> 2) + 4 * (lane >> 4) + (slot & 3);
+}
+
 __host__ __device__ inline long packed_b_offset(int n, int k)
 {
     return ((long)(k >> 4) * 64 + n + 16 * ((k & 15) >> 2)) * 4 + (k & 3);

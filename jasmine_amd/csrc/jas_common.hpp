@@ -63,6 +63,7 @@ __host__ __device__ inline float bf16_to_f32(uint16_t v)
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // four consecutive bf16 elements (one 8-byte load) widened to fp32
 __device__ __forceinline__ floatx4 widen_bf16x4(u32x2 u)
 {

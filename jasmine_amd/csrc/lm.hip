@@ -25,15 +25,16 @@ namespace jas {
 
 // A stacked weight tensor: `layers` matrices of [rows][cols]; packed matrices use the
 // MFMA-native layout of weight_pack_offset with rows padded to a multiple of 16.
-// bf16 (packed only): 2-byte elements; offsets and strides stay in float (4-byte) units of
-// the arena, so a bf16 layer occupies half as many of them (cols % 16 == 0: even counts).
+// bf16 (packed only): 2-byte elements in the pair-tile layout; offsets and strides stay in
+// float (4-byte) units of the arena, so a bf16 layer occupies half as many of them.
 struct Tensor {
     size_t off = 0, count = 0;
     int layers = 1, rows = 1, cols = 1;
     bool packed = false, bf16 = false;
     long lstride() const
     {
-        const long elems = (long)(packed ? (rows + 15) / 16 * 16 : rows) * cols;
+        // bf16 packed layers use the pair-tile layout: K padded to a multiple of 32
+        const long elems = (long)(packed ? (rows + 15) / 16 * 16 : rows) * (bf16 ? k32_of(cols) : cols);
         return bf16 ? elems / 2 : elems;
     }
 };
@@ -97,7 +98,7 @@ __global__ void embed_packed_kernel(const void *__restrict__ wte, const float *_
     long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (g >= (long)n * d) return;
     int t = (int)(g / d), e = (int)(g % d);
-    const long off = weight_pack_offset(ids[t], e, d, (V + 15) >> 4);
+    const long off = WB ? weight_pack_offset_b(ids[t], e, d, (V + 15) >> 4) : weight_pack_offset(ids[t], e, d, (V + 15) >> 4);
     float v = WB ? bf16_to_f32(((const uint16_t *)wte)[off]) : ((const float *)wte)[off];
     if (wpe) v = v + wpe[(long)pos[t] * d + e];
     out[g] = v;
