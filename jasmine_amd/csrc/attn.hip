@@ -408,15 +408,17 @@ __device__ __forceinline__ long decode_out_index(const DecodeArgs &p, int bh, in
 
 // TPK lanes per key (D/4 floats each); each group of TPK lanes walks its own keys.
 // KB: the cache holds bf16 keys/values (8-byte loads, widened to fp32).
-template <int D, bool KB>
-__global__ void __launch_bounds__(256) attn_decode_kernel(const DecodeArgs p)
+// WPB waves per workgroup: 4 with key splits; 16 when few (sequence, head) pairs let one
+// workgroup take a whole context (no split, no merge launch).
+template <int D, bool KB, int WPB>
+__global__ void __launch_bounds__(WPB * 64) attn_decode_kernel(const DecodeArgs p)
 {
     using KT = typename std::conditional<KB, uint16_t, float>::type;
     constexpr int EPL = KB ? 8 : 4;         // elements per lane and key: one 16-byte load
     constexpr int TPK = D / EPL;            // lanes per key
     constexpr int GPW = WAVE / TPK;         // key groups per wave
-    constexpr int NG = 4 * GPW;             // key groups per workgroup
-    constexpr int U = 4;                    // keys per group per iteration (loads in flight)
+    constexpr int NG = WPB * GPW;           // key groups per workgroup
+    constexpr int U = WPB > 4 ? 8 : 4;      // keys per group per iteration (loads in flight)
     __shared__ float sm[NG], sl[NG];
     __shared__ float sacc[NG][D];
 
@@ -531,8 +533,24 @@ __global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p
 // bf16 caches take twice the keys per step (8 elements per lane), so their chunk is never
 // shorter and their split count never larger than the fp32 one: the fp32 workspace size
 // covers both.
-static int decode_nsplit(int B, int H, int D, int max_len, int *chunk, bool kv_bf16 = false)
+// "wide" form: one 16-wave workgroup per (sequence, head) over the whole context -- no split
+// and no merge launch.  It needs few pairs (all of them resident at once) and wins when the
+// contexts are short: the decoder runner of a GPT-2 size model (about 500 keys per head at
+// 8 x 12 pairs: 0.544 against 0.588 ms per step), but not a full 1024-key cache at the same
+// count (18 against 15 us: only 96 CUs stream).  The runner asks for it; jas_attn_decode
+// keeps the split form.
+constexpr int DECODE_WIDE_PAIRS = 128;
+static bool decode_wide_ok(int B, int H, int D, int max_len, bool kv_bf16)
 {
+    return B * H <= DECODE_WIDE_PAIRS && max_len <= 4096 && D >= 64 && !kv_bf16;
+}
+
+static int decode_nsplit(int B, int H, int D, int max_len, int *chunk, bool kv_bf16 = false, bool wide = false)
+{
+    if (wide && decode_wide_ok(B, H, D, max_len, kv_bf16)) {
+        *chunk = max_len;
+        return 1;
+    }
     const int keys_per_step = 4 * (WAVE / (D / (kv_bf16 ? 8 : 4))) * 4;  // NG * U
     int ch = std::max(2 * B * H, 192);
     ch = (ch + keys_per_step - 1) / keys_per_step * keys_per_step;
@@ -540,16 +558,24 @@ static int decode_nsplit(int B, int H, int D, int max_len, int *chunk, bool kv_b
     return std::max(1, (max_len + ch - 1) / ch);
 }
 
+// the wide form exists for fp32 caches and D >= 64 only (decode_wide_ok)
+template <int D>
+static void launch_decode_wide(dim3 grid, hipStream_t s, const DecodeArgs &p)
+{
+    if constexpr (D >= 64) hipLaunchKernelGGL((attn_decode_kernel<D, false, 16>), grid, dim3(1024), 0, s, p);
+}
+
 jas_status attn_decode_impl(const float *q, const void *K, const void *V, float *O, const int32_t *seqlens, int B,
                             int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, hipStream_t s,
-                            int o_packed_d, bool kv_bf16)
+                            int o_packed_d, bool kv_bf16, bool wide)
 {
     JAS_CHECK(q && K && V && O && seqlens, JAS_ERR_INVALID, "jas_attn_decode: null tensor");
     JAS_CHECK(B > 0 && H > 0 && max_len > 0, JAS_ERR_INVALID, "jas_attn_decode: empty shape");
     JAS_CHECK(D == 32 || D == 64 || D == 128, JAS_ERR_INVALID, "jas_attn_decode: head dim must be 32, 64 or 128");
     JAS_CHECK(k_sb % 4 == 0 && k_sh % 4 == 0, JAS_ERR_INVALID, "jas_attn_decode: strides must be multiples of 4");
     int chunk;
-    int ns = decode_nsplit(B, H, D, max_len, &chunk, kv_bf16);
+    const bool use_wide = wide && decode_wide_ok(B, H, D, max_len, kv_bf16);
+    int ns = decode_nsplit(B, H, D, max_len, &chunk, kv_bf16, use_wide);
     JAS_CHECK(ns == 1 || work, JAS_ERR_INVALID, "jas_attn_decode: workspace required");
     JAS_CHECK(o_packed_d <= 0 || (B <= 16 && o_packed_d == H * D), JAS_ERR_INVALID, "attn_decode: bad packed output");
     DecodeArgs p{q, K, V, O, seqlens, (float *)work, k_sb, k_sh, B, H, ns, chunk, scale * 1.4426950408889634f,
@@ -557,8 +583,9 @@ jas_status attn_decode_impl(const float *q, const void *K, const void *V, float 
     dim3 grid(ns, B * H);
 #define JAS_DEC(DD)                                                                                  \
     if (D == DD) {                                                                                   \
-        if (kv_bf16) hipLaunchKernelGGL((attn_decode_kernel<DD, true>), grid, dim3(256), 0, s, p);     \
-        else hipLaunchKernelGGL((attn_decode_kernel<DD, false>), grid, dim3(256), 0, s, p);          \
+        if (use_wide) launch_decode_wide<DD>(grid, s, p);                                              \
+        else if (kv_bf16) hipLaunchKernelGGL((attn_decode_kernel<DD, true, 4>), grid, dim3(256), 0, s, p); \
+        else hipLaunchKernelGGL((attn_decode_kernel<DD, false, 4>), grid, dim3(256), 0, s, p);       \
         if (ns > 1) hipLaunchKernelGGL((attn_decode_merge_kernel<DD>), dim3(B * H), dim3(DD), 0, s, p); \
     }
     JAS_DEC(32) JAS_DEC(64) JAS_DEC(128)

@@ -23,7 +23,7 @@ jas_status resid_norm(float *x, const float *part, int ks, const float *bias, co
 // kv_bf16: K/V hold bf16 elements (same element strides)
 jas_status attn_decode_impl(const float *q, const void *K, const void *V, float *O, const int32_t *seqlens, int B,
                             int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, hipStream_t s,
-                            int o_packed_d, bool kv_bf16 = false);
+                            int o_packed_d, bool kv_bf16 = false, bool wide = false);
 
 // two-pass row argmax with caller-provided scratch of argmax_workspace_bytes(n, V) bytes
 size_t argmax_workspace_bytes(int n, int V);

@@ -349,7 +349,7 @@ jas_status decode_step(jas_lm *lm, bool device_pos)
         TRY(prof_begin(lm, 1));
         TRY(attn_decode_impl(lm->q, lm->kv_layer_ptr(lm->kc, l), lm->kv_layer_ptr(lm->vc, l), lm->att, lm->seqlens, B, H,
                              dh, c.max_ctx, lm->kv_sb, lm->kv_sh, 1.0f / sqrtf((float)dh), lm->attn_ws, s, d,
-                             c.kv_bf16 != 0));
+                             c.kv_bf16 != 0, /*wide*/ true));
         TRY(prof_end(lm));
         SkinnyEpiArgs eo;
         eo.mode = EPI_PARTIAL;
