@@ -557,7 +557,8 @@ SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split, bool wbf
             if (K >= 8192) { t.nt = 4; t.wpb = 4; t.depth = 4; }
             else { t.nt = 2; t.wpb = 8; t.depth = 2; }
         } else if (split) { t.nt = 2; t.wpb = 8; t.depth = 2; }
-        else if (rt >= 1536) { t.nt = 4; t.wpb = 4; t.depth = 2; }
+        else if (rt >= 1536 && K >= 2048) { t.nt = 4; t.wpb = 4; t.depth = 2; }
+        else if (rt >= 1536) { t.nt = 4; t.wpb = 4; t.depth = 3; }
         else if (rt >= 512) { t.nt = 4; t.wpb = 4; t.depth = 4; }
         else { t.nt = 1; t.wpb = 8; t.depth = 3; }
         return t;
@@ -569,8 +570,9 @@ SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split, bool wbf
         // the split partials then reads twice as much)
         if (rt >= 256) { t.nt = 2; t.wpb = 4; t.depth = K >= 8192 ? 2 : 3; }
         else { t.nt = 2; t.wpb = 8; t.depth = 2; }
-    } else if (rt >= 1536) {         // LM head
-        t.nt = 4; t.wpb = 4; t.depth = 3;
+    } else if (rt >= 1536) {         // LM head (short K: more waves share each row tile's chunks)
+        if (K >= 2048) { t.nt = 4; t.wpb = 4; t.depth = 3; }
+        else { t.nt = 2; t.wpb = 8; t.depth = 2; }
     } else if (rt >= 512) {          // QKV at LLaMA-7B width
         t.nt = 4; t.wpb = 4; t.depth = 2;
     } else {
