@@ -358,6 +358,8 @@ def main():
     ap.add_argument("--no-gpt2", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-bf16", action="store_true", help="skip the bf16-storage LLaMA leg")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="only the config 2/3 kernel lines (one JSON object; for profilers)")
     ap.add_argument("--no-kernels", action="store_true", help="skip the config 2/3 kernel lines")
     ap.add_argument("--no-graph", action="store_true",
                     help="decode with eager launches instead of graph replay (same kernels; for profilers)")
@@ -372,6 +374,11 @@ def main():
         return
     if args.traffic_kernels:
         traffic_kernels(args)
+        return
+    if args.kernels_only:
+        import jasmine_amd as jas
+        jas.check(jas.lib.jas_init(0))
+        print(json.dumps({"kernels": run_kernel_legs(jas)}), flush=True)
         return
     if args.summarize_pmc:
         out = summarize_pmc(*args.summarize_pmc, args)
