@@ -99,6 +99,19 @@ def test_bf16_storage(jas, kind, wb, kb):
     run_parity(jas, cfg, seed=12, B=4, P=11, steps=6, prompt_seed=12)
 
 
+@pytest.mark.parametrize("kind,bf16", [(1, 0), (0, 0), (1, 1)])
+def test_full_batch_16(jas, kind, bf16):
+    """max_batch 16 -- the headline's batch -- fills all 16 token columns of the packed
+    activation operand and of every MFMA tile.  The LLaMA kind (head dim 128, 16 x 16 = 256
+    (sequence, head) pairs) takes the split-K attention with its merge; the GPT-2 kind
+    (16 x 4 = 64 pairs) the unsplit 16-wave form."""
+    if kind == 1:
+        cfg = jas.LmConfig(1, 2, 2048, 16, 512, 300, 40, 16, 1e-6, 10000.0, bf16, bf16)
+    else:
+        cfg = jas.LmConfig(0, 2, 256, 4, 512, 300, 40, 16, 1e-5, 10000.0, bf16, bf16)
+    run_parity(jas, cfg, seed=21, B=16, P=9, steps=4, prompt_seed=21)
+
+
 def test_bf16_weight_roundtrip(jas):
     # set_weight rounds to bf16 (nearest even) and get_weight widens exactly; fp32 tensors
     # (norm gains, biases, positions) are untouched
