@@ -544,9 +544,9 @@ static void launch_skinny(const void *W, const void *W2, const float *X, long ld
 
 // Geometry per decode shape, from a cold-weight sweep on MI355X (16 tokens, packed weights).
 // More row tiles per workgroup amortise each activation chunk (read from L2) over more
-// weight bytes -- four tiles for the large matrices even though that leaves fewer
-// workgroups than CUs for the QKV projection; small matrices (GPT-2 widths) are
-// latency-bound and keep one tile and 8 waves so that more workgroups are in flight.
+// weight bytes, best when the workgroup count lands on the 256 CUs (the QKV projection:
+// three tiles); small matrices (GPT-2 widths) are latency-bound and keep one tile and
+// 8 waves so that more workgroups are in flight.
 SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split, bool wbf16)
 {
     SkinnyTuning t;
@@ -559,7 +559,7 @@ SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split, bool wbf
         } else if (split) { t.nt = 2; t.wpb = 8; t.depth = 2; }
         else if (rt >= 1536 && K >= 2048) { t.nt = 4; t.wpb = 4; t.depth = 2; }
         else if (rt >= 1536) { t.nt = 4; t.wpb = 4; t.depth = 3; }
-        else if (rt >= 512) { t.nt = 4; t.wpb = 4; t.depth = 4; }
+        else if (rt >= 512) { t.nt = 3; t.wpb = 4; t.depth = 4; }
         else { t.nt = 1; t.wpb = 8; t.depth = 3; }
         return t;
     }
@@ -573,8 +573,8 @@ SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split, bool wbf
     } else if (rt >= 1536) {         // LM head (short K: more waves share each row tile's chunks)
         if (K >= 2048) { t.nt = 4; t.wpb = 4; t.depth = 3; }
         else { t.nt = 2; t.wpb = 8; t.depth = 2; }
-    } else if (rt >= 512) {          // QKV at LLaMA-7B width
-        t.nt = 4; t.wpb = 4; t.depth = 2;
+    } else if (rt >= 512) {          // QKV at LLaMA-7B width: 768 row tiles, 3 per workgroup
+        t.nt = 3; t.wpb = 4; t.depth = 2;  // = 256 workgroups, one per CU (4 tiles: 192, 15 % slower)
     } else {
         t.nt = 1; t.wpb = 8; t.depth = 3;
     }
@@ -607,7 +607,7 @@ jas_status skinny_gemm(const void *W, const void *W2, const float *X, long ldx, 
         JAS_CHECK(epi.d % 16 == 0 && epi.dh % 4 == 0 && M == 3 * epi.d, JAS_ERR_INVALID, "skinny_gemm: bad QKV shape");
     if (dual) JAS_CHECK(W2 != nullptr, JAS_ERR_INVALID, "skinny_gemm: SwiGLU needs both weights");
     SkinnyTuning tu = tune ? *tune : skinny_default_tuning(M, K, dual, epi.mode == EPI_PARTIAL, wbf16);
-    if (!tune && !packed && tu.nt == 4) tu.nt = 2;  // four-tile geometry: packed weights only
+    if (!tune && !packed && tu.nt > 2) tu.nt = 2;  // three and four tiles: packed weights only
     const int nt = dual ? 2 : tu.nt;
     SkinnyEpiArgs ep = epi;
     const int nchunk = (K + 63) / 64;
@@ -638,6 +638,7 @@ jas_status skinny_gemm(const void *W, const void *W2, const float *X, long ldx, 
         JAS_SKB(2, 4, true, 3) JAS_SKB(2, 4, true, 4) JAS_SKB(2, 4, false, 2) JAS_SKB(2, 4, false, 3)
         JAS_SKB(2, 4, false, 4) JAS_SKB(2, 8, false, 2) JAS_SKB(2, 8, false, 3) JAS_SKB(4, 4, false, 2)
         JAS_SKB(4, 4, false, 3) JAS_SKB(4, 4, false, 4) JAS_SKB(1, 8, false, 3) JAS_SKB(1, 8, false, 4)
+        JAS_SKB(3, 4, false, 3) JAS_SKB(3, 4, false, 4)
 #undef JAS_SKB
         return fail(JAS_ERR_INVALID, "skinny_gemm: unsupported tuning for bf16 weights");
     }
@@ -648,6 +649,7 @@ jas_status skinny_gemm(const void *W, const void *W2, const float *X, long ldx, 
     JAS_SK(1, 16, false, false, 3)
     // four row tiles per workgroup share each activation chunk (packed weights only)
     JAS_SK(4, 4, false, true, 2) JAS_SK(4, 4, false, true, 3) JAS_SK(4, 8, false, true, 2)
+    JAS_SK(3, 4, false, true, 2) JAS_SK(3, 4, false, true, 3) JAS_SK(3, 8, false, true, 2)
 #undef JAS_SK_P
 #undef JAS_SK_D
 #undef JAS_SK
