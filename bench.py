@@ -459,6 +459,28 @@ def main():
             "avg_launch_us": 1e3 * dom["gpu_ms"] / max(dom["launches"], 1)}
     step_roofline_frac = (step_bytes_timed / (dt / args.steps)) / 1e9 / HBM_PEAK_GBS
 
+    # batch-1 decode on the same model (BASELINE's second config-5 row): re-prefill one sequence
+    b1 = None
+    try:
+        lm.prefill(prompt[:1])
+        lm.generate(args.warmup, 1)
+        b1_pos0 = lm.position
+        jas.check(jas.lib.jas_synchronize(lm.stream))
+        t0 = time.perf_counter()
+        lm.generate(args.steps, 1)
+        b1_dt = time.perf_counter() - t0
+        b1_bytes = weight_bytes_per_step(L, d, F, V) + sum(
+            L * H * (b1_pos0 + st + 1) * dh * 4 * 2 for st in range(args.steps)) / args.steps
+        b1_frac = b1_bytes / (b1_dt / args.steps) / 1e9 / HBM_PEAK_GBS
+        b1 = {"decode_tok_s": round(args.steps / b1_dt, 2), "ms_per_step": round(1e3 * b1_dt / args.steps, 3),
+              "step_bytes": b1_bytes, "step_hbm_frac": round(b1_frac, 4),
+              "workload": f"config5 shape fp32, batch 1, {P}-token prompt, timed positions "
+                          f"{b1_pos0}..{b1_pos0 + args.steps - 1}"}
+        log(f"[bench] llama batch 1: {args.steps / b1_dt:.1f} tok/s, {1e3 * b1_dt / args.steps:.3f} ms/step, "
+            f"{100 * b1_frac:.1f}% of HBM peak")
+    except Exception as e:  # the headline number stands on its own
+        log("[bench] batch-1 leg failed:", e)
+
     step_flops = 2.0 * B * (L * (3 * d * d + d * d + 3 * d * F) + V * d) + 4.0 * B * L * H * (P + 64) * dh
     cpu = None if args.no_cpu else cpu_baseline(step_flops, B)
 
@@ -526,6 +548,7 @@ def main():
                          "frac": round(prefill_flops / prefill_s / 1e12 / 157.3, 4),
                          "flops": prefill_flops, "note": "fp32 MFMA peak; wall time of the whole prefill"},
         "cpu_baseline": cpu,
+        "llama7b_batch1": b1,
         "llama7b_bf16_storage": llama_bf16,
         "gpt2_small": gpt2,
         "tiny_gpt2": tiny,

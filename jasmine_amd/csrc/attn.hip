@@ -542,7 +542,9 @@ __global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p
 constexpr int DECODE_WIDE_PAIRS = 128;
 static bool decode_wide_ok(int B, int H, int D, int max_len, bool kv_bf16)
 {
-    return B * H <= DECODE_WIDE_PAIRS && max_len <= 4096 && D >= 64 && !kv_bf16;
+    // a cache of more than 1024 keys per pair keeps the split: one workgroup per pair would
+    // stream it from a handful of CUs (LLaMA-7B at batch 1: 32 pairs x 2300 keys)
+    return B * H <= DECODE_WIDE_PAIRS && max_len <= 1024 && D >= 64 && !kv_bf16;
 }
 
 static int decode_nsplit(int B, int H, int D, int max_len, int *chunk, bool kv_bf16 = false, bool wide = false)
