@@ -61,9 +61,9 @@ struct PrefillArgs {
     int causal;
 };
 
-// waves per workgroup (16 queries each): 8 for both types (measured with the heaviest-first
-// work order: 4 or 16 waves are slower for bf16, and 8 beats 4 for fp32, by 17 % at D = 128)
-template <bool BF16> struct FaWaves { static constexpr int value = BF16 ? 8 : 8; };
+// waves per workgroup (16 queries each), measured with the heaviest-first work order: 4 or
+// 16 waves are slower for bf16, and 8 beats 4 for fp32 (by 17 % at D = 128)
+constexpr int FA_WAVES = 8;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
@@ -98,9 +98,9 @@ __device__ __forceinline__ bool fa_work_item(int nqb, int BH, int &bh, int &qb)
 // second product); the reduction index of each product is permuted identically in both
 // operands so that S lands in the P operand's registers with no shuffle.
 template <int D, bool BF16, int BK>
-__global__ void __launch_bounds__(64 * FaWaves<BF16>::value) flash_prefill_kernel(const PrefillArgs p)
+__global__ void __launch_bounds__(64 * FA_WAVES) flash_prefill_kernel(const PrefillArgs p)
 {
-    constexpr int FA_NW = FaWaves<BF16>::value, FA_BQ = 16 * FA_NW;
+    constexpr int FA_NW = FA_WAVES, FA_BQ = 16 * FA_NW;
     constexpr int NT = 64 * FA_NW;
     using T = typename std::conditional<BF16, uint16_t, float>::type;
     constexpr int EPC = 16 / (int)sizeof(T);    // elements per 16-byte chunk
@@ -626,11 +626,11 @@ jas_status jas_attn_prefill(const void *Q, const void *K, const void *V, void *O
 #define JAS_FA(DD)                                                                                     \
     if (D == DD) {                                                                                     \
         if (dtype == JAS_BF16) {                                                                       \
-            constexpr int nw = FaWaves<true>::value;                                                  \
+            constexpr int nw = FA_WAVES;                                                               \
             const int total = ceil_div(Sq, 16 * nw) * B * H;                                           \
             hipLaunchKernelGGL((flash_prefill_kernel<DD, true, 64>), dim3((total + 7) / 8 * 8), dim3(64 * nw), 0, s, p); \
         } else {                                                                                       \
-            constexpr int nw = FaWaves<false>::value;                                                 \
+            constexpr int nw = FA_WAVES;                                                               \
             const int total = ceil_div(Sq, 16 * nw) * B * H;                                           \
             hipLaunchKernelGGL((flash_prefill_kernel<DD, false, 64>), dim3((total + 7) / 8 * 8), dim3(64 * nw), 0, s, p); \
         }                                                                                              \
