@@ -334,6 +334,37 @@ def test_attn_prefill_bf16(jas, B, H, Sq, Sk, D, causal):
     close(unbf(do.numpy()), want, atol=2e-2, rtol=2e-2)
 
 
+@pytest.mark.parametrize("B,H,Sq,Sk,D,dt", [(1, 2, 600, 600, 64, 0), (2, 3, 513, 700, 128, 0), (1, 2, 1030, 1030, 32, 0),
+                                            (1, 2, 520, 520, 128, 3), (2, 1, 777, 800, 64, 3)])
+def test_attn_prefill_long_causal(jas, B, H, Sq, Sk, D, dt):
+    """Causal launches of four or more 128-query blocks (the heaviest-first work order over
+    blocks of unequal cost), with Sk > Sq in two cases.  Two launches in a row with different
+    inputs."""
+    sc = 1 / math.sqrt(D)
+
+    def bf(x):
+        u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    def unbf(u):
+        return (u.astype(np.uint32) << 16).view(np.float32)
+
+    for rep in range(2):
+        Q, K, V = (normal(sh, 33 + rep, i) for i, sh in enumerate(((B, H, Sq, D), (B, H, Sk, D), (B, H, Sk, D))))
+        if dt:
+            Q, K, V = (unbf(bf(x)) for x in (Q, K, V))
+        want = np.zeros((B, H, Sq, D), np.float32)
+        orc.orc_attention(fp(Q), fp(K), fp(V), fp(want), B, H, Sq, Sk, D, sc, 1)
+        dq, dk, dv = (jas.to_device(bf(x) if dt else x) for x in (Q, K, V))
+        do = jas.DeviceArray((B, H, Sq, D), np.uint16 if dt else np.float32)
+        jas.check(jas.lib.jas_attn_prefill(dq.p, dk.p, dv.p, do.p, B, H, Sq, Sk, D, H * Sq * D, Sq * D, D, H * Sk * D,
+                                           Sk * D, D, H * Sq * D, Sq * D, D, sc, 1, dt, None))
+        if dt:
+            close(unbf(do.numpy()), want, atol=2e-2, rtol=2e-2)
+        else:
+            close(do.numpy(), want, atol=1e-5, rtol=1e-4)
+
+
 @pytest.mark.parametrize("B,H,D,lens", [(2, 3, 64, (1, 37)), (3, 2, 128, (1000, 513, 64)), (1, 4, 32, (2049,)),
                                         (8, 12, 64, (1024,) * 8)])
 def test_attn_decode(jas, B, H, D, lens):
