@@ -288,6 +288,24 @@ jas_stream_t jas_lm_stream(jas_lm *lm);
  * 2 other. enable=0 turns event recording off. */
 jas_status jas_lm_profile(jas_lm *lm, int enable, double *ms_by_class, long *launches_by_class);
 
+/* Weight files (safetensors container: 8-byte little-endian header length, JSON header,
+ * raw little-endian data).  The reference has no weight file format; its nets take weights
+ * only through the init_weight<I>() traversal (mat_init_t.hpp:113-118, mat_net_t.hpp:51-56).
+ * Tensors carry the jas_lm_set_weight names, shape [layers, rows, cols] (2-D [rows, cols] is
+ * read as one layer) and logical row-major data, F32 or BF16; "__metadata__" holds the
+ * config as strings (format = "jasmine_amd.lm").
+ * save:  writes every weight (BF16 where the model stores bf16, else F32), atomically
+ *        (a temporary file renamed over path).
+ * load:  the file must hold exactly this model's tensors with their shapes ("wpe" may have
+ *        more positions than max_ctx: its prefix is used); F32 data rounds to bf16 where
+ *        the model stores bf16, BF16 data widens exactly to fp32.  The file streams through
+ *        pinned staging buffers and is packed on the device; on error the model's weights
+ *        are partly overwritten.
+ * read_config: the config saved in the file's metadata (host only, no device call). */
+jas_status jas_lm_save(jas_lm *lm, const char *path);
+jas_status jas_lm_load(jas_lm *lm, const char *path);
+jas_status jas_lm_read_config(const char *path, jas_lm_config *cfg);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,6 +6,6 @@ mat_net_t / mat_mha_t / mat_transformer_t API.  This module is a thin ctypes bin
 the C ABI used by the tests and bench.py.  There is no CPU fallback: importing the
 binding without the built library raises.
 """
-from .capi import lib, LIB_PATH, JasError, check, DeviceArray, to_device, LmConfig, Lm, leaf  # noqa: F401
+from .capi import lib, LIB_PATH, JasError, check, DeviceArray, to_device, LmConfig, Lm, leaf, read_lm_config  # noqa: F401
 
-__all__ = ["lib", "LIB_PATH", "JasError", "check", "DeviceArray", "to_device", "LmConfig", "Lm", "leaf"]
+__all__ = ["lib", "LIB_PATH", "JasError", "check", "DeviceArray", "to_device", "LmConfig", "Lm", "leaf", "read_lm_config"]

@@ -81,6 +81,8 @@ _sigs = {
     "jas_lm_generate": [VP, I, IP],
     "jas_lm_profile": [VP, I, C.POINTER(C.c_double), C.POINTER(C.c_long)],
     "jas_lm_use_graph": [VP, I],
+    "jas_lm_save": [VP, C.c_char_p], "jas_lm_load": [VP, C.c_char_p],
+    "jas_lm_read_config": [C.c_char_p, C.POINTER(LmConfig)],
 }
 for _n, _a in _sigs.items():
     getattr(lib, _n).argtypes = _a
@@ -201,6 +203,14 @@ class Lm:
         assert l and a.size == l * r * c, (name, a.size, (l, r, c))
         check(lib.jas_lm_set_weight(self.h, name.encode(), a.ctypes.data_as(FP), a.size))
 
+    def save(self, path):
+        """Write every weight to a safetensors file (jas_lm_save)."""
+        check(lib.jas_lm_save(self.h, os.fsencode(path)))
+
+    def load(self, path):
+        """Read every weight from a safetensors file (jas_lm_load)."""
+        check(lib.jas_lm_load(self.h, os.fsencode(path)))
+
     @property
     def stream(self):
         return VP(lib.jas_lm_stream(self.h))
@@ -240,3 +250,10 @@ class Lm:
         cnt = (C.c_long * 3)()
         check(lib.jas_lm_profile(self.h, int(enable), ms, cnt))
         return list(ms), list(cnt)
+
+
+def read_lm_config(path):
+    """The runner config stored in a weight file's metadata (host only)."""
+    cfg = LmConfig()
+    check(lib.jas_lm_read_config(os.fsencode(path), C.byref(cfg)))
+    return cfg

@@ -216,7 +216,6 @@ __global__ void __launch_bounds__(64 * FA_WAVES) flash_prefill_kernel(const Pref
         bf16x8 kfr[BF16 ? NJ : 1][BF16 ? D / 32 : 1];
         bf16x8 vfr[BF16 ? NC : 1][BF16 ? NJ / 2 : 1];
         if constexpr (BF16) {
-            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
 #pragma unroll
