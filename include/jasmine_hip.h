@@ -49,6 +49,15 @@ const char *jas_version(void);
 jas_stream_t jas_default_stream(void);
 jas_status jas_malloc(void **d_ptr, size_t bytes);          /* mat_t.hpp:67 new[] */
 jas_status jas_free(void *d_ptr);                            /* mat_t.hpp:39 delete[] */
+/* Stream-ordered block cache behind the C++ headers' mat_t storage (jasmine allocates and
+ * frees per matrix, mat_t.hpp:67 / :39; a device free would synchronise the GPU each time).
+ * A released block is reused by the next allocation of its rounded size at once, so the
+ * memory may only be used by work on the library stream (NULL stream), as the headers do.
+ * jas_pool_trim synchronises that stream and returns every cached block to the device
+ * (cached_before may be NULL). */
+jas_status jas_pool_alloc(void **d_ptr, size_t bytes);
+jas_status jas_pool_free(void *d_ptr);
+jas_status jas_pool_trim(size_t *cached_before);
 jas_status jas_memset(void *d_ptr, int value, size_t bytes, jas_stream_t stream); /* mat_t.hpp:68 memset */
 jas_status jas_memcpy_h2d(void *d_dst, const void *src, size_t bytes, jas_stream_t stream);
 jas_status jas_memcpy_d2h(void *dst, const void *d_src, size_t bytes, jas_stream_t stream);

@@ -51,6 +51,7 @@ _sigs = {
     "jas_memset": [VP, I, C.c_size_t, VP], "jas_memcpy_h2d": [VP, VP, C.c_size_t, VP],
     "jas_memcpy_d2h": [VP, VP, C.c_size_t, VP], "jas_memcpy_d2d": [VP, VP, C.c_size_t, VP],
     "jas_synchronize": [VP],
+    "jas_pool_alloc": [C.POINTER(VP), C.c_size_t], "jas_pool_free": [VP], "jas_pool_trim": [C.POINTER(C.c_size_t)],
     "jas_ew_eval": [C.POINTER(Ins), I, C.POINTER(Leaf), I, VP, C.c_int32, I, I, VP],
     "jas_reduce": [C.POINTER(Leaf), I, I, VP, C.c_int32, VP],
     "jas_softmax": [VP, VP, I, I, L, L, L, VP],

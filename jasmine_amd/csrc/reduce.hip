@@ -141,38 +141,70 @@ rowop_loop_kernel(const float *__restrict__ x, float *__restrict__ y, int len, l
     }
 }
 
-// column form: one thread per vector, sequential over the elements (coalesced when the
-// vectors are adjacent columns of a row-major matrix, vstride == 1)
-template <int MODE>
-__global__ void __launch_bounds__(256)
-rowop_col_kernel(const float *__restrict__ x, float *__restrict__ y, int n_vec, int len, long vstride, long ystride, long estride,
-                 float eps, const float *__restrict__ g, const float *__restrict__ bta)
+// column form: a workgroup takes 64 adjacent vectors (one per lane: coalesced when they
+// are adjacent columns of a row-major matrix, vstride == 1); its W waves split the elements
+// into W contiguous ranges, each lane accumulating its range in order, and the W partials
+// are combined in wave order through LDS (deterministic for a given shape).
+template <int MODE, int W>
+__global__ void __launch_bounds__(64 * W)
+rowop_col_kernel(const float *__restrict__ x, float *__restrict__ y, int n_vec, int len, long vstride, long ystride,
+                 long estride, float eps, const float *__restrict__ g, const float *__restrict__ bta)
 {
-#pragma clang fp contract(off)  // same float roundings as jasmine's sequential column loops
-    int v = blockIdx.x * blockDim.x + threadIdx.x;
-    if (v >= n_vec) return;
-    const float *xr = x + (long)v * vstride;
-    float *yr = y + (long)v * ystride;
+#pragma clang fp contract(off)  // separate multiply and add, as jasmine's loops round them
+    __shared__ float red[W][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int v = blockIdx.x * 64 + lane;
+    const bool live = v < n_vec;
+    const float *xr = x + (long)(live ? v : 0) * vstride;
+    float *yr = y + (long)(live ? v : 0) * ystride;
+    const int per = (len + W - 1) / W, r0 = min(len, w * per), r1 = min(len, r0 + per);
+    auto combine = [&](float a, bool is_max) {
+        red[w][lane] = a;
+        __syncthreads();
+        float t = red[0][lane];
+#pragma unroll
+        for (int k = 1; k < W; ++k) t = is_max ? fmaxf(t, red[k][lane]) : t + red[k][lane];
+        __syncthreads();
+        return t;
+    };
     if (MODE == RM_SOFTMAX) {
         float m = -FLT_MAX;
-        for (int e = 0; e < len; ++e) m = xr[e * estride] > m ? xr[e * estride] : m;
+        if (live)
+#pragma unroll 8
+            for (int e = r0; e < r1; ++e) m = fmaxf(m, xr[e * estride]);
+        m = combine(m, true);
         float s = 0.f;
-        for (int e = 0; e < len; ++e) s += expf(xr[e * estride] - m);
-        for (int e = 0; e < len; ++e) yr[e * estride] = expf(xr[e * estride] - m) / s;
+        if (live)
+#pragma unroll 8
+            for (int e = r0; e < r1; ++e) s += expf(xr[e * estride] - m);
+        s = combine(s, false);
+        if (live)
+            for (int e = r0; e < r1; ++e) yr[e * estride] = expf(xr[e * estride] - m) / s;
     } else if (MODE == RM_LN) {
         float s = 0.f;
-        for (int e = 0; e < len; ++e) s += xr[e * estride];
-        float mean = s / (float)len;
+        if (live)
+#pragma unroll 8
+            for (int e = r0; e < r1; ++e) s += xr[e * estride];
+        const float mean = combine(s, false) / (float)len;
         float s2 = 0.f;
-        for (int e = 0; e < len; ++e) { float d = xr[e * estride] - mean; s2 += d * d; }
-        float den = sqrtf(s2 / (float)len + eps);
-        for (int e = 0; e < len; ++e)
-            yr[e * estride] = (xr[e * estride] - mean) / den * (g ? g[e] : 1.f) + (bta ? bta[e] : 0.f);
+        if (live)
+#pragma unroll 8
+            for (int e = r0; e < r1; ++e) {
+                const float d = xr[e * estride] - mean;
+                s2 += d * d;
+            }
+        const float den = sqrtf(combine(s2, false) / (float)len + eps);
+        if (live)
+            for (int e = r0; e < r1; ++e)
+                yr[e * estride] = (xr[e * estride] - mean) / den * (g ? g[e] : 1.f) + (bta ? bta[e] : 0.f);
     } else {
         float s2 = 0.f;
-        for (int e = 0; e < len; ++e) s2 += xr[e * estride] * xr[e * estride];
-        float den = sqrtf(s2 / (float)len + eps);
-        for (int e = 0; e < len; ++e) yr[e * estride] = xr[e * estride] / den * (g ? g[e] : 1.f);
+        if (live)
+#pragma unroll 8
+            for (int e = r0; e < r1; ++e) s2 += xr[e * estride] * xr[e * estride];
+        const float den = sqrtf(combine(s2, false) / (float)len + eps);
+        if (live)
+            for (int e = r0; e < r1; ++e) yr[e * estride] = xr[e * estride] / den * (g ? g[e] : 1.f);
     }
 }
 
@@ -198,8 +230,13 @@ static jas_status rowop(const float *x, float *y, int n_vec, int len, long vstri
     JAS_CHECK(n_vec < (1 << 30), JAS_ERR_INVALID, "row op: too many vectors");
     hipStream_t s = stream_or_default(stream);
     if (estride != 1) {
-        hipLaunchKernelGGL((rowop_col_kernel<MODE>), dim3(ceil_div(n_vec, 256)), dim3(256), 0, s, x, y, n_vec, len,
-                           vstride, ystride, estride, eps, g, b);
+        // fewer waves for short vectors: each wave keeps at least 16 elements
+        if (len >= 128)
+            hipLaunchKernelGGL((rowop_col_kernel<MODE, 8>), dim3(ceil_div(n_vec, 64)), dim3(512), 0, s, x, y, n_vec,
+                               len, vstride, ystride, estride, eps, g, b);
+        else
+            hipLaunchKernelGGL((rowop_col_kernel<MODE, 2>), dim3(ceil_div(n_vec, 64)), dim3(128), 0, s, x, y, n_vec,
+                               len, vstride, ystride, estride, eps, g, b);
         JAS_LAUNCH_CHECK();
         return JAS_OK;
     }

@@ -2,7 +2,10 @@
 // Storage behind jasmine's mat_t (mat_t.hpp:53-69 allocate+zero, :30-42 release).
 #include "jas_common.hpp"
 
+#include <algorithm>
 #include <mutex>
+#include <unordered_map>
+#include <vector>
 
 namespace jas {
 
@@ -90,6 +93,108 @@ jas_status jas_malloc(void **p, size_t bytes)
 jas_status jas_free(void *p)
 {
     if (p) JAS_HIP(hipFree(p));
+    return JAS_OK;
+}
+
+} // extern "C"
+
+namespace jas {
+namespace {
+// Stream-ordered cache of device blocks behind the C++ headers' matrices.  Every device
+// operation the headers issue runs on the library stream, so a block released by the host
+// may be handed to the next allocation at once: work that uses it later is queued behind
+// the work that used it before.  Sizes are rounded to 1/8 of their power of two (at least
+// 512 bytes), blocks are reused by rounded size, and the cache is emptied (after a stream
+// synchronisation) when it holds more than kMaxCached or an allocation fails.
+struct Pool {
+    std::mutex mu;
+    std::unordered_map<size_t, std::vector<void *>> free_by_size;
+    std::unordered_map<void *, size_t> live;
+    size_t cached = 0;
+    static constexpr size_t kMaxCached = 16ull << 30;
+};
+Pool &pool()
+{
+    static Pool *p = new Pool;  // never destroyed: no device call after the runtime's teardown
+    return *p;
+}
+size_t pool_round(size_t b)
+{
+    if (b <= 512) return 512;
+    size_t p2 = 1;
+    while (p2 < b) p2 <<= 1;
+    const size_t g = std::max<size_t>(512, p2 / 8);
+    return (b + g - 1) / g * g;
+}
+// caller holds the lock
+hipError_t pool_drain(Pool &pl)
+{
+    hipError_t e = hipSuccess;
+    if (!pl.cached) return e;
+    if (g_stream) e = hipStreamSynchronize(g_stream);
+    for (auto &kv : pl.free_by_size)
+        for (void *q : kv.second) {
+            const hipError_t f = hipFree(q);
+            if (e == hipSuccess) e = f;
+        }
+    pl.free_by_size.clear();
+    pl.cached = 0;
+    return e;
+}
+} // namespace
+} // namespace jas
+
+extern "C" {
+
+jas_status jas_pool_alloc(void **p, size_t bytes)
+{
+    JAS_CHECK(p, JAS_ERR_INVALID, "jas_pool_alloc: null out pointer");
+    *p = nullptr;
+    const size_t r = pool_round(bytes ? bytes : 1);
+    Pool &pl = pool();
+    std::lock_guard<std::mutex> lk(pl.mu);
+    auto it = pl.free_by_size.find(r);
+    if (it != pl.free_by_size.end() && !it->second.empty()) {
+        *p = it->second.back();
+        it->second.pop_back();
+        pl.cached -= r;
+    } else {
+        hipError_t e = hipMalloc(p, r);
+        if (e != hipSuccess) {  // give the cached blocks back and try once more
+            (void)hipGetLastError();
+            (void)pool_drain(pl);
+            e = hipMalloc(p, r);
+        }
+        if (e != hipSuccess) {
+            *p = nullptr;
+            return fail(JAS_ERR_OOM, std::string("jas_pool_alloc: ") + hipGetErrorString(e));
+        }
+    }
+    pl.live[*p] = r;
+    return JAS_OK;
+}
+
+jas_status jas_pool_free(void *p)
+{
+    if (!p) return JAS_OK;
+    Pool &pl = pool();
+    std::lock_guard<std::mutex> lk(pl.mu);
+    auto it = pl.live.find(p);
+    JAS_CHECK(it != pl.live.end(), JAS_ERR_INVALID, "jas_pool_free: not a pool block");
+    const size_t r = it->second;
+    pl.live.erase(it);
+    pl.free_by_size[r].push_back(p);
+    pl.cached += r;
+    if (pl.cached > Pool::kMaxCached) JAS_HIP(pool_drain(pl));
+    return JAS_OK;
+}
+
+jas_status jas_pool_trim(size_t *cached_before)
+{
+    Pool &pl = pool();
+    std::lock_guard<std::mutex> lk(pl.mu);
+    if (cached_before) *cached_before = pl.cached;
+    JAS_HIP(pool_drain(pl));
     return JAS_OK;
 }
 

@@ -3,6 +3,7 @@
 #ifndef JASMINE_AMD_JASMINE_HIP_HPP
 #define JASMINE_AMD_JASMINE_HIP_HPP
 
+#include <atomic>
 #include <cstdint>
 #include <cstring>
 #include <stdexcept>
@@ -23,6 +24,14 @@ inline void check(jas_status s)
     if (s == JAS_ERR_INVALID) throw std::invalid_argument(m);
     if (s == JAS_ERR_RANGE) throw std::out_of_range(m);
     throw std::runtime_error(m);
+}
+
+// A process-wide counter: every mat_t takes a fresh value whenever its contents may change,
+// so (stamp) identifies one state of one matrix (caches key derived data on it).
+inline uint64_t next_stamp() noexcept
+{
+    static std::atomic<uint64_t> counter{0};
+    return counter.fetch_add(1, std::memory_order_relaxed) + 1;
 }
 
 inline void ensure_init()
@@ -73,12 +82,12 @@ public:
         if (bytes <= m_bytes && m_p) return;
         release();
         ensure_init();
-        check(jas_malloc(&m_p, bytes ? bytes : 1));
+        check(jas_pool_alloc(&m_p, bytes ? bytes : 1));
         m_bytes = bytes;
     }
     void release() noexcept
     {
-        if (m_p) jas_free(m_p);
+        if (m_p) jas_pool_free(m_p);
         m_p = nullptr;
         m_bytes = 0;
     }

@@ -597,6 +597,7 @@ template <typename scalar_type>
 requires std::is_arithmetic_v<scalar_type>
 mat_t<val_type> &mat_t<val_type>::operator=(scalar_type s)
 {
+    touch();
     if (m_scalar) {
         m_scalar_val = static_cast<val_type>(s);
         return *this;

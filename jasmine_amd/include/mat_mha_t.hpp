@@ -7,6 +7,7 @@
 // softmax); only shapes cross to the host.
 #ifndef __MAT_MHA_T_HPP__
 #define __MAT_MHA_T_HPP__
+#include <array>
 #include <cmath>
 #include <limits>
 #include <vector>
@@ -125,6 +126,11 @@ public:
 
     std::string net_type(int const &indent = 0) const { return print_indent(indent) + "mat_head_gen_t"; }
 
+    // the head's projections (read by the fused all-heads path of mat_mha_t)
+    ffn_type &q_net() { return m_q_net; }
+    ffn_type &k_net() { return m_k_net; }
+    ffn_type &v_net() { return m_v_net; }
+
     void step()
     {
         m_q_net.step();
@@ -132,6 +138,39 @@ public:
         m_v_net.step();
     }
 };
+
+namespace jas {
+// Whether mat_mha_t may run all heads through the fused path (below); the per-head path
+// computes the same attention with the score matrix materialised.
+inline bool &fused_heads_enabled()
+{
+    static bool on = true;
+    return on;
+}
+
+namespace detail {
+// Device scratch of the fused path.  A copied net starts with an empty cache.
+struct mha_scratch {
+    device_buffer w;      // [3][H][d_h][d_h] projection weights, then [3][H][d_h] biases
+    device_buffer qkv;    // self: [T][3][H][d_h]; cross: queries [T_q][H][d_h]
+    device_buffer kv;     // cross: encoder keys / values [T_k][2][H][d_h]
+    device_buffer o;      // attention output [T_q][H][d_h]
+    std::vector<uint64_t> w_stamps;
+    uint64_t kv_stamp = 0;  // stamp of the encoder output the cached keys / values belong to
+    int kv_T = 0;
+    mha_scratch() = default;
+    mha_scratch(const mha_scratch &) {}
+    mha_scratch &operator=(const mha_scratch &)
+    {
+        w_stamps.clear();
+        kv_stamp = 0;
+        return *this;
+    }
+    mha_scratch(mha_scratch &&) noexcept = default;
+    mha_scratch &operator=(mha_scratch &&) noexcept = default;
+};
+} // namespace detail
+} // namespace jas
 
 // stack matrices by rows (mat_mha_t.hpp:163-196): device-to-device block copies
 template <typename val_type>
@@ -180,11 +219,126 @@ private:
     int m_num_heads;
     int m_d_model;
     int m_d_head;
+    bool m_mask = false;
+    jas::detail::mha_scratch m_fx;
+
+    // All heads at once for float matrices with d_h in {32, 64, 128}: the per-head Q/K/V
+    // projections are three batched GEMMs (one problem per head) writing token-major rows,
+    // attention is the flash kernel over every head (no score matrix in memory), and the
+    // output projection reads the token-major result transposed.  Cross attention keeps
+    // the encoder-side keys / values while the encoder output and the weights are unchanged.
+    // Same arithmetic as the per-head path up to rounding order (scores scaled in float).
+    bool fusable(int Tq) const
+    {
+        if constexpr (!std::is_same_v<val_type, float>) return false;
+        else {
+            if (!jas::fused_heads_enabled() || Tq < 1) return false;
+            if (m_d_head != 32 && m_d_head != 64 && m_d_head != 128) return false;
+            auto &self = const_cast<mat_mha_t &>(*this);
+            for (auto &hd : self.m_heads)
+                for (auto *n : {&hd.q_net(), &hd.k_net(), &hd.v_net()})
+                    if (!n->weight().row_first() || n->weight().row_num() != m_d_head ||
+                        n->weight().col_num() != m_d_head || n->bias().row_num() != m_d_head ||
+                        n->bias().col_num() != 1)
+                        return false;
+            auto &wo = self.m_output_proj;
+            return wo.weight().row_first() && wo.weight().row_num() == m_d_model &&
+                   wo.weight().col_num() == m_d_model && wo.bias().row_num() == m_d_model && wo.bias().col_num() == 1;
+        }
+    }
+
+    // gather the heads' weights and biases into one block (when any of them changed)
+    const float *packed_weights()
+    {
+        const int H = m_num_heads, dh = m_d_head;
+        std::vector<uint64_t> st;
+        st.reserve(6 * H);
+        for (auto &hd : m_heads)
+            for (auto *n : {&hd.q_net(), &hd.k_net(), &hd.v_net()}) {
+                st.push_back(n->weight().stamp());
+                st.push_back(n->bias().stamp());
+            }
+        if (st != m_fx.w_stamps) {
+            m_fx.w.allocate(sizeof(float) * 3 * H * ((size_t)dh * dh + dh));
+            float *w = (float *)m_fx.w.get();
+            float *b = w + (size_t)3 * H * dh * dh;
+            for (int h = 0; h < H; ++h) {
+                const std::array<weight_net_t<input_type, updator_type> *, 3> ns{
+                    &m_heads[h].q_net(), &m_heads[h].k_net(), &m_heads[h].v_net()};
+                for (int sct = 0; sct < 3; ++sct) {
+                    const size_t i = (size_t)sct * H + h;
+                    jas::check(jas_memcpy_d2d(w + i * dh * dh, ns[sct]->weight().device_data(),
+                                              sizeof(float) * dh * dh, nullptr));
+                    jas::check(jas_memcpy_d2d(b + i * dh, ns[sct]->bias().device_data(), sizeof(float) * dh, nullptr));
+                }
+            }
+            // device_data() may have uploaded a host mirror: stamps are unchanged by that
+            m_fx.w_stamps = std::move(st);
+            m_fx.kv_stamp = 0;
+        }
+        return (const float *)m_fx.w.get();
+    }
+
+    // projection `sct` (0 q, 1 k, 2 v) of every head: out(n, h*dh + m) at out[n*ld + h*dh + m]
+    void project(int sct, const jas::gemm_operand_t<float> &x, int T, float *out, long ld)
+    {
+        const int H = m_num_heads, dh = m_d_head;
+        const float *w = (const float *)m_fx.w.get();
+        const float *b = w + (size_t)3 * H * dh * dh + (size_t)sct * H * dh;
+        jas::check(jas_gemm(dh, T, dh, w + (size_t)sct * H * dh * dh, dh, 1, x.p, x.s0, x.s1, out, 1, ld, b, 1,
+                            JAS_ACT_NONE, 0, H, (long)dh * dh, (long)dh * x.s0, dh, dh, nullptr));
+    }
+
+    mat_t<val_type> fused_forward(const input_type &input, const input_type *encoder_input)
+    {
+        const int d = m_d_model, H = m_num_heads, dh = m_d_head, Tq = input.col_num();
+        packed_weights();
+        auto xq = jas::gemm_operand<float>(input);
+        const float *Q, *K, *V;
+        long qs, ks;
+        int Tk;
+        if (!encoder_input) {
+            Tk = Tq;
+            m_fx.qkv.allocate(sizeof(float) * (size_t)Tq * 3 * d);
+            float *qkv = (float *)m_fx.qkv.get();
+            for (int sct = 0; sct < 3; ++sct) project(sct, xq, Tq, qkv + (size_t)sct * d, 3L * d);
+            Q = qkv, K = qkv + d, V = qkv + 2 * d, qs = ks = 3L * d;
+        } else {
+            Tk = encoder_input->col_num();
+            m_fx.qkv.allocate(sizeof(float) * (size_t)Tq * d);
+            float *q = (float *)m_fx.qkv.get();
+            project(0, xq, Tq, q, d);
+            const uint64_t es = encoder_input->stamp();
+            if (m_fx.kv_stamp != es || m_fx.kv_T != Tk) {
+                auto xe = jas::gemm_operand<float>(*encoder_input);
+                m_fx.kv.allocate(sizeof(float) * (size_t)Tk * 2 * d);
+                float *kv = (float *)m_fx.kv.get();
+                project(1, xe, Tk, kv, 2L * d);
+                project(2, xe, Tk, kv + d, 2L * d);
+                m_fx.kv_stamp = es;
+                m_fx.kv_T = Tk;
+            }
+            const float *kv = (const float *)m_fx.kv.get();
+            Q = q, K = kv, V = kv + d, qs = d, ks = 2L * d;
+        }
+        m_fx.o.allocate(sizeof(float) * (size_t)Tq * d);
+        float *o = (float *)m_fx.o.get();
+        const bool causal = !encoder_input && m_mask;
+        jas::check(jas_attn_prefill(Q, K, V, o, 1, H, Tq, Tk, dh, (long)Tq * qs, dh, qs, (long)Tk * ks, dh, ks,
+                                    (long)Tq * d, dh, d, (float)(1.0 / std::sqrt((double)dh)), causal ? 1 : 0,
+                                    JAS_F32, nullptr));
+        // y = W_o . concat(heads) + b_o, the concatenation read from the token-major rows
+        auto &wo = m_output_proj;
+        mat_t<val_type> y(d, Tq, typename mat_t<val_type>::device_uninit_tag{});
+        jas::check(jas_gemm(d, Tq, d, wo.weight().device_data(), d, 1, o, 1, d, y.device_data_mut(), Tq, 1,
+                            wo.bias().device_data(), 1, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, nullptr));
+        return y;
+    }
 
 public:
     mat_mha_t(int num_heads = 1, int d_model = 1, bool mask = false, int seq_len = 1)
         : m_output_proj(d_model, d_model), m_num_heads(num_heads), m_d_model(d_model),
-          m_d_head(num_heads ? d_model / num_heads : 0)
+          m_d_head(num_heads ? d_model / num_heads : 0), m_mask(mask)
     {
         if (num_heads <= 0 || d_model % num_heads != 0) throw std::runtime_error("d_model must be divisible by num_heads");
         for (int i = 0; i < num_heads; ++i) m_heads.emplace_back(m_d_head, mask, seq_len);
@@ -196,6 +350,7 @@ public:
         m_num_heads = num_heads;
         m_d_model = d_model;
         m_d_head = d_model / num_heads;
+        m_mask = mask;
         m_heads.resize(num_heads);
         for (int i = 0; i < num_heads; ++i) m_heads[i].set_param(m_d_head, mask, seq_len);
         m_output_proj.reinit(std::vector<int>{d_model, d_model});
@@ -204,6 +359,7 @@ public:
     mat_t<val_type> forward(const input_type &input)
     {
         if (input.row_num() != m_d_model) throw std::runtime_error("Input row dimension must match d_model");
+        if (fusable(input.col_num())) return fused_forward(input, nullptr);
         auto splits = vsplit(input, m_num_heads);
         std::vector<mat_t<val_type>> head_outputs;
         head_outputs.reserve(m_num_heads);
@@ -216,6 +372,7 @@ public:
         if (input.row_num() != m_d_model) throw std::runtime_error("Input row dimension must match d_model");
         if (encoder_input.row_num() != m_d_model)
             throw std::runtime_error("Encoder input row dimension must match d_model");
+        if (fusable(input.col_num()) && encoder_input.col_num() >= 1) return fused_forward(input, &encoder_input);
         auto splits = vsplit(input, m_num_heads);
         auto enc_splits = vsplit(encoder_input, m_num_heads);
         std::vector<mat_t<val_type>> head_outputs;

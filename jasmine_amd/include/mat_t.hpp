@@ -43,11 +43,15 @@ private:
     mutable std::vector<val_type> m_host;
     mutable jas::device_buffer m_dev;
     mutable bool m_host_ok = true, m_dev_ok = false;
+    uint64_t m_stamp = jas::next_stamp();  // renewed on every change of the contents
+
+    void touch() noexcept { m_stamp = jas::next_stamp(); }
 
     size_t count() const { return (size_t)m_rows * (size_t)m_cols; }
 
     void init_scalar(val_type v)
     {
+        touch();
         m_scalar = true;
         m_alloc = true;
         m_scalar_val = v;
@@ -61,6 +65,7 @@ private:
     // zero-filled rows x cols (mat_t.hpp:53-69): zeros on the host, device copy on demand
     void init_matrix(int rows, int cols, bool row_first)
     {
+        touch();
         m_scalar = false;
         m_alloc = true;
         m_rows = rows;
@@ -74,6 +79,7 @@ private:
 
     void copy_from(const mat_t &m)
     {
+        touch();
         m_row_first = m.m_row_first;
         if (m.m_scalar) {
             init_scalar(m.m_scalar_val);
@@ -100,6 +106,8 @@ private:
 
     void move_from(mat_t &m) noexcept
     {
+        touch();
+        m.touch();
         m_rows = m.m_rows, m_cols = m.m_cols, m_row_first = m.m_row_first;
         m_scalar = m.m_scalar, m_alloc = m.m_alloc, m_scalar_val = m.m_scalar_val;
         m_host = std::move(m.m_host);
@@ -189,6 +197,9 @@ public:
     bool row_first() const noexcept { return m_row_first; }
     std::tuple<int, int> shape() const noexcept { return std::make_tuple(row_num(), col_num()); }
     bool valid() const noexcept { return m_alloc; }
+    // identifies the current contents: changes whenever they may have changed (a write
+    // through a reference kept from operator() after a later stamp() is not seen)
+    uint64_t stamp() const noexcept { return m_stamp; }
 
     // mat_t.hpp:280-300: 1x1 becomes a scalar holding element (0,0); a different element
     // count re-allocates a zero row-major matrix; the same count keeps the matrix as is
@@ -234,6 +245,7 @@ public:
     {
         const val_type *p = device_data();
         if (!m_scalar) m_host_ok = false;
+        touch();
         return const_cast<val_type *>(p);
     }
     // the jas_leaf describing this matrix as an expression operand
@@ -253,6 +265,7 @@ public:
     // ---- element access with jasmine's modulo broadcast (mat_t.hpp:302-320) ----
     val_type &operator()(int r, int c)
     {
+        touch();
         if (m_scalar) return m_scalar_val;
         host_sync();
         m_dev_ok = false;  // the caller may write through the reference

@@ -6,6 +6,7 @@
 //
 // The entry points mirror the reference driver one for one (api_X <-> ref_X); the bodies
 // are written against this API only, so every call exercises the device path.
+#include <chrono>
 #include <cmath>
 #include <cstring>
 #include <stdexcept>
@@ -251,6 +252,73 @@ int api_transformer(const float *en, int Te, const float *de, int Td, int d, int
         tf.encoder_forward(to_mat(en, d, Te));
         from_mat(tf.forward(to_mat(de, d, Td)), Y);
     });
+}
+
+// one model: encoder_forward(en1), forward(de) -> Y1; encoder_forward(en2), forward(de)
+// twice -> Y2, Y3 (the decoder's cross attention must follow the new encoder output)
+int api_transformer_reencode(const float *en1, int Te1, const float *en2, int Te2, const float *de, int Td, int d,
+                             int H, int n_enc, int n_dec, const float *W, float *Y1, float *Y2, float *Y3)
+{
+    return guarded([&] {
+        transformer_base_t<mat_t<float>, upd_t> tf(n_enc, n_dec, H, d);
+        g_fixture = W;
+        g_fixture_pos = 0;
+        tf.init_weight<api_fixture_init_t>();
+        auto dm = to_mat(de, d, Td);
+        tf.encoder_forward(to_mat(en1, d, Te1));
+        from_mat(tf.forward(dm), Y1);
+        tf.encoder_forward(to_mat(en2, d, Te2));
+        from_mat(tf.forward(dm), Y2);
+        from_mat(tf.forward(dm), Y3);
+    });
+}
+
+// wall-clock milliseconds per encoder_forward and per decoder forward (device work
+// synchronised) of a transformer_base_t with deterministic pseudo-random weights
+int api_transformer_bench(int d, int H, int n_enc, int n_dec, int Te, int Td, int fused, int reps, double *ms_enc,
+                          double *ms_fwd)
+{
+    return guarded([&] {
+        jas::fused_heads_enabled() = fused != 0;
+        transformer_base_t<mat_t<float>, upd_t> tf(n_enc, n_dec, H, d);
+        std::vector<float> w(1 << 26);
+        uint32_t st = 12345u;
+        for (auto &v : w) {
+            st = st * 1664525u + 1013904223u;
+            v = ((float)(st >> 8) / 16777216.0f - 0.5f) * 0.08f;
+        }
+        g_fixture = w.data();
+        g_fixture_pos = 0;
+        tf.init_weight<api_fixture_init_t>();
+        if (g_fixture_pos > w.size()) throw std::runtime_error("api_transformer_bench: model too large");
+        std::vector<float> en((size_t)d * Te), de((size_t)d * Td);
+        for (size_t i = 0; i < en.size(); ++i) en[i] = w[i % 4096] * 25.0f;
+        for (size_t i = 0; i < de.size(); ++i) de[i] = w[(i + 77) % 4096] * 25.0f;
+        auto em = to_mat(en.data(), d, Te), dm = to_mat(de.data(), d, Td);
+        auto now = [] { return std::chrono::steady_clock::now(); };
+        auto sync = [] { jas::check(jas_synchronize(nullptr)); };
+        tf.encoder_forward(em);
+        (void)tf.forward(dm);
+        sync();
+        auto t0 = now();
+        for (int r = 0; r < reps; ++r) tf.encoder_forward(em);
+        sync();
+        auto t1 = now();
+        for (int r = 0; r < reps; ++r) (void)tf.forward(dm);
+        sync();
+        auto t2 = now();
+        *ms_enc = std::chrono::duration<double, std::milli>(t1 - t0).count() / reps;
+        *ms_fwd = std::chrono::duration<double, std::milli>(t2 - t1).count() / reps;
+        jas::fused_heads_enabled() = true;
+    });
+}
+
+// 1: mat_mha_t runs every head through the fused path where it applies (the default);
+// 0: the per-head path with materialised scores
+int api_set_fused_heads(int on)
+{
+    jas::fused_heads_enabled() = on != 0;
+    return 0;
 }
 
 // parameters transformer_base_t::init_weight visits, counted without a device

@@ -111,6 +111,29 @@ def main():
     ref.ref_transformer(fp(en), Te, fp(np.ascontiguousarray(de[:, :3])), 3, d, H, ne, nd, fp(Wt), fp(Yp))
     g["tf_prefix3"] = Yp
 
+    # head dims the fused all-heads path takes (32, 64): self attention with the mask, cross
+    # attention, and an encoder-decoder stack with its causal-prefix invariant
+    for tag, (d2, H2, T2, Tk2, seed) in {"mha32": (64, 2, 40, 23, 70), "mha64": (128, 2, 33, 19, 74)}.items():
+        n2 = 3 * H2 * ((d2 // H2) ** 2 + d2 // H2) + d2 * d2 + d2
+        W2 = normal(n2, 1, seed, std=0.1)
+        X2, K2 = normal((d2, T2), 1, seed + 1), normal((d2, Tk2), 1, seed + 2)
+        Ys, Yc = np.zeros((d2, T2), np.float32), np.zeros((d2, T2), np.float32)
+        ref.ref_mha(fp(X2), None, d2, H2, T2, T2, fp(W2), 1, fp(Ys))
+        ref.ref_mha(fp(X2), fp(K2), d2, H2, T2, Tk2, fp(W2), 0, fp(Yc))
+        g.update({f"{tag}_w": W2, f"{tag}_x": X2, f"{tag}_xk": K2, f"{tag}_self": Ys, f"{tag}_cross": Yc,
+                  f"{tag}_dims": np.array([d2, H2, T2, Tk2])})
+    d3, H3, ne3, nd3, Te3, Td3 = 64, 2, 1, 2, 20, 17
+    W3 = normal(ref.ref_transformer_nparams(d3, H3, ne3, nd3), 1, 78, std=0.1)
+    en3, de3 = normal((d3, Te3), 1, 79), normal((d3, Td3), 1, 80)
+    Y3, Y3p = np.zeros((d3, Td3), np.float32), np.zeros((d3, 5), np.float32)
+    ref.ref_transformer(fp(en3), Te3, fp(de3), Td3, d3, H3, ne3, nd3, fp(W3), fp(Y3))
+    ref.ref_transformer(fp(en3), Te3, fp(np.ascontiguousarray(de3[:, :5])), 5, d3, H3, ne3, nd3, fp(W3), fp(Y3p))
+    en3b, Y3b = normal((d3, Te3 + 3), 1, 81), np.zeros((d3, Td3), np.float32)  # a second, longer encoder input
+    ref.ref_transformer(fp(en3b), Te3 + 3, fp(de3), Td3, d3, H3, ne3, nd3, fp(W3), fp(Y3b))
+    g.update(tf32_en2=en3b, tf32_y2=Y3b)
+    g.update(tf32_w=W3, tf32_en=en3, tf32_de=de3, tf32_y=Y3, tf32_prefix5=Y3p,
+             tf32_dims=np.array([d3, H3, ne3, nd3, Te3, Td3]))
+
     np.savez_compressed(OUT, **g)
     print("wrote", OUT, os.path.getsize(OUT), "bytes,", len(g), "arrays")
 

@@ -62,7 +62,7 @@ def bitexact(a, b):
 def test_api_library_exports(api):
     for name in ("api_gemm", "api_gemm_tn", "api_cfg2_expr", "api_expr", "api_hsoftmax", "api_softmax_global",
                  "api_reductions", "api_linear", "api_relu", "api_sigmoid", "api_layernorm_cols", "api_head",
-                 "api_mha", "api_rope", "api_transformer", "api_transformer_nparams", "api_last_error"):
+                 "api_mha", "api_rope", "api_transformer", "api_transformer_nparams", "api_last_error", "api_set_fused_heads", "api_transformer_reencode"):
         assert hasattr(api, name), name
 
 
@@ -197,3 +197,62 @@ def test_api_transformer(api, g):
     ok(api, api.api_transformer(fp(en), Te, fp(np.ascontiguousarray(de[:, :3])), 3, d, H, ne, nd, fp(Wt), fp(Yp)))
     close(Yp, g["tf_prefix3"])
     close(Y[:, :3], Yp)
+
+
+def _mha_case(api, g, tag, cross):
+    d, H, T, Tk = (int(v) for v in g[f"{tag}_dims"])
+    Y = np.zeros((d, T), np.float32)
+    if cross:
+        ok(api, api.api_mha(fp(g[f"{tag}_x"]), fp(g[f"{tag}_xk"]), d, H, T, Tk, fp(g[f"{tag}_w"]), 0, fp(Y)))
+    else:
+        ok(api, api.api_mha(fp(g[f"{tag}_x"]), None, d, H, T, T, fp(g[f"{tag}_w"]), 1, fp(Y)))
+    return Y
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tag", ["mha32", "mha64"])
+@pytest.mark.parametrize("cross", [0, 1])
+def test_api_mha_fused_heads(api, g, tag, cross):
+    """Head dims 32 / 64: every head in batched projections plus the flash kernel, against
+    the reference's outputs; the per-head path (materialised scores) agrees with both."""
+    Y = _mha_case(api, g, tag, cross)
+    close(Y, g[f"{tag}_cross" if cross else f"{tag}_self"])
+    api.api_set_fused_heads(0)
+    try:
+        Yp = _mha_case(api, g, tag, cross)
+    finally:
+        api.api_set_fused_heads(1)
+    close(Yp, g[f"{tag}_cross" if cross else f"{tag}_self"])
+    close(Y, Yp, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fused", [1, 0])
+def test_api_transformer_head_dim_32(api, g, fused):
+    d, H, ne, nd, Te, Td = (int(v) for v in g["tf32_dims"])
+    api.api_set_fused_heads(fused)
+    try:
+        Y = np.zeros((d, Td), np.float32)
+        ok(api, api.api_transformer(fp(g["tf32_en"]), Te, fp(g["tf32_de"]), Td, d, H, ne, nd, fp(g["tf32_w"]), fp(Y)))
+        close(Y, g["tf32_y"])
+        Yp = np.zeros((d, 5), np.float32)
+        de5 = np.ascontiguousarray(g["tf32_de"][:, :5])
+        ok(api, api.api_transformer(fp(g["tf32_en"]), Te, fp(de5), 5, d, H, ne, nd, fp(g["tf32_w"]), fp(Yp)))
+        close(Yp, g["tf32_prefix5"])
+        close(Y[:, :5], Yp)
+    finally:
+        api.api_set_fused_heads(1)
+
+
+@pytest.mark.gpu
+def test_api_transformer_reencode(api, g):
+    """The decoder's cross attention keeps the encoder-side keys / values between forwards;
+    a new encoder_forward must replace them (its output is a new matrix state)."""
+    d, H, ne, nd, Te, Td = (int(v) for v in g["tf32_dims"])
+    en2 = g["tf32_en2"]
+    Y1, Y2, Y3 = (np.zeros((d, Td), np.float32) for _ in range(3))
+    ok(api, api.api_transformer_reencode(fp(g["tf32_en"]), Te, fp(en2), en2.shape[1], fp(g["tf32_de"]), Td, d, H, ne,
+                                         nd, fp(g["tf32_w"]), fp(Y1), fp(Y2), fp(Y3)))
+    close(Y1, g["tf32_y"])
+    close(Y2, g["tf32_y2"])
+    assert np.array_equal(Y2, Y3)

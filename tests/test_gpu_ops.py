@@ -224,6 +224,29 @@ def test_column_layernorm_jasmine(jas):
     close(dy.numpy(), g["hsoftmax"], atol=1e-6, rtol=1e-5)
 
 
+@pytest.mark.parametrize("mode", ["ln", "rms", "softmax"])
+@pytest.mark.parametrize("R,Cc", [(512, 100), (130, 37), (1000, 64), (3, 5), (4096, 130)])
+def test_column_row_ops(jas, mode, R, Cc):
+    """Vectors down the columns of a row-major [R, Cc] matrix (element stride Cc): the
+    column kernels (64 vectors per workgroup, rows split over waves) against the oracle's
+    row functions on the transposed matrix."""
+    x = normal((R, Cc), 34, 0)
+    xt = np.ascontiguousarray(x.T)
+    gam, bet = normal(R, 34, 1), normal(R, 34, 2)
+    want = np.zeros_like(xt)
+    dx, dy, dg, db = jas.to_device(x), jas.DeviceArray((R, Cc)), jas.to_device(gam), jas.to_device(bet)
+    if mode == "ln":
+        orc.orc_layernorm_rows(fp(xt), Cc, R, 1e-5, fp(gam), fp(bet), fp(want))
+        jas.check(jas.lib.jas_layernorm(dx.p, dy.p, Cc, R, 1, 1, Cc, 1e-5, dg.p, db.p, None))
+    elif mode == "rms":
+        orc.orc_rmsnorm_rows(fp(xt), Cc, R, 1e-6, fp(gam), fp(want))
+        jas.check(jas.lib.jas_rmsnorm(dx.p, dy.p, Cc, R, 1, 1, Cc, 1e-6, dg.p, None))
+    else:
+        orc.orc_hsoftmax(fp(xt), Cc, R, fp(want))
+        jas.check(jas.lib.jas_softmax(dx.p, dy.p, Cc, R, 1, 1, Cc, None))
+    close(dy.numpy(), np.ascontiguousarray(want.T), atol=1e-5, rtol=1e-5)
+
+
 def test_softmax_global(jas):
     x = normal((300, 517), 5, 0)
     dx, dy = jas.to_device(x), jas.DeviceArray(x.shape)
@@ -508,3 +531,25 @@ def test_rope_jasmine_f64(jas):
             for r in range(2):
                 want[2 * i + r, m] = entry(2 * i + r, 2 * m) * x[2 * i, m] + entry(2 * i + r, 2 * m + 1) * x[2 * i + 1, m]
     assert np.max(np.abs(dy.numpy() - want)) <= 1e-13
+
+
+# ---------------------------------------------------------------- block pool behind mat_t
+def test_pool_reuses_and_trims(jas):
+    import ctypes as C
+    lib = jas.lib
+    a, b, c = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    jas.check(lib.jas_pool_alloc(C.byref(a), 1000))
+    jas.check(lib.jas_pool_alloc(C.byref(b), 1000))
+    assert a.value and b.value and a.value != b.value
+    jas.check(lib.jas_pool_free(b))
+    jas.check(lib.jas_pool_alloc(C.byref(c), 900))  # same rounded size (1 KiB): the cached block
+    assert c.value == b.value
+    with pytest.raises(jas.JasError):
+        jas.check(lib.jas_pool_free(C.c_void_p(a.value + 4)))  # not a block of the pool
+    jas.check(lib.jas_pool_free(a))
+    jas.check(lib.jas_pool_free(c))
+    n = C.c_size_t()
+    jas.check(lib.jas_pool_trim(C.byref(n)))
+    assert n.value >= 2048
+    jas.check(lib.jas_pool_trim(C.byref(n)))
+    assert n.value == 0
