@@ -348,6 +348,46 @@ def load_traffic(args, dom_kernel_class):
     return None if c is None else round(c["bytes_per_launch"])
 
 
+def encdec_flops(d, H, ne, nd, T):
+    """FLOPs of one encoder_forward and of one decoder forward (cross-attention keys/values
+    already cached) of jasmine's transformer_base_t: per-head d_h x d_h projections, d x d
+    output projection and FFN, attention 4*T*T*d (halved under the causal mask)."""
+    dh = d // H
+    mha_proj = 2.0 * 3 * d * dh * T + 2.0 * d * d * T
+    ffn = 2.0 * d * d * T
+    enc = ne * (mha_proj + 4.0 * T * T * d + ffn)
+    dec = nd * (mha_proj + 2.0 * T * T * d + 2.0 * d * dh * T + 2.0 * d * d * T + 4.0 * T * T * d + ffn)
+    return enc, dec
+
+
+def run_encdec(reps=5):
+    """jasmine's encoder-decoder transformer through the C++ API (tests/cpp/api_driver.cpp,
+    built against this build's headers): wall ms per encoder_forward and per decoder forward,
+    all-heads fused path and the per-head path (materialised scores)."""
+    import ctypes as C
+    path = os.path.join(ROOT, "tests", "cpp", "libjasapi.so")
+    if not os.path.exists(path):
+        return {"skipped": "tests/cpp/libjasapi.so is not built"}
+    api = C.CDLL(path)
+    api.api_last_error.restype = C.c_char_p
+    out = {}
+    for tag, (d, H, ne, nd, T) in {"base_T512": (512, 8, 6, 6, 512), "d1024_T1024": (1024, 16, 6, 6, 1024)}.items():
+        fe, fd = encdec_flops(d, H, ne, nd, T)
+        row = {"workload": f"transformer_base_t d {d}, {H} heads, {ne}+{nd} layers, {T} tokens in and out, fp32"}
+        for fused in (1, 0):
+            a, b = C.c_double(), C.c_double()
+            rc = api.api_transformer_bench(d, H, ne, nd, T, T, fused, reps, C.byref(a), C.byref(b))
+            if rc:
+                raise RuntimeError(api.api_last_error().decode())
+            row["fused" if fused else "per_head"] = {
+                "encode_ms": round(a.value, 3), "forward_ms": round(b.value, 3),
+                "encode_tflops": round(fe / a.value / 1e9, 2), "forward_tflops": round(fd / b.value / 1e9, 2)}
+        row["mfma_frac_forward"] = round(row["fused"]["forward_tflops"] / 157.3, 4)
+        out[tag] = row
+        log(f"[bench] encdec {tag}: fused {row['fused']}, per-head {row['per_head']}")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -357,6 +397,9 @@ def main():
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--no-gpt2", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-encdec", action="store_true", help="skip the C++ API encoder-decoder leg")
+    ap.add_argument("--encdec-only", action="store_true",
+                    help="only the C++ API encoder-decoder leg (one JSON object; for profilers)")
     ap.add_argument("--no-bf16", action="store_true", help="skip the bf16-storage LLaMA leg")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the config 2/3 kernel lines (one JSON object; for profilers)")
@@ -379,6 +422,11 @@ def main():
         import jasmine_amd as jas
         jas.check(jas.lib.jas_init(0))
         print(json.dumps({"kernels": run_kernel_legs(jas)}), flush=True)
+        return
+    if args.encdec_only:
+        import jasmine_amd as jas
+        jas.check(jas.lib.jas_init(0))
+        print(json.dumps({"encdec_cpp_api": run_encdec()}), flush=True)
         return
     if args.summarize_pmc:
         out = summarize_pmc(*args.summarize_pmc, args)
@@ -517,6 +565,13 @@ def main():
         except Exception as e:  # the headline number stands on its own
             log("[bench] gpt2 legs failed:", e)
 
+    encdec = None
+    if not args.no_encdec:
+        try:
+            encdec = run_encdec()
+        except Exception as e:  # the headline number stands on its own
+            log("[bench] encoder-decoder leg failed:", e)
+
     line = {
         "metric": "decode tok/s (GPT-2-small, LLaMA-7B shape); kernel % of HBM/MFMA peak",
         "value": round(tok_s, 2),
@@ -552,6 +607,7 @@ def main():
         "llama7b_bf16_storage": llama_bf16,
         "gpt2_small": gpt2,
         "tiny_gpt2": tiny,
+        "encdec_cpp_api": encdec,
         "kernels": kernels,
     }
     print(json.dumps(line), flush=True)

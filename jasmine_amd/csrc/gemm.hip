@@ -37,17 +37,19 @@ constexpr int TBM = 128, TBN = 128, TBK = 16, TLD = 20;  // LDS row stride (floa
 enum LoadMode : int { LM_KC = 0, LM_OC = 1, LM_GEN = 2, LM_PK = 3, LM_PKB = 4 };
 
 
-// Loads a [128 outer x 16 k] tile of X(o, k) = X[o*so + k*sk] into registers, then LDS
-// rows [o][k] (K-contiguous, padded stride TLD).
-template <int MODE>
+// Loads an [OUTER (128 or 64) outer x 16 k] tile of X(o, k) = X[o*so + k*sk] into
+// registers (256 threads), then LDS rows [o][k] (K-contiguous, padded stride TLD).
+template <int MODE, int OUTER = 128>
 struct TileLoader {
-    float r[8];
+    static constexpr int NV = OUTER / 64;  // float4 loads per thread (vector modes)
+    static constexpr int NS = OUTER / 16;  // scalar loads per thread (generic mode)
+    float r[NS];
     __device__ __forceinline__ void load(const float *__restrict__ X, long so, long sk, int o0, int k0, int O, int K,
                                          int tid)
     {
         if (MODE == LM_KC) {
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
+            for (int q = 0; q < NV; ++q) {
                 int idx = tid + q * 256, o = idx >> 2, kq = (idx & 3) * 4;
                 int go = o0 + o, gk = k0 + kq;
                 float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -56,7 +58,7 @@ struct TileLoader {
             }
         } else if (MODE == LM_PK || MODE == LM_PKB) {  // 8 row tiles x one 16-wide K block: 8 contiguous blocks
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
+            for (int q = 0; q < NV; ++q) {
                 int idx = tid + q * 256, i = idx >> 6, ln = idx & 63;
                 long rt = o0 / 16 + i;
                 floatx4 v = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -73,8 +75,8 @@ struct TileLoader {
             }
         } else if (MODE == LM_OC) {
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                int idx = tid + q * 256, k = idx >> 5, oq = (idx & 31) * 4;
+            for (int q = 0; q < NV; ++q) {
+                int idx = tid + q * 256, k = idx / (OUTER / 4), oq = (idx % (OUTER / 4)) * 4;
                 int go = o0 + oq, gk = k0 + k;
                 float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (go < O && gk < K) v = *(const float4 *)(X + (long)gk * sk + go);
@@ -82,7 +84,7 @@ struct TileLoader {
             }
         } else {
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
+            for (int q = 0; q < NS; ++q) {
                 int idx = tid + q * 256, o = idx >> 4, k = idx & 15;
                 int go = o0 + o, gk = k0 + k;
                 r[q] = (go < O && gk < K) ? X[(long)go * so + (long)gk * sk] : 0.f;
@@ -93,27 +95,27 @@ struct TileLoader {
     {
         if (MODE == LM_KC) {
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
+            for (int q = 0; q < NV; ++q) {
                 int idx = tid + q * 256, o = idx >> 2, kq = (idx & 3) * 4;
                 *(float4 *)(lds + o * TLD + kq) = make_float4(r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]);
             }
         } else if (MODE == LM_PK || MODE == LM_PKB) {
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
+            for (int q = 0; q < NV; ++q) {
                 int idx = tid + q * 256, i = idx >> 6, ln = idx & 63;
                 *(float4 *)(lds + (i * 16 + (ln & 15)) * TLD + 4 * (ln >> 4)) =
                     make_float4(r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]);
             }
         } else if (MODE == LM_OC) {
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                int idx = tid + q * 256, k = idx >> 5, oq = (idx & 31) * 4;
+            for (int q = 0; q < NV; ++q) {
+                int idx = tid + q * 256, k = idx / (OUTER / 4), oq = (idx % (OUTER / 4)) * 4;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) lds[(oq + e) * TLD + k] = r[4 * q + e];
             }
         } else {
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
+            for (int q = 0; q < NS; ++q) {
                 int idx = tid + q * 256, o = idx >> 4, k = idx & 15;
                 lds[o * TLD + k] = r[q];
             }
@@ -131,31 +133,34 @@ struct TileArgs {
     int bias_mode, act, accumulate;
 };
 
-template <int AM, int BMODE, bool C4>
+// T x T output tile (T = 128, or 64 for problems too small to fill the chip with 128-wide
+// tiles); 4 waves in a 2 x 2 grid, each T/2 x T/2 (NB x NB blocks of 16 x 16)
+template <int AM, int BMODE, bool C4, int T = TBM>
 __global__ void __launch_bounds__(256) gemm_tile_kernel(const TileArgs p)
 {
-    __shared__ float As[TBM * TLD];
-    __shared__ float Bs[TBN * TLD];
+    constexpr int NB = T / 32;
+    __shared__ float As[T * TLD];
+    __shared__ float Bs[T * TLD];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wm = w >> 1, wn = w & 1, r16 = lane & 15, g = lane >> 4;
-    const int m0 = blockIdx.y * TBM, n0 = blockIdx.x * TBN;
+    const int m0 = blockIdx.y * T, n0 = blockIdx.x * T;
     const long bz = blockIdx.z;
     const float *A = p.A + bz * p.abs_;
     const float *B = p.B + bz * p.bbs;
     float *C = p.C + bz * p.cbs;
     const float *bias = p.bias ? p.bias + bz * p.biasbs : nullptr;
 
-    TileLoader<AM> la;
-    TileLoader<BMODE> lb;
+    TileLoader<AM, T> la;
+    TileLoader<BMODE, T> lb;
     // A(m, k) = A[m*as0 + k*as1]: outer = m.  B(k, n) = B[k*bs0 + n*bs1]: outer = n.
     la.load(A, p.as0, p.as1, m0, 0, p.M, p.K, tid);
     lb.load(B, p.bs1, p.bs0, n0, 0, p.N, p.K, tid);
 
-    floatx4 acc[4][4];
+    floatx4 acc[NB][NB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NB; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     for (int k0 = 0; k0 < p.K; k0 += TBK) {
         __syncthreads();
@@ -166,15 +171,15 @@ __global__ void __launch_bounds__(256) gemm_tile_kernel(const TileArgs p)
             la.load(A, p.as0, p.as1, m0, k0 + TBK, p.M, p.K, tid);
             lb.load(B, p.bs1, p.bs0, n0, k0 + TBK, p.N, p.K, tid);
         }
-        float4 a[4], b[4];
+        float4 a[NB], b[NB];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) a[i] = *(const float4 *)(As + (wm * 64 + i * 16 + r16) * TLD + 4 * g);
+        for (int i = 0; i < NB; ++i) a[i] = *(const float4 *)(As + (wm * (T / 2) + i * 16 + r16) * TLD + 4 * g);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = *(const float4 *)(Bs + (wn * 64 + j * 16 + r16) * TLD + 4 * g);
+        for (int j = 0; j < NB; ++j) b[j] = *(const float4 *)(Bs + (wn * (T / 2) + j * 16 + r16) * TLD + 4 * g);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < NB; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < NB; ++j) {
                 acc[i][j] = mfma4(a[i].x, b[j].x, acc[i][j]);
                 acc[i][j] = mfma4(a[i].y, b[j].y, acc[i][j]);
                 acc[i][j] = mfma4(a[i].z, b[j].z, acc[i][j]);
@@ -184,10 +189,10 @@ __global__ void __launch_bounds__(256) gemm_tile_kernel(const TileArgs p)
 
     // epilogue: lane holds rows m = 4g + r of each 16x16 block, column n = r16
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NB; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int mb = m0 + wm * 64 + i * 16 + 4 * g, n = n0 + wn * 64 + j * 16 + r16;
+        for (int j = 0; j < NB; ++j) {
+            const int mb = m0 + wm * (T / 2) + i * 16 + 4 * g, n = n0 + wn * (T / 2) + j * 16 + r16;
             if (n >= p.N) continue;
             float v[4];
 #pragma unroll
@@ -217,18 +222,25 @@ __global__ void __launch_bounds__(256) gemm_tile_kernel(const TileArgs p)
 }
 
 template <int AM, int BMODE>
-static void launch_tile_c(const TileArgs &p, bool c4, dim3 grid, hipStream_t s)
+static void launch_tile_c(const TileArgs &p, bool c4, bool small, int batch, hipStream_t s)
 {
-    if (c4) hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, true>), grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, false>), grid, dim3(256), 0, s, p);
+    if (small) {
+        const dim3 grid(ceil_div(p.N, 64), ceil_div(p.M, 64), batch);
+        if (c4) hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, true, 64>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, false, 64>), grid, dim3(256), 0, s, p);
+    } else {
+        const dim3 grid(ceil_div(p.N, TBN), ceil_div(p.M, TBM), batch);
+        if (c4) hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, true>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, false>), grid, dim3(256), 0, s, p);
+    }
 }
 
 template <int AM>
-static void launch_tile_b(const TileArgs &p, int bm, bool c4, dim3 grid, hipStream_t s)
+static void launch_tile_b(const TileArgs &p, int bm, bool c4, bool small, int batch, hipStream_t s)
 {
-    if (bm == LM_KC) launch_tile_c<AM, LM_KC>(p, c4, grid, s);
-    else if (bm == LM_OC) launch_tile_c<AM, LM_OC>(p, c4, grid, s);
-    else launch_tile_c<AM, LM_GEN>(p, c4, grid, s);
+    if (bm == LM_KC) launch_tile_c<AM, LM_KC>(p, c4, small, batch, s);
+    else if (bm == LM_OC) launch_tile_c<AM, LM_OC>(p, c4, small, batch, s);
+    else launch_tile_c<AM, LM_GEN>(p, c4, small, batch, s);
 }
 
 static bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
@@ -258,12 +270,13 @@ jas_status gemm_general(int M, int N, int K, const void *A, long as0, long as1, 
     int am = a_packed ? (a_bf16 ? LM_PKB : LM_PK) : pick_mode((const float *)A, as0, as1, M, K, abs_);
     int bm = pick_mode(B, bs1, bs0, N, K, bbs);
     bool c4 = cs0 == 1 && al16(C) && (cs1 % 4 == 0) && (cbs % 4 == 0);
-    dim3 grid(ceil_div(N, TBN), ceil_div(M, TBM), batch);
-    if (am == LM_PKB) launch_tile_b<LM_PKB>(p, bm, c4, grid, s);
-    else if (am == LM_PK) launch_tile_b<LM_PK>(p, bm, c4, grid, s);
-    else if (am == LM_KC) launch_tile_b<LM_KC>(p, bm, c4, grid, s);
-    else if (am == LM_OC) launch_tile_b<LM_OC>(p, bm, c4, grid, s);
-    else launch_tile_b<LM_GEN>(p, bm, c4, grid, s);
+    // 64-wide tiles when 128-wide ones would leave CUs idle (fewer workgroups than CUs)
+    const bool small = (long)ceil_div(N, TBN) * ceil_div(M, TBM) * batch < 256;
+    if (am == LM_PKB) launch_tile_b<LM_PKB>(p, bm, c4, small, batch, s);
+    else if (am == LM_PK) launch_tile_b<LM_PK>(p, bm, c4, small, batch, s);
+    else if (am == LM_KC) launch_tile_b<LM_KC>(p, bm, c4, small, batch, s);
+    else if (am == LM_OC) launch_tile_b<LM_OC>(p, bm, c4, small, batch, s);
+    else launch_tile_b<LM_GEN>(p, bm, c4, small, batch, s);
     JAS_LAUNCH_CHECK();
     return JAS_OK;
 }

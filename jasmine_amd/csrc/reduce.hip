@@ -141,71 +141,86 @@ rowop_loop_kernel(const float *__restrict__ x, float *__restrict__ y, int len, l
     }
 }
 
-// column form: a workgroup takes 64 adjacent vectors (one per lane: coalesced when they
-// are adjacent columns of a row-major matrix, vstride == 1); its W waves split the elements
-// into W contiguous ranges, each lane accumulating its range in order, and the W partials
-// are combined in wave order through LDS (deterministic for a given shape).
-template <int MODE, int W>
-__global__ void __launch_bounds__(64 * W)
+// column form: a workgroup of 512 threads takes CW adjacent vectors (coalesced when they are
+// adjacent columns of a row-major matrix, vstride == 1): lane l of the group serves vector
+// l % CW, and the 512 / CW row groups split the elements, row group r taking elements
+// r, r + RG, r + 2 RG, ...  Each thread accumulates its elements in order; the row groups'
+// partials are combined in row-group order through LDS (deterministic for a given shape).
+// With CACHE (len <= RG * 16) a thread keeps its elements in registers, so the vectors are
+// read from memory once.
+template <int MODE, int CW, bool CACHE>
+__global__ void __launch_bounds__(512)
 rowop_col_kernel(const float *__restrict__ x, float *__restrict__ y, int n_vec, int len, long vstride, long ystride,
                  long estride, float eps, const float *__restrict__ g, const float *__restrict__ bta)
 {
 #pragma clang fp contract(off)  // separate multiply and add, as jasmine's loops round them
-    __shared__ float red[W][64];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int v = blockIdx.x * 64 + lane;
+    constexpr int RG = 512 / CW, PER = 16;
+    __shared__ float red[RG][CW];
+    const int c = threadIdx.x % CW, rg = threadIdx.x / CW;
+    const int v = blockIdx.x * CW + c;
     const bool live = v < n_vec;
     const float *xr = x + (long)(live ? v : 0) * vstride;
     float *yr = y + (long)(live ? v : 0) * ystride;
-    const int per = (len + W - 1) / W, r0 = min(len, w * per), r1 = min(len, r0 + per);
-    auto combine = [&](float a, bool is_max) {
-        red[w][lane] = a;
-        __syncthreads();
-        float t = red[0][lane];
+    float xc[CACHE ? PER : 1];
+    if (CACHE) {
 #pragma unroll
-        for (int k = 1; k < W; ++k) t = is_max ? fmaxf(t, red[k][lane]) : t + red[k][lane];
+        for (int k = 0; k < PER; ++k) {
+            const int e = rg + k * RG;
+            xc[k] = (live && e < len) ? xr[e * estride] : 0.f;
+        }
+    }
+    auto at = [&](int k, int e) { return CACHE ? xc[k] : xr[(long)e * estride]; };
+    const int n_mine = live ? (len - rg + RG - 1) / RG : 0;  // elements of this thread
+    auto combine = [&](float a, bool is_max) {
+        red[rg][c] = a;
+        __syncthreads();
+        float t = red[0][c];
+        for (int k = 1; k < RG; ++k) t = is_max ? fmaxf(t, red[k][c]) : t + red[k][c];
         __syncthreads();
         return t;
     };
+#define JAS_COL_LOOP(BODY)                                                                                             \
+    if (CACHE) {                                                                                                      \
+        _Pragma("unroll") for (int k = 0; k < PER; ++k) if (k < n_mine) { const int e = rg + k * RG; BODY }           \
+    } else {                                                                                                          \
+        for (int k = 0; k < n_mine; ++k) { const int e = rg + k * RG; BODY }                                         \
+    }
     if (MODE == RM_SOFTMAX) {
         float m = -FLT_MAX;
-        if (live)
-#pragma unroll 8
-            for (int e = r0; e < r1; ++e) m = fmaxf(m, xr[e * estride]);
+        JAS_COL_LOOP(m = fmaxf(m, at(k, e));)
         m = combine(m, true);
         float s = 0.f;
-        if (live)
-#pragma unroll 8
-            for (int e = r0; e < r1; ++e) s += expf(xr[e * estride] - m);
+        JAS_COL_LOOP(s += expf(at(k, e) - m);)
         s = combine(s, false);
-        if (live)
-            for (int e = r0; e < r1; ++e) yr[e * estride] = expf(xr[e * estride] - m) / s;
+        JAS_COL_LOOP(yr[(long)e * estride] = expf(at(k, e) - m) / s;)
     } else if (MODE == RM_LN) {
         float s = 0.f;
-        if (live)
-#pragma unroll 8
-            for (int e = r0; e < r1; ++e) s += xr[e * estride];
+        JAS_COL_LOOP(s += at(k, e);)
         const float mean = combine(s, false) / (float)len;
         float s2 = 0.f;
-        if (live)
-#pragma unroll 8
-            for (int e = r0; e < r1; ++e) {
-                const float d = xr[e * estride] - mean;
-                s2 += d * d;
-            }
+        JAS_COL_LOOP(const float d = at(k, e) - mean; s2 += d * d;)
         const float den = sqrtf(combine(s2, false) / (float)len + eps);
-        if (live)
-            for (int e = r0; e < r1; ++e)
-                yr[e * estride] = (xr[e * estride] - mean) / den * (g ? g[e] : 1.f) + (bta ? bta[e] : 0.f);
+        JAS_COL_LOOP(yr[(long)e * estride] = (at(k, e) - mean) / den * (g ? g[e] : 1.f) + (bta ? bta[e] : 0.f);)
     } else {
         float s2 = 0.f;
-        if (live)
-#pragma unroll 8
-            for (int e = r0; e < r1; ++e) s2 += xr[e * estride] * xr[e * estride];
+        JAS_COL_LOOP(s2 += at(k, e) * at(k, e);)
         const float den = sqrtf(combine(s2, false) / (float)len + eps);
-        if (live)
-            for (int e = r0; e < r1; ++e) yr[e * estride] = xr[e * estride] / den * (g ? g[e] : 1.f);
+        JAS_COL_LOOP(yr[(long)e * estride] = at(k, e) / den * (g ? g[e] : 1.f);)
     }
+#undef JAS_COL_LOOP
+}
+
+template <int MODE, int CW>
+static void launch_col(const float *x, float *y, int n_vec, int len, long vstride, long ystride, long estride,
+                       float eps, const float *g, const float *b, hipStream_t s)
+{
+    const dim3 grid(ceil_div(n_vec, CW));
+    if (len <= (512 / CW) * 16)
+        hipLaunchKernelGGL((rowop_col_kernel<MODE, CW, true>), grid, dim3(512), 0, s, x, y, n_vec, len, vstride,
+                           ystride, estride, eps, g, b);
+    else
+        hipLaunchKernelGGL((rowop_col_kernel<MODE, CW, false>), grid, dim3(512), 0, s, x, y, n_vec, len, vstride,
+                           ystride, estride, eps, g, b);
 }
 
 template <int NT, int PER, int MODE>
@@ -230,13 +245,12 @@ static jas_status rowop(const float *x, float *y, int n_vec, int len, long vstri
     JAS_CHECK(n_vec < (1 << 30), JAS_ERR_INVALID, "row op: too many vectors");
     hipStream_t s = stream_or_default(stream);
     if (estride != 1) {
-        // fewer waves for short vectors: each wave keeps at least 16 elements
-        if (len >= 128)
-            hipLaunchKernelGGL((rowop_col_kernel<MODE, 8>), dim3(ceil_div(n_vec, 64)), dim3(512), 0, s, x, y, n_vec,
-                               len, vstride, ystride, estride, eps, g, b);
-        else
-            hipLaunchKernelGGL((rowop_col_kernel<MODE, 2>), dim3(ceil_div(n_vec, 64)), dim3(128), 0, s, x, y, n_vec,
-                               len, vstride, ystride, estride, eps, g, b);
+        // the widest column group that still gives one workgroup per CU (64 columns: full
+        // 256-byte rows per wave; 8: 32-byte segments, but 8x the workgroups)
+        if ((long)ceil_div(n_vec, 64) >= 256) launch_col<MODE, 64>(x, y, n_vec, len, vstride, ystride, estride, eps, g, b, s);
+        else if ((long)ceil_div(n_vec, 32) >= 256) launch_col<MODE, 32>(x, y, n_vec, len, vstride, ystride, estride, eps, g, b, s);
+        else if ((long)ceil_div(n_vec, 16) >= 256) launch_col<MODE, 16>(x, y, n_vec, len, vstride, ystride, estride, eps, g, b, s);
+        else launch_col<MODE, 8>(x, y, n_vec, len, vstride, ystride, estride, eps, g, b, s);
         JAS_LAUNCH_CHECK();
         return JAS_OK;
     }
