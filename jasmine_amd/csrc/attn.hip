@@ -97,10 +97,10 @@ __device__ __forceinline__ bool fa_work_item(int nqb, int BH, int &bh, int &qb)
 // v_mfma_f32_16x16x32_bf16 (fp32 accumulate, softmax in fp32, P rounded to bf16 for the
 // second product); the reduction index of each product is permuted identically in both
 // operands so that S lands in the P operand's registers with no shuffle.
-template <int D, bool BF16, int BK>
-__global__ void __launch_bounds__(64 * FA_WAVES) flash_prefill_kernel(const PrefillArgs p)
+template <int D, bool BF16, int BK, int NW = FA_WAVES>
+__global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArgs p)
 {
-    constexpr int FA_NW = FA_WAVES, FA_BQ = 16 * FA_NW;
+    constexpr int FA_NW = NW, FA_BQ = 16 * FA_NW;
     constexpr int NT = 64 * FA_NW;
     using T = typename std::conditional<BF16, uint16_t, float>::type;
     constexpr int EPC = 16 / (int)sizeof(T);    // elements per 16-byte chunk
@@ -621,21 +621,27 @@ jas_status jas_attn_prefill(const void *Q, const void *K, const void *V, void *O
     PrefillArgs p{Q, K, V, O, q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, o_sb, o_sh, o_ss, B, H, Sq, Sk,
                   scale * 1.4426950408889634f, causal};
     hipStream_t s = stream_or_default(stream);
-    // grid: one workgroup per (query block, batch x head), padded to a multiple of the 8 XCDs
+    // grid: one workgroup per (query block, batch x head), padded to a multiple of the 8 XCDs.
+    // When 8-wave workgroups (128 queries) would not give every CU one, 4-wave workgroups
+    // (64 queries) double the count -- where a thread's K/V staging stays at four 16-byte
+    // loads per tile (not fp32 with D = 128).
+#define JAS_FA_LAUNCH(DD, BF, NWV)                                                                     \
+    {                                                                                                  \
+        const int total = ceil_div(Sq, 16 * (NWV)) * B * H;                                            \
+        hipLaunchKernelGGL((flash_prefill_kernel<DD, BF, 64, NWV>), dim3((total + 7) / 8 * 8), dim3(64 * (NWV)), 0, s, p); \
+    }
 #define JAS_FA(DD)                                                                                     \
     if (D == DD) {                                                                                     \
+        const bool few = (long)ceil_div(Sq, 16 * FA_WAVES) * B * H < 256;                              \
         if (dtype == JAS_BF16) {                                                                       \
-            constexpr int nw = FA_WAVES;                                                               \
-            const int total = ceil_div(Sq, 16 * nw) * B * H;                                           \
-            hipLaunchKernelGGL((flash_prefill_kernel<DD, true, 64>), dim3((total + 7) / 8 * 8), dim3(64 * nw), 0, s, p); \
+            if (few) JAS_FA_LAUNCH(DD, true, 4) else JAS_FA_LAUNCH(DD, true, FA_WAVES)                 \
         } else {                                                                                       \
-            constexpr int nw = FA_WAVES;                                                               \
-            const int total = ceil_div(Sq, 16 * nw) * B * H;                                           \
-            hipLaunchKernelGGL((flash_prefill_kernel<DD, false, 64>), dim3((total + 7) / 8 * 8), dim3(64 * nw), 0, s, p); \
+            if (few && DD <= 64) JAS_FA_LAUNCH(DD, false, 4) else JAS_FA_LAUNCH(DD, false, FA_WAVES)   \
         }                                                                                              \
     }
     JAS_FA(32) JAS_FA(64) JAS_FA(128)
 #undef JAS_FA
+#undef JAS_FA_LAUNCH
     JAS_LAUNCH_CHECK();
     return JAS_OK;
 }
