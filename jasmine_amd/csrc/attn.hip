@@ -59,6 +59,11 @@ struct PrefillArgs {
     int B, H, Sq, Sk;
     float scale_log2;  // scale * log2(e)
     int causal;
+    // key split (non-causal only): work item `split` attends over keys
+    // [split * kchunk, min(Sk, (split + 1) * kchunk)) and writes its unnormalised output with
+    // its row max and row sum to part[split][b*H + h][q][D + 2]; a merge kernel combines them
+    int nsplit = 1, kchunk = 0;
+    float *part = nullptr;
 };
 
 // waves per workgroup (16 queries each), measured with the heaviest-first work order: 4 or
@@ -80,12 +85,14 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // ones starting late: about 1.4x longer for the causal config-3 shape).  Consecutive ids go
 // round robin to the 8 XCDs, so with B*H a multiple of 8 the query blocks of one head,
 // which share its K/V, stay on one XCD's L2.
-__device__ __forceinline__ bool fa_work_item(int nqb, int BH, int &bh, int &qb)
+__device__ __forceinline__ bool fa_work_item(int nqb, int BH, int nsplit, int &bh, int &qb, int &split)
 {
     const int id = (int)blockIdx.x;
-    if (id >= nqb * BH) return false;
-    qb = nqb - 1 - id / BH;
-    bh = id % BH;
+    if (id >= nqb * BH * nsplit) return false;
+    split = id / (nqb * BH);
+    const int rem = id % (nqb * BH);
+    qb = nqb - 1 - rem / BH;
+    bh = rem % BH;
     return true;
 }
 
@@ -119,9 +126,9 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
 
     const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
-    int bh, qb;
+    int bh, qb, split;
     const int nqb = (p.Sq + FA_BQ - 1) / FA_BQ;
-    if (!fa_work_item(nqb, p.B * p.H, bh, qb)) return;
+    if (!fa_work_item(nqb, p.B * p.H, p.nsplit, bh, qb, split)) return;
     const int b = bh / p.H, h = bh % p.H;
     const int q0 = qb * FA_BQ + w * 16;
     const int qi = q0 + r16;  // this lane's query (column of S^T)
@@ -130,7 +137,9 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
     const long qbase = (long)b * p.q_sb + (long)h * p.q_sh + (long)qq * p.q_ss;
 
     const int q_last = min(qb * FA_BQ + FA_BQ - 1, p.Sq - 1);
-    const int k_end = p.causal ? min(p.Sk, q_last + shift + 1) : p.Sk;
+    // keys of this work item: [k_lo, k_end)
+    const int k_lo = p.nsplit > 1 ? split * p.kchunk : 0;
+    const int k_end = p.nsplit > 1 ? min(p.Sk, k_lo + p.kchunk) : p.causal ? min(p.Sk, q_last + shift + 1) : p.Sk;
     // keys this wave can see at all (causal): [0, wave_kend)
     const int wave_kend = p.causal ? min(p.Sk, min(q0 + 15, p.Sq - 1) + shift + 1) : p.Sk;
     const long kbase = (long)b * p.k_sb + (long)h * p.k_sh;
@@ -199,11 +208,11 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
     // (staged into the other buffer at the top of step t) and tile t+2 is in flight from HBM
     // into the other register set -- loads are issued two tiles ahead of their use.
     // Register set A holds the odd tiles, B the even ones (after tile 0).
-    if (k_end > 0) {
-        FA_GLOAD(0, kra, vra)
+    if (k_end > k_lo) {
+        FA_GLOAD(k_lo, kra, vra)
         FA_LSTORE(0, kra, vra)
-        if (BK < k_end) { FA_GLOAD(BK, kra, vra) }
-        if (2 * BK < k_end) { FA_GLOAD(2 * BK, krb, vrb) }
+        if (k_lo + BK < k_end) { FA_GLOAD(k_lo + BK, kra, vra) }
+        if (k_lo + 2 * BK < k_end) { FA_GLOAD(k_lo + 2 * BK, krb, vrb) }
     }
     __syncthreads();
     auto tile = [&](const int kv0, const int buf) __attribute__((always_inline)) {
@@ -355,7 +364,7 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
         if ((KV0) < wave_kend) tile(KV0, BUF); /* else every key is masked for this wave */  \
         __syncthreads();                                                                     \
     }
-    for (int kv0 = 0; kv0 < k_end; kv0 += 2 * BK) {
+    for (int kv0 = k_lo; kv0 < k_end; kv0 += 2 * BK) {
         FA_STEP(kv0, 0, kra, vra)
         if (kv0 + BK >= k_end) break;
         FA_STEP(kv0 + BK, 1, krb, vrb)
@@ -364,6 +373,23 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
     float l_run = l_part + __shfl_xor(l_part, 16, WAVE);
     l_run += __shfl_xor(l_run, 32, WAVE);
 
+    if (p.nsplit > 1) {  // unnormalised partial: O, then the row max (raw units) and row sum
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float lr = BF16 ? lacc[r] : __shfl(l_run, 4 * g + r, WAVE);
+            const float mr = __shfl(m_run, 4 * g + r, WAVE);
+            const int qo = q0 + 4 * g + r;
+            if (qo >= p.Sq) continue;
+            float *row = p.part + (((long)split * p.B * p.H + bh) * p.Sq + qo) * (D + 2);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) row[16 * c + r16] = oacc[c][r];
+            if (r16 == 0) {
+                row[D] = mr;
+                row[D + 1] = lr;
+            }
+        }
+        return;
+    }
     // lane holds O[query = q0 + 4g + r][d = 16c + r16]; 1/l of query 4g + r from lane 4g + r
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -383,6 +409,37 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
     }
 #undef FA_GLOAD
 #undef FA_LSTORE
+}
+
+// Combines the key-split partials of a prefill launch: one thread per (row, head-dim
+// element); O = sum_i 2^((m_i - M) s) O_i / sum_i 2^((m_i - M) s) l_i with M = max_i m_i.
+template <bool BF16>
+__global__ void __launch_bounds__(256) flash_merge_kernel(const PrefillArgs p, int D)
+{
+    const long g = (long)blockIdx.x * 256 + threadIdx.x;
+    const long rows = (long)p.B * p.H * p.Sq;
+    if (g >= rows * D) return;
+    const long row = g / D;
+    const int e = (int)(g % D);
+    const int bh = (int)(row / p.Sq), q = (int)(row % p.Sq);
+    const long sstride = rows * (D + 2);
+    const float *pr = p.part + row * (D + 2);
+    float mx = -INFINITY;
+    for (int i = 0; i < p.nsplit; ++i) mx = fmaxf(mx, pr[i * sstride + D]);
+    float o = 0.f, l = 0.f;
+    for (int i = 0; i < p.nsplit; ++i) {
+        const float mi = pr[i * sstride + D];
+        const float w = mi == -INFINITY ? 0.f : exp2_fast((mi - mx) * p.scale_log2);
+        o += w * pr[i * sstride + e];
+        l += w * pr[i * sstride + D + 1];
+    }
+    const float v = l > 0.f ? o / l : 0.f;
+    const int b = bh / p.H, h = bh % p.H;
+    const long oi = (long)b * p.o_sb + (long)h * p.o_sh + (long)q * p.o_ss + e;
+    if constexpr (BF16)
+        ((uint16_t *)p.O)[oi] = __builtin_bit_cast(uint16_t, (__bf16)v);
+    else
+        ((float *)p.O)[oi] = v;
 }
 
 // ---------------------------------------------------------------- decode
@@ -624,24 +681,43 @@ jas_status jas_attn_prefill(const void *Q, const void *K, const void *V, void *O
     // grid: one workgroup per (query block, batch x head), padded to a multiple of the 8 XCDs.
     // When 8-wave workgroups (128 queries) would not give every CU one, 4-wave workgroups
     // (64 queries) double the count -- where a thread's K/V staging stays at four 16-byte
-    // loads per tile (not fp32 with D = 128).
+    // loads per tile (not fp32 with D = 128).  A non-causal launch that still leaves CUs
+    // idle also splits its keys over up to 4 work items (at least two 64-key tiles each),
+    // merged by a second kernel.
+    const bool few = (long)ceil_div(Sq, 16 * FA_WAVES) * B * H < 256;
+    const int nw = few && (dtype == JAS_BF16 || D <= 64) ? 4 : FA_WAVES;
+    const long items = (long)ceil_div(Sq, 16 * nw) * B * H;
+    if (!causal && items < 256 && Sk >= 4 * 64) {
+        int ns = (int)std::min<long>(4, (512 + items - 1) / items);
+        ns = std::min(ns, Sk / 128);
+        if (ns > 1) {
+            p.kchunk = ceil_div(ceil_div(Sk, ns), 64) * 64;
+            p.nsplit = ceil_div(Sk, p.kchunk);
+            p.part = (float *)workspace(sizeof(float) * (size_t)p.nsplit * B * H * Sq * (D + 2), s);
+            JAS_CHECK(p.part, JAS_ERR_OOM, "jas_attn_prefill: workspace allocation failed");
+        }
+    }
 #define JAS_FA_LAUNCH(DD, BF, NWV)                                                                     \
     {                                                                                                  \
-        const int total = ceil_div(Sq, 16 * (NWV)) * B * H;                                            \
+        const int total = ceil_div(Sq, 16 * (NWV)) * B * H * p.nsplit;                                 \
         hipLaunchKernelGGL((flash_prefill_kernel<DD, BF, 64, NWV>), dim3((total + 7) / 8 * 8), dim3(64 * (NWV)), 0, s, p); \
     }
 #define JAS_FA(DD)                                                                                     \
     if (D == DD) {                                                                                     \
-        const bool few = (long)ceil_div(Sq, 16 * FA_WAVES) * B * H < 256;                              \
         if (dtype == JAS_BF16) {                                                                       \
-            if (few) JAS_FA_LAUNCH(DD, true, 4) else JAS_FA_LAUNCH(DD, true, FA_WAVES)                 \
+            if (nw == 4) JAS_FA_LAUNCH(DD, true, 4) else JAS_FA_LAUNCH(DD, true, FA_WAVES)             \
         } else {                                                                                       \
-            if (few && DD <= 64) JAS_FA_LAUNCH(DD, false, 4) else JAS_FA_LAUNCH(DD, false, FA_WAVES)   \
+            if (nw == 4 && DD <= 64) JAS_FA_LAUNCH(DD, false, 4) else JAS_FA_LAUNCH(DD, false, FA_WAVES) \
         }                                                                                              \
     }
     JAS_FA(32) JAS_FA(64) JAS_FA(128)
 #undef JAS_FA
 #undef JAS_FA_LAUNCH
+    if (p.nsplit > 1) {
+        const long n = (long)B * H * Sq * D;
+        if (dtype == JAS_BF16) hipLaunchKernelGGL(flash_merge_kernel<true>, dim3(ceil_div(n, 256)), dim3(256), 0, s, p, D);
+        else hipLaunchKernelGGL(flash_merge_kernel<false>, dim3(ceil_div(n, 256)), dim3(256), 0, s, p, D);
+    }
     JAS_LAUNCH_CHECK();
     return JAS_OK;
 }

@@ -319,7 +319,11 @@ def test_gemm_skinny(jas, M, N, K):
 
 # ---------------------------------------------------------------- attention
 @pytest.mark.parametrize("B,H,Sq,Sk,D,causal", [(2, 3, 100, 100, 64, 1), (1, 2, 64, 64, 32, 0), (2, 2, 70, 130, 128, 1),
-                                                (1, 4, 200, 200, 128, 1), (1, 1, 1, 1, 64, 1), (2, 2, 37, 90, 64, 0)])
+                                                (1, 4, 200, 200, 128, 1), (1, 1, 1, 1, 64, 1), (2, 2, 37, 90, 64, 0),
+                                                # non-causal with few query blocks: keys split over
+                                                # work items and merged (ragged last split included)
+                                                (1, 2, 100, 700, 64, 0), (2, 3, 130, 1000, 32, 0),
+                                                (1, 1, 50, 513, 128, 0), (1, 2, 1, 300, 64, 0)])
 def test_attn_prefill(jas, B, H, Sq, Sk, D, causal):
     Q, K, V = normal((B, H, Sq, D), 30, 0), normal((B, H, Sk, D), 30, 1), normal((B, H, Sk, D), 30, 2)
     want = np.zeros((B, H, Sq, D), np.float32)
@@ -332,7 +336,8 @@ def test_attn_prefill(jas, B, H, Sq, Sk, D, causal):
 
 
 @pytest.mark.parametrize("B,H,Sq,Sk,D,causal", [(2, 2, 96, 96, 64, 1), (1, 3, 70, 130, 128, 1), (2, 1, 64, 64, 32, 0),
-                                                (1, 2, 200, 200, 128, 0), (1, 1, 1, 17, 64, 1)])
+                                                (1, 2, 200, 200, 128, 0), (1, 1, 1, 17, 64, 1),
+                                                (1, 2, 77, 600, 128, 0), (2, 2, 64, 1024, 64, 0)])
 def test_attn_prefill_bf16(jas, B, H, Sq, Sk, D, causal):
     """bf16 inputs on bf16 MFMA with fp32 accumulation and softmax; P is rounded to bf16 for
     the P.V product.  Held to 2e-2 abs + 2e-2 rel against the fp32 attention of the same
