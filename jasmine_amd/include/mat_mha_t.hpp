@@ -308,8 +308,10 @@ private:
             m_fx.qkv.allocate(sizeof(float) * (size_t)Tq * d);
             float *q = (float *)m_fx.qkv.get();
             project(0, xq, Tq, q, d);
-            const uint64_t es = encoder_input->stamp();
-            if (m_fx.kv_stamp != es || m_fx.kv_T != Tk) {
+            // matrices carry a content stamp; other input types recompute every call
+            uint64_t es = 0;
+            if constexpr (requires { encoder_input->stamp(); }) es = encoder_input->stamp();
+            if (es == 0 || m_fx.kv_stamp != es || m_fx.kv_T != Tk) {
                 auto xe = jas::gemm_operand<float>(*encoder_input);
                 m_fx.kv.allocate(sizeof(float) * (size_t)Tk * 2 * d);
                 float *kv = (float *)m_fx.kv.get();
