@@ -139,8 +139,9 @@ template <int AM, int BMODE, bool C4, int T = TBM>
 __global__ void __launch_bounds__(256) gemm_tile_kernel(const TileArgs p)
 {
     constexpr int NB = T / 32;
-    __shared__ float As[T * TLD];
-    __shared__ float Bs[T * TLD];
+    // two LDS buffers: slab k is read from one while slab k+1 is written to the other
+    __shared__ float As[2][T * TLD];
+    __shared__ float Bs[2][T * TLD];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wm = w >> 1, wn = w & 1, r16 = lane & 15, g = lane >> 4;
     const int m0 = blockIdx.y * T, n0 = blockIdx.x * T;
@@ -155,6 +156,13 @@ __global__ void __launch_bounds__(256) gemm_tile_kernel(const TileArgs p)
     // A(m, k) = A[m*as0 + k*as1]: outer = m.  B(k, n) = B[k*bs0 + n*bs1]: outer = n.
     la.load(A, p.as0, p.as1, m0, 0, p.M, p.K, tid);
     lb.load(B, p.bs1, p.bs0, n0, 0, p.N, p.K, tid);
+    la.store(As[0], tid);
+    lb.store(Bs[0], tid);
+    if (TBK < p.K) {  // slab 1 in flight
+        la.load(A, p.as0, p.as1, m0, TBK, p.M, p.K, tid);
+        lb.load(B, p.bs1, p.bs0, n0, TBK, p.N, p.K, tid);
+    }
+    __syncthreads();
 
     floatx4 acc[NB][NB];
 #pragma unroll
@@ -162,20 +170,24 @@ __global__ void __launch_bounds__(256) gemm_tile_kernel(const TileArgs p)
 #pragma unroll
         for (int j = 0; j < NB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+    int buf = 0;
     for (int k0 = 0; k0 < p.K; k0 += TBK) {
-        __syncthreads();
-        la.store(As, tid);
-        lb.store(Bs, tid);
-        __syncthreads();
-        if (k0 + TBK < p.K) {  // prefetch the next K slab while the matrix cores work
-            la.load(A, p.as0, p.as1, m0, k0 + TBK, p.M, p.K, tid);
-            lb.load(B, p.bs1, p.bs0, n0, k0 + TBK, p.N, p.K, tid);
+        // stage slab k+1 (in registers) into the other buffer, then start slab k+2's loads;
+        // the other buffer was last read in the previous step, before its closing barrier
+        if (k0 + TBK < p.K) {
+            la.store(As[buf ^ 1], tid);
+            lb.store(Bs[buf ^ 1], tid);
+            if (k0 + 2 * TBK < p.K) {
+                la.load(A, p.as0, p.as1, m0, k0 + 2 * TBK, p.M, p.K, tid);
+                lb.load(B, p.bs1, p.bs0, n0, k0 + 2 * TBK, p.N, p.K, tid);
+            }
         }
+        const float *as = As[buf], *bs = Bs[buf];
         float4 a[NB], b[NB];
 #pragma unroll
-        for (int i = 0; i < NB; ++i) a[i] = *(const float4 *)(As + (wm * (T / 2) + i * 16 + r16) * TLD + 4 * g);
+        for (int i = 0; i < NB; ++i) a[i] = *(const float4 *)(as + (wm * (T / 2) + i * 16 + r16) * TLD + 4 * g);
 #pragma unroll
-        for (int j = 0; j < NB; ++j) b[j] = *(const float4 *)(Bs + (wn * (T / 2) + j * 16 + r16) * TLD + 4 * g);
+        for (int j = 0; j < NB; ++j) b[j] = *(const float4 *)(bs + (wn * (T / 2) + j * 16 + r16) * TLD + 4 * g);
 #pragma unroll
         for (int i = 0; i < NB; ++i)
 #pragma unroll
@@ -185,6 +197,8 @@ __global__ void __launch_bounds__(256) gemm_tile_kernel(const TileArgs p)
                 acc[i][j] = mfma4(a[i].z, b[j].z, acc[i][j]);
                 acc[i][j] = mfma4(a[i].w, b[j].w, acc[i][j]);
             }
+        __syncthreads();
+        buf ^= 1;
     }
 
     // epilogue: lane holds rows m = 4g + r of each 16x16 block, column n = r16
