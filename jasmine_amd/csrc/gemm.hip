@@ -37,12 +37,15 @@ constexpr int TBM = 128, TBN = 128, TBK = 16, TLD = 20;  // LDS row stride (floa
 enum LoadMode : int { LM_KC = 0, LM_OC = 1, LM_GEN = 2, LM_PK = 3, LM_PKB = 4 };
 
 
-// Loads an [OUTER (128 or 64) outer x 16 k] tile of X(o, k) = X[o*so + k*sk] into
-// registers (256 threads), then LDS rows [o][k] (K-contiguous, padded stride TLD).
-template <int MODE, int OUTER = 128>
+// Loads an [OUTER (128 or 64) outer x KW (16 or 32) k] tile of X(o, k) = X[o*so + k*sk]
+// into registers (256 threads), then LDS rows [o][k] (K-contiguous, padded stride KW + 4).
+// The packed layouts are read in 16-wide K blocks only.
+template <int MODE, int OUTER = 128, int KW = 16>
 struct TileLoader {
-    static constexpr int NV = OUTER / 64;  // float4 loads per thread (vector modes)
-    static constexpr int NS = OUTER / 16;  // scalar loads per thread (generic mode)
+    static_assert(KW == 16 || (MODE != LM_PK && MODE != LM_PKB), "packed operands use 16-wide K slabs");
+    static constexpr int LD = KW + 4;              // LDS row stride (floats)
+    static constexpr int NV = OUTER * KW / 1024;   // float4 loads per thread (vector modes)
+    static constexpr int NS = OUTER * KW / 256;    // scalar loads per thread (generic mode)
     float r[NS];
     __device__ __forceinline__ void load(const float *__restrict__ X, long so, long sk, int o0, int k0, int O, int K,
                                          int tid)
@@ -50,7 +53,7 @@ struct TileLoader {
         if (MODE == LM_KC) {
 #pragma unroll
             for (int q = 0; q < NV; ++q) {
-                int idx = tid + q * 256, o = idx >> 2, kq = (idx & 3) * 4;
+                int idx = tid + q * 256, o = idx / (KW / 4), kq = (idx % (KW / 4)) * 4;
                 int go = o0 + o, gk = k0 + kq;
                 float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (go < O && gk < K) v = *(const float4 *)(X + (long)go * so + gk);
@@ -85,7 +88,7 @@ struct TileLoader {
         } else {
 #pragma unroll
             for (int q = 0; q < NS; ++q) {
-                int idx = tid + q * 256, o = idx >> 4, k = idx & 15;
+                int idx = tid + q * 256, o = idx / KW, k = idx % KW;
                 int go = o0 + o, gk = k0 + k;
                 r[q] = (go < O && gk < K) ? X[(long)go * so + (long)gk * sk] : 0.f;
             }
@@ -96,14 +99,14 @@ struct TileLoader {
         if (MODE == LM_KC) {
 #pragma unroll
             for (int q = 0; q < NV; ++q) {
-                int idx = tid + q * 256, o = idx >> 2, kq = (idx & 3) * 4;
-                *(float4 *)(lds + o * TLD + kq) = make_float4(r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]);
+                int idx = tid + q * 256, o = idx / (KW / 4), kq = (idx % (KW / 4)) * 4;
+                *(float4 *)(lds + o * LD + kq) = make_float4(r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]);
             }
         } else if (MODE == LM_PK || MODE == LM_PKB) {
 #pragma unroll
             for (int q = 0; q < NV; ++q) {
                 int idx = tid + q * 256, i = idx >> 6, ln = idx & 63;
-                *(float4 *)(lds + (i * 16 + (ln & 15)) * TLD + 4 * (ln >> 4)) =
+                *(float4 *)(lds + (i * 16 + (ln & 15)) * LD + 4 * (ln >> 4)) =
                     make_float4(r[4 * q], r[4 * q + 1], r[4 * q + 2], r[4 * q + 3]);
             }
         } else if (MODE == LM_OC) {
@@ -111,13 +114,13 @@ struct TileLoader {
             for (int q = 0; q < NV; ++q) {
                 int idx = tid + q * 256, k = idx / (OUTER / 4), oq = (idx % (OUTER / 4)) * 4;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) lds[(oq + e) * TLD + k] = r[4 * q + e];
+                for (int e = 0; e < 4; ++e) lds[(oq + e) * LD + k] = r[4 * q + e];
             }
         } else {
 #pragma unroll
             for (int q = 0; q < NS; ++q) {
-                int idx = tid + q * 256, o = idx >> 4, k = idx & 15;
-                lds[o * TLD + k] = r[q];
+                int idx = tid + q * 256, o = idx / KW, k = idx % KW;
+                lds[o * LD + k] = r[q];
             }
         }
     }
@@ -135,13 +138,13 @@ struct TileArgs {
 
 // T x T output tile (T = 128, or 64 for problems too small to fill the chip with 128-wide
 // tiles); 4 waves in a 2 x 2 grid, each T/2 x T/2 (NB x NB blocks of 16 x 16)
-template <int AM, int BMODE, bool C4, int T = TBM>
+template <int AM, int BMODE, bool C4, int T = TBM, int KW = TBK>
 __global__ void __launch_bounds__(256) gemm_tile_kernel(const TileArgs p)
 {
-    constexpr int NB = T / 32;
+    constexpr int NB = T / 32, LD = KW + 4;
     // two LDS buffers: slab k is read from one while slab k+1 is written to the other
-    __shared__ float As[2][T * TLD];
-    __shared__ float Bs[2][T * TLD];
+    __shared__ float As[2][T * LD];
+    __shared__ float Bs[2][T * LD];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int wm = w >> 1, wn = w & 1, r16 = lane & 15, g = lane >> 4;
     const int m0 = blockIdx.y * T, n0 = blockIdx.x * T;
@@ -151,16 +154,16 @@ __global__ void __launch_bounds__(256) gemm_tile_kernel(const TileArgs p)
     float *C = p.C + bz * p.cbs;
     const float *bias = p.bias ? p.bias + bz * p.biasbs : nullptr;
 
-    TileLoader<AM, T> la;
-    TileLoader<BMODE, T> lb;
+    TileLoader<AM, T, KW> la;
+    TileLoader<BMODE, T, KW> lb;
     // A(m, k) = A[m*as0 + k*as1]: outer = m.  B(k, n) = B[k*bs0 + n*bs1]: outer = n.
     la.load(A, p.as0, p.as1, m0, 0, p.M, p.K, tid);
     lb.load(B, p.bs1, p.bs0, n0, 0, p.N, p.K, tid);
     la.store(As[0], tid);
     lb.store(Bs[0], tid);
-    if (TBK < p.K) {  // slab 1 in flight
-        la.load(A, p.as0, p.as1, m0, TBK, p.M, p.K, tid);
-        lb.load(B, p.bs1, p.bs0, n0, TBK, p.N, p.K, tid);
+    if (KW < p.K) {  // slab 1 in flight
+        la.load(A, p.as0, p.as1, m0, KW, p.M, p.K, tid);
+        lb.load(B, p.bs1, p.bs0, n0, KW, p.N, p.K, tid);
     }
     __syncthreads();
 
@@ -171,32 +174,37 @@ __global__ void __launch_bounds__(256) gemm_tile_kernel(const TileArgs p)
         for (int j = 0; j < NB; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     int buf = 0;
-    for (int k0 = 0; k0 < p.K; k0 += TBK) {
+    for (int k0 = 0; k0 < p.K; k0 += KW) {
         // stage slab k+1 (in registers) into the other buffer, then start slab k+2's loads;
         // the other buffer was last read in the previous step, before its closing barrier
-        if (k0 + TBK < p.K) {
+        if (k0 + KW < p.K) {
             la.store(As[buf ^ 1], tid);
             lb.store(Bs[buf ^ 1], tid);
-            if (k0 + 2 * TBK < p.K) {
-                la.load(A, p.as0, p.as1, m0, k0 + 2 * TBK, p.M, p.K, tid);
-                lb.load(B, p.bs1, p.bs0, n0, k0 + 2 * TBK, p.N, p.K, tid);
+            if (k0 + 2 * KW < p.K) {
+                la.load(A, p.as0, p.as1, m0, k0 + 2 * KW, p.M, p.K, tid);
+                lb.load(B, p.bs1, p.bs0, n0, k0 + 2 * KW, p.N, p.K, tid);
             }
         }
         const float *as = As[buf], *bs = Bs[buf];
-        float4 a[NB], b[NB];
 #pragma unroll
-        for (int i = 0; i < NB; ++i) a[i] = *(const float4 *)(as + (wm * (T / 2) + i * 16 + r16) * TLD + 4 * g);
+        for (int kh = 0; kh < KW / 16; ++kh) {  // 16-wide K blocks of the slab
+            float4 a[NB], b[NB];
 #pragma unroll
-        for (int j = 0; j < NB; ++j) b[j] = *(const float4 *)(bs + (wn * (T / 2) + j * 16 + r16) * TLD + 4 * g);
+            for (int i = 0; i < NB; ++i)
+                a[i] = *(const float4 *)(as + (wm * (T / 2) + i * 16 + r16) * LD + 16 * kh + 4 * g);
 #pragma unroll
-        for (int i = 0; i < NB; ++i)
+            for (int j = 0; j < NB; ++j)
+                b[j] = *(const float4 *)(bs + (wn * (T / 2) + j * 16 + r16) * LD + 16 * kh + 4 * g);
 #pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                acc[i][j] = mfma4(a[i].x, b[j].x, acc[i][j]);
-                acc[i][j] = mfma4(a[i].y, b[j].y, acc[i][j]);
-                acc[i][j] = mfma4(a[i].z, b[j].z, acc[i][j]);
-                acc[i][j] = mfma4(a[i].w, b[j].w, acc[i][j]);
-            }
+            for (int i = 0; i < NB; ++i)
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    acc[i][j] = mfma4(a[i].x, b[j].x, acc[i][j]);
+                    acc[i][j] = mfma4(a[i].y, b[j].y, acc[i][j]);
+                    acc[i][j] = mfma4(a[i].z, b[j].z, acc[i][j]);
+                    acc[i][j] = mfma4(a[i].w, b[j].w, acc[i][j]);
+                }
+        }
         __syncthreads();
         buf ^= 1;
     }
@@ -235,17 +243,21 @@ __global__ void __launch_bounds__(256) gemm_tile_kernel(const TileArgs p)
         }
 }
 
+// 64-wide tiles of plain operands take K slabs of 32 (128-byte row segments, half the
+// barriers per flop); 128-wide tiles keep 16 (32-wide slabs need 72 KB of LDS there and
+// lose occupancy), as do packed weights
 template <int AM, int BMODE>
 static void launch_tile_c(const TileArgs &p, bool c4, bool small, int batch, hipStream_t s)
 {
+    constexpr int KW = (AM == LM_PK || AM == LM_PKB) ? 16 : 32;
     if (small) {
         const dim3 grid(ceil_div(p.N, 64), ceil_div(p.M, 64), batch);
-        if (c4) hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, true, 64>), grid, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, false, 64>), grid, dim3(256), 0, s, p);
+        if (c4) hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, true, 64, KW>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, false, 64, KW>), grid, dim3(256), 0, s, p);
     } else {
         const dim3 grid(ceil_div(p.N, TBN), ceil_div(p.M, TBM), batch);
-        if (c4) hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, true>), grid, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, false>), grid, dim3(256), 0, s, p);
+        if (c4) hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, true, TBM, TBK>), grid, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL((gemm_tile_kernel<AM, BMODE, false, TBM, TBK>), grid, dim3(256), 0, s, p);
     }
 }
 
