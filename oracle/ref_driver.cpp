@@ -232,6 +232,28 @@ void ref_transformer(const float *en, int Te, const float *de, int Td, int d, in
     from_mat(tf.forward(to_mat(de, d, Td)), Y);
 }
 
+// the decode loop of test_transformer_t::predict (transformer_test.hpp:227-239) without the
+// harness's SOS/EOS flag rows: column 0 of the decoder input is given; each step runs
+// forward on the prefix view [0, len) and appends the output's last column.  Y receives the
+// d x (steps + 1) sequence.
+void ref_predict_loop(const float *en, int Te, const float *de0, int d, int H, int n_enc, int n_dec,
+                      const float *W, int steps, float *Y)
+{
+    transformer_base_t<mat_t<float>, upd_t> tf(n_enc, n_dec, H, d);
+    g_fixture = W; g_fixture_pos = 0;
+    tf.init_weight<fixture_init_t>();
+    tf.encoder_forward(to_mat(en, d, Te));
+    mat_t<float> seq(d, steps + 1);
+    for (int i = 0; i < d; ++i) seq(i, 0) = de0[i];
+    int len = 1;
+    for (int s = 0; s < steps; ++s) {
+        auto cur = seq.view(0, 0, d, len);
+        auto out = tf.forward(cur);
+        seq.col(len++).assign(out.back_col());
+    }
+    from_mat(seq, Y);
+}
+
 // number of parameters transformer_base_t::init_weight visits (for buffer sizing)
 long ref_transformer_nparams(int d, int H, int n_enc, int n_dec)
 {

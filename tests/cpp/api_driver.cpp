@@ -313,6 +313,29 @@ int api_transformer_bench(int d, int H, int n_enc, int n_dec, int Te, int Td, in
     });
 }
 
+// the prefix-recompute decode loop of test_transformer_t::predict (transformer_test.hpp:
+// 227-239) without the harness's flag rows, written as jasmine user code
+int api_predict_loop(const float *en, int Te, const float *de0, int d, int H, int n_enc, int n_dec, const float *W,
+                     int steps, float *Y)
+{
+    return guarded([&] {
+        transformer_base_t<mat_t<float>, upd_t> tf(n_enc, n_dec, H, d);
+        g_fixture = W;
+        g_fixture_pos = 0;
+        tf.init_weight<api_fixture_init_t>();
+        tf.encoder_forward(to_mat(en, d, Te));
+        mat_t<float> seq(d, steps + 1);
+        for (int i = 0; i < d; ++i) seq(i, 0) = de0[i];
+        int len = 1;
+        for (int s = 0; s < steps; ++s) {
+            auto cur = seq.view(0, 0, d, len);
+            auto out = tf.forward(cur);
+            seq.col(len++).assign(out.back_col());
+        }
+        from_mat(seq, Y);
+    });
+}
+
 // 1: mat_mha_t runs every head through the fused path where it applies (the default);
 // 0: the per-head path with materialised scores
 int api_set_fused_heads(int on)

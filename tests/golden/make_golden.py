@@ -134,6 +134,17 @@ def main():
     g.update(tf32_w=W3, tf32_en=en3, tf32_de=de3, tf32_y=Y3, tf32_prefix5=Y3p,
              tf32_dims=np.array([d3, H3, ne3, nd3, Te3, Td3]))
 
+    # the prefix-recompute decode loop (transformer_test.hpp:227-239): per-head path (d_h 4)
+    # and the fused path (d_h 32), 6 steps each
+    for tag, (dp, Hp, nep, ndp, Tep, seed) in {"pred4": (12, 3, 2, 2, 5, 84), "pred32": (64, 2, 1, 2, 9, 88)}.items():
+        Wp = normal(ref.ref_transformer_nparams(dp, Hp, nep, ndp), 1, seed, std=0.1)
+        enp, dep = normal((dp, Tep), 1, seed + 1), normal(dp, 1, seed + 2)
+        steps = 6
+        Yp = np.zeros((dp, steps + 1), np.float32)
+        ref.ref_predict_loop(fp(enp), Tep, fp(dep), dp, Hp, nep, ndp, fp(Wp), steps, fp(Yp))
+        g.update({f"{tag}_w": Wp, f"{tag}_en": enp, f"{tag}_de0": dep, f"{tag}_y": Yp,
+                  f"{tag}_dims": np.array([dp, Hp, nep, ndp, Tep, steps])})
+
     np.savez_compressed(OUT, **g)
     print("wrote", OUT, os.path.getsize(OUT), "bytes,", len(g), "arrays")
 

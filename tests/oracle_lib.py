@@ -111,6 +111,7 @@ if ref is not None:
     ref.ref_mha.argtypes = [FP, FP, C.c_int, C.c_int, C.c_int, C.c_int, FP, C.c_int, FP]
     ref.ref_rope.argtypes = [FP, C.c_int, C.c_int, FP]
     ref.ref_transformer.argtypes = [FP, C.c_int, FP, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, FP, FP]
+    ref.ref_predict_loop.argtypes = [FP, C.c_int, FP, C.c_int, C.c_int, C.c_int, C.c_int, FP, C.c_int, FP]
     ref.ref_transformer_nparams.restype = C.c_long
     ref.ref_transformer_nparams.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int]
     for n, k in (("ref_time_linear", 4), ("ref_time_cfg2", 3), ("ref_time_hsoftmax", 3), ("ref_time_head", 3)):

@@ -62,7 +62,7 @@ def bitexact(a, b):
 def test_api_library_exports(api):
     for name in ("api_gemm", "api_gemm_tn", "api_cfg2_expr", "api_expr", "api_hsoftmax", "api_softmax_global",
                  "api_reductions", "api_linear", "api_relu", "api_sigmoid", "api_layernorm_cols", "api_head",
-                 "api_mha", "api_rope", "api_transformer", "api_transformer_nparams", "api_last_error", "api_set_fused_heads", "api_transformer_reencode"):
+                 "api_mha", "api_rope", "api_transformer", "api_transformer_nparams", "api_last_error", "api_set_fused_heads", "api_transformer_reencode", "api_predict_loop"):
         assert hasattr(api, name), name
 
 
@@ -256,3 +256,16 @@ def test_api_transformer_reencode(api, g):
     close(Y1, g["tf32_y"])
     close(Y2, g["tf32_y2"])
     assert np.array_equal(Y2, Y3)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tag", ["pred4", "pred32"])
+def test_api_predict_loop(api, g, tag):
+    """The reference's autoregressive loop (test_transformer_t::predict without its flag
+    rows): decoder forward on a growing prefix view, last output column appended, 6 steps.
+    d_h 4 runs the per-head path, d_h 32 the fused one."""
+    d, H, ne, nd, Te, steps = (int(v) for v in g[f"{tag}_dims"])
+    Y = np.zeros((d, steps + 1), np.float32)
+    ok(api, api.api_predict_loop(fp(g[f"{tag}_en"]), Te, fp(g[f"{tag}_de0"]), d, H, ne, nd, fp(g[f"{tag}_w"]), steps,
+                                 fp(Y)))
+    close(Y, g[f"{tag}_y"])
