@@ -30,7 +30,7 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c)
 }
 
 // ---------------------------------------------------------------- tiled GEMM
-constexpr int TBM = 128, TBN = 128, TBK = 16, TLD = 20;  // LDS row stride (floats)
+constexpr int TBM = 128, TBN = 128, TBK = 16;  // output tile edge, K slab width
 
 // K-contiguous, outer-contiguous, generic strides, packed weights (weight_pack_offset)
 // and the packed layout with bf16 elements (widened on load)
