@@ -537,23 +537,43 @@ __global__ void __launch_bounds__(WPB * 64) attn_decode_kernel(const DecodeArgs 
         }
         m = mx;
     }
-    // merge the key groups of this workgroup
+    // merge the key groups of this workgroup: wave 0 finds the common max and each group's
+    // weight (one group per lane, shuffle reductions); then every thread sums the weighted
+    // accumulators of a slice of the groups for one output element, and the slices are added
     if (lig == 0) { sm[grp] = m; sl[grp] = l; }
 #pragma unroll
     for (int e = 0; e < EPL; e += 4)
         *(float4 *)(&sacc[grp][EPL * lig + e]) = make_float4(acc[e], acc[e + 1], acc[e + 2], acc[e + 3]);
     __syncthreads();
+    static_assert(NG <= WAVE, "one key group per lane of wave 0");
+    __shared__ float sf[NG], sML[2];
+    if (w == 0) {
+        const float mg = lane < NG ? sm[lane] : -FLT_MAX;
+        float M = mg;
+#pragma unroll
+        for (int o = WAVE / 2; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, WAVE));
+        const float f = (lane < NG && mg != -FLT_MAX) ? exp2f(mg - M) : 0.f;
+        float L = lane < NG ? sl[lane] * f : 0.f;
+#pragma unroll
+        for (int o = WAVE / 2; o > 0; o >>= 1) L += __shfl_xor(L, o, WAVE);
+        if (lane < NG) sf[lane] = f;
+        if (lane == 0) { sML[0] = M; sML[1] = L; }
+    }
+    __syncthreads();
+    constexpr int NT = WPB * 64, SL = NT / D < NG ? NT / D : NG;  // slices of the groups
+    __shared__ float spart[SL][D];
+    if (tid < SL * D) {
+        const int sl_i = tid / D, e = tid % D;
+        float a = 0.f;
+        for (int k = sl_i; k < NG; k += SL) a += sacc[k][e] * sf[k];
+        spart[sl_i][e] = a;
+    }
+    __syncthreads();
     if (tid < D) {
-        float M = -FLT_MAX;
+        const float M = sML[0], L = sML[1];
+        float A = 0.f;
 #pragma unroll
-        for (int k = 0; k < NG; ++k) M = fmaxf(M, sm[k]);
-        float L = 0.f, A = 0.f;
-#pragma unroll
-        for (int k = 0; k < NG; ++k) {
-            float f = sm[k] == -FLT_MAX ? 0.f : exp2f(sm[k] - M);
-            L += sl[k] * f;
-            A += sacc[k][tid] * f;
-        }
+        for (int k = 0; k < SL; ++k) A += spart[k][tid];
         if (p.nsplit == 1) {
             p.O[decode_out_index(p, bh, D, tid)] = L > 0.f ? A / L : 0.f;
         } else {
