@@ -372,6 +372,7 @@ static jas_status reduce_t(const jas_leaf *in, int op, int axis, void *d_out, hi
 // x[n] += (sum_s part[s][n] + bias); y[n] = norm(x[n]) * g (+ b).  `part` holds the K-split
 // partial sums of the projection that feeds the residual stream ([split][16][d], split
 // order), so the split-K reduction costs no launch of its own.  One workgroup per token.
+constexpr int RN_MAX_SPLITS = 8;  // the decode projections split K at most 8 ways
 template <int PER, bool RMS>
 __global__ void __launch_bounds__(256)
 resid_norm_kernel(float *__restrict__ x, const float *__restrict__ part, int ks, const float *__restrict__ bias,
@@ -389,11 +390,16 @@ resid_norm_kernel(float *__restrict__ x, const float *__restrict__ part, int ks,
         if (e < d) {
             a = *(const float4 *)(xr + e);
             if (ks > 0) {
-                float4 sacc = *(const float4 *)(part + (long)n * d + e);
-                for (int sp = 1; sp < ks; ++sp) {
-                    float4 q = *(const float4 *)(part + ((long)sp * 16 + n) * d + e);
-                    sacc.x += q.x; sacc.y += q.y; sacc.z += q.z; sacc.w += q.w;
-                }
+                // every split's partial is requested before the first is added (one round
+                // trip, not ks); the sum keeps split order
+                float4 q[RN_MAX_SPLITS];
+#pragma unroll
+                for (int sp = 0; sp < RN_MAX_SPLITS; ++sp)
+                    if (sp < ks) q[sp] = *(const float4 *)(part + ((long)sp * 16 + n) * d + e);
+                float4 sacc = q[0];
+#pragma unroll
+                for (int sp = 1; sp < RN_MAX_SPLITS; ++sp)
+                    if (sp < ks) { sacc.x += q[sp].x; sacc.y += q[sp].y; sacc.z += q[sp].z; sacc.w += q[sp].w; }
                 if (bias) {
                     float4 bb = *(const float4 *)(bias + e);
                     sacc.x += bb.x; sacc.y += bb.y; sacc.z += bb.z; sacc.w += bb.w;
@@ -442,6 +448,7 @@ jas_status resid_norm(float *x, const float *part, int ks, const float *bias, co
                       int N, int d, float eps, bool rms, hipStream_t s, bool y_packed)
 {
     JAS_CHECK(d % 4 == 0 && d <= 8192 && N >= 1 && N <= 16 && g, JAS_ERR_INVALID, "resid_norm: unsupported shape");
+    JAS_CHECK(ks <= RN_MAX_SPLITS, JAS_ERR_INVALID, "resid_norm: more K splits than supported");
     JAS_CHECK(!y_packed || d % 16 == 0, JAS_ERR_INVALID, "resid_norm: packed output needs d % 16 == 0");
     const int yp = y_packed ? 1 : 0;
 #define JAS_RN(PER)                                                                                              \
