@@ -548,8 +548,14 @@ skinny_kernel(const void *__restrict__ W, const void *__restrict__ W2, const flo
 #pragma unroll
                 for (int pr = 0; pr < 2; ++pr) {
                     int i = (ee + 2 * pr) / 2;
-                    double inv = pow((double)epi.theta, -2.0 * i / (double)epi.dh);
-                    double a = (double)pos * inv, cs = cos(a), sn = sin(a);
+                    double cs, sn;
+                    if (epi.rope_tab) {
+                        const double2 cst = epi.rope_tab[(long)pos * (epi.dh / 2) + i];
+                        cs = cst.x, sn = cst.y;
+                    } else {
+                        const double a = (double)pos * pow((double)epi.theta, -2.0 * i / (double)epi.dh);
+                        cs = cos(a), sn = sin(a);
+                    }
                     double x0 = v[2 * pr], x1 = v[2 * pr + 1];
                     v[2 * pr] = (float)(x0 * cs - x1 * sn);
                     v[2 * pr + 1] = (float)(x0 * sn + x1 * cs);

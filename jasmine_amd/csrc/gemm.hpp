@@ -36,6 +36,9 @@ struct SkinnyEpiArgs {
     int d = 0, dh = 0;
     int rope = 0;
     float theta = 10000.f;
+    // optional [position][dh / 2] (cos, sin) of the rotary angles, the same double values
+    // the epilogue would compute; saves the pow / cos / sin at the end of every workgroup
+    const double2 *rope_tab = nullptr;
 };
 
 // Launch geometry of the weight-streaming GEMM: NT 16-row tiles per workgroup (non-SwiGLU)

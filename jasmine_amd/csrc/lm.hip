@@ -65,6 +65,17 @@ __global__ void kv_scatter_kernel(const float *__restrict__ qkv, void *kc, void 
     }
 }
 
+// rotary (cos, sin) per (position, frequency), the QKV epilogue's formula in double
+__global__ void rope_table_kernel(double2 *tab, int ctx, int dh, float theta)
+{
+    const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int hp = dh / 2;
+    if (g >= (long)ctx * hp) return;
+    const int i = (int)(g % hp), p = (int)(g / hp);
+    const double a = (double)p * pow((double)theta, -2.0 * i / (double)dh);
+    tab[g] = make_double2(cos(a), sin(a));
+}
+
 __global__ void swiglu_kernel(const float *__restrict__ gate, const float *__restrict__ up, float *out, long n)
 {
     long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -264,6 +275,7 @@ jas_status decode_step(jas_lm *lm, bool device_pos)
         eq.dh = dh;
         eq.rope = c.kind == 1;
         eq.theta = c.rope_theta;
+        eq.rope_tab = lm->rope_tab;
         TRY(proj(lm, lm->LW("w_qkv", l), lm->h, B, 3 * d, d, eq));
         TRY(prof_begin(lm, 1));
         TRY(attn_decode_impl(lm->q, lm->kv_layer_ptr(lm->kc, l), lm->kv_layer_ptr(lm->vc, l), lm->att, lm->seqlens, B, H,
@@ -426,6 +438,13 @@ jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out)
     for (int b = 1; b < Bm; ++b)  // workspace must cover every batch size actually used
         lm->attn_ws_bytes = std::max(lm->attn_ws_bytes, jas_attn_decode_workspace(b, c.n_head, dh, c.max_ctx));
     if (st == JAS_OK && lm->attn_ws_bytes) st = jas_malloc(&lm->attn_ws, lm->attn_ws_bytes);
+    if (st == JAS_OK && c.kind == 1) {
+        const long n = (long)c.max_ctx * (dh / 2);
+        st = jas_malloc((void **)&lm->rope_tab, sizeof(double2) * n);
+        if (st == JAS_OK)
+            hipLaunchKernelGGL(rope_table_kernel, dim3(ceil_div(n, 256)), dim3(256), 0, lm->stream, lm->rope_tab,
+                               c.max_ctx, dh, c.rope_theta);
+    }
     // K splits of the d-row residual projections: enough workgroups to cover the chip
     lm->ks_o = skinny_pick_ksplit(c.d_model, c.d_model, lm->wbf16());
     lm->ks_d = skinny_pick_ksplit(c.d_model, c.d_ff, lm->wbf16());
@@ -446,7 +465,7 @@ jas_status jas_lm_destroy(jas_lm *lm)
     if (lm->graph) (void)hipGraphExecDestroy(lm->graph);
     void *ptrs[] = {lm->argmax_ws, lm->dstate, lm->arena, lm->kc, lm->vc, lm->x, lm->h, lm->q, lm->att, lm->ff, lm->logits, lm->ids, lm->pos,
                     lm->seqlens, lm->hist, lm->attn_ws, lm->part, lm->pX, lm->pH, lm->pQKV, lm->pATT, lm->pG, lm->pU, lm->pFF,
-                    lm->pIds, lm->pPos};
+                    lm->pIds, lm->pPos, lm->rope_tab};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     for (auto e : lm->ev) (void)hipEventDestroy(e);
