@@ -401,6 +401,7 @@ def main():
     ap.add_argument("--encdec-only", action="store_true",
                     help="only the C++ API encoder-decoder leg (one JSON object; for profilers)")
     ap.add_argument("--no-bf16", action="store_true", help="skip the bf16-storage LLaMA leg")
+    ap.add_argument("--no-batch1", action="store_true", help="skip the batch-1 LLaMA leg")
     ap.add_argument("--kernels-only", action="store_true",
                     help="only the config 2/3 kernel lines (one JSON object; for profilers)")
     ap.add_argument("--no-kernels", action="store_true", help="skip the config 2/3 kernel lines")
@@ -510,6 +511,8 @@ def main():
     # batch-1 decode on the same model (BASELINE's second config-5 row): re-prefill one sequence
     b1 = None
     try:
+        if args.no_batch1:
+            raise RuntimeError("skipped (--no-batch1)")
         lm.prefill(prompt[:1])
         lm.generate(args.warmup, 1)
         b1_pos0 = lm.position
