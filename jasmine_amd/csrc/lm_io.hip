@@ -332,7 +332,7 @@ jas_status parse_header(const char *path, File &f, FileHeader &h)
         const size_t r = sh->arr.size();
         for (size_t k = 0; k < r; ++k) {
             const JVal &d = sh->arr[k];
-            JAS_CHECK(d.kind == JVal::Num && d.integral && d.i >= 0 && d.i <= (1ll << 40), JAS_ERR_INVALID,
+            JAS_CHECK(d.kind == JVal::Num && d.integral && d.i >= 0 && d.i <= INT32_MAX, JAS_ERR_INVALID,
                       tw + "bad shape entry");
             dims[3 - r + k] = (long)d.i;
         }
@@ -342,8 +342,11 @@ jas_status parse_header(const char *path, File &f, FileHeader &h)
                   JAS_ERR_INVALID, tw + "bad data_offsets");
         t.begin = (unsigned long long)of->arr[0].i;
         t.end = (unsigned long long)of->arr[1].i;
-        const unsigned long long want = (unsigned long long)t.layers * t.rows * t.cols * (t.bf16 ? 2 : 4);
-        JAS_CHECK(t.end - t.begin == want, JAS_ERR_INVALID, tw + "data_offsets do not match shape and dtype");
+        unsigned long long want = t.bf16 ? 2 : 4;
+        const bool ovf = __builtin_mul_overflow(want, (unsigned long long)t.layers, &want) ||
+                         __builtin_mul_overflow(want, (unsigned long long)t.rows, &want) ||
+                         __builtin_mul_overflow(want, (unsigned long long)t.cols, &want);
+        JAS_CHECK(!ovf && t.end - t.begin == want, JAS_ERR_INVALID, tw + "data_offsets do not match shape and dtype");
         JAS_CHECK(t.end <= h.data_bytes, JAS_ERR_INVALID, tw + "data runs past the end of the file");
         JAS_CHECK(!h.find(t.name), JAS_ERR_INVALID, tw + "listed twice");
         h.tensors.push_back(t);

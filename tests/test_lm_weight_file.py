@@ -70,7 +70,7 @@ def test_read_config_json_escapes(tmp_path):
 
 
 @pytest.mark.parametrize("case", ["missing", "short", "badlen", "json", "trailing", "dtype", "offsets", "past_end",
-                                  "shape", "nometa", "wrongformat", "badint", "lacks_key", "dup"])
+                                  "shape", "nometa", "wrongformat", "badint", "lacks_key", "dup", "overflow"])
 def test_header_errors(tmp_path, case):
     c = capi()
     vals = (0, 2, 128, 4, 512, 256, 64, 1, 1e-5, 10000.0, 0, 0)
@@ -106,6 +106,9 @@ def test_header_errors(tmp_path, case):
         m = dict(meta)
         del m["rope_theta"]
         write_raw(p, {"a": good_t, "__metadata__": m}, b"\0" * 8)
+    elif case == "overflow":  # 4 * 2^31 * 2^31 * 2^2 wraps to 0 in 64 bits
+        write_raw(p, {"a": dict(good_t, shape=[2147483647, 2147483647, 4], data_offsets=[0, 0]),
+                      "__metadata__": meta}, b"")
     elif case == "dup":
         write_raw(p, '{"a": %s, "a": %s, "__metadata__": %s}' % (json.dumps(good_t), json.dumps(good_t),
                                                                   json.dumps(meta)), b"\0" * 8)
