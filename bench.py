@@ -2,7 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--batch 16] [--prompt 2048] [--no-gpt2] [--no-cpu]
 
-Workload (the north-star target): 32 layers, d_model 4096, 32
+Workload (config 5, the LLaMA-7B shape): 32 layers, d_model 4096, 32
 heads (head dim 128), SwiGLU FFN 11008, RMSNorm eps 1e-6, RoPE theta 1e4, vocab 32000,
 weights N(0, 0.02) from seed 4 (generated on the device), batch 16, prompts of 2048 token
 ids uniform over the vocab (seed 4).  The prompt is prefilled (untimed, reported), W
@@ -42,7 +42,7 @@ def llama_cfg(jas, B, ctx, bf16=False):
 
 def run_llama_bf16(jas, args):
     """The config-5 shape with bf16 weight and KV-cache storage (fp32 activations and
-    accumulation; the survey's first 'next' item).  Same prompt, warm-up and timed steps as
+    accumulation).  Same prompt, warm-up and timed steps as
     the fp32 headline; returns its own line (not the headline value)."""
     from oracle_lib import randint
     B, P = args.batch, args.prompt

@@ -1,4 +1,4 @@
-// Attention (north-star item 4): flash-attention prefill and split-K KV-cache decode.
+// Attention: flash-attention prefill and split-K KV-cache decode.
 //
 // Reference: mat_head_gen_t::forward (mat_mha_t.hpp:45-74) materialises the full
 // S = Q'K / sqrt(d) matrix, masks j > i to -inf (:58-67), runs hsoftmax and multiplies

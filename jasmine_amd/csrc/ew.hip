@@ -1,4 +1,4 @@
-// Fused elementwise evaluation of a jasmine expression tree (north-star item 1).
+// Fused elementwise evaluation of a jasmine expression tree.
 //
 // Reference: mat_express_2_param_stable_t / mat_express_1_param_stable_t
 // (mat_express_t.hpp:35-117, 360-436) evaluate lazily, element by element, at clone()

@@ -1,4 +1,4 @@
-// fp32 GEMMs on the CDNA4 matrix cores (north-star item 5).
+// fp32 GEMMs on the CDNA4 matrix cores.
 //
 // Reference: mat_dot_t::operator() (mat_express_t.hpp:730-736) is a scalar triple loop
 // with sequential-k accumulation, reached from weight_net_t::forward (mat_net_t.hpp:38-49)

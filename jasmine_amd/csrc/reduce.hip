@@ -1,4 +1,4 @@
-// Row reductions (north-star item 2): softmax, LayerNorm, RMSNorm, and jasmine's generic
+// Row reductions: softmax, LayerNorm, RMSNorm, and jasmine's generic
 // sum/max/mean reductions.
 //
 // Reference: hsoftmax (mat_express_t.hpp:681-694) makes four materialised passes (hmax,

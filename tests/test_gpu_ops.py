@@ -1,7 +1,6 @@
 """GPU parity of every kernel behind the C ABI against the CPU oracle / golden vectors.
 
-Tolerance (fp32): |gpu - ref| <= 1e-3 + 1e-4 * |ref| (max-abs 1e-3, rel 1e-4), the
-north-star bound.  Paths whose arithmetic order matches jasmine exactly (per-column
+Tolerance (fp32): |gpu - ref| <= 1e-3 + 1e-4 * |ref| (max-abs 1e-3, rel 1e-4).  Paths whose arithmetic order matches jasmine exactly (per-column
 reductions, elementwise trees) are additionally checked for bit-exactness.  bf16
 attention: |gpu - fp32 ref| <= 2e-2 + 2e-2 * |ref|.
 """
