@@ -221,7 +221,7 @@ static Gen generate(const jas_ew_ins *prog, int n_ins, const LeafDev *leaves, in
     o << "        const " << OT << " res = (" << OT << ")v" << stack.back() << ";\n";
     if (vec && out_dtype == JAS_F32) {
         o << "        ov[e] = res;\n    }\n"
-             "    __builtin_nontemporal_store(fx4{ov[0], ov[1], ov[2], ov[3]}, (fx4 *)((float *)A.out + lin0));\n}\n";
+             "    *(fx4 *)((float *)A.out + lin0) = fx4{ov[0], ov[1], ov[2], ov[3]};\n}\n";
     } else {
         o << "        if (" << (vec ? "true" : "e < nv") << ") ((" << OT << " *)A.out)[lin0 + e] = res;\n    }\n}\n";
     }

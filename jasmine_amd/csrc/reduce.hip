@@ -93,9 +93,9 @@ rowop_reg_kernel(const float *__restrict__ x, float *__restrict__ y, int len, lo
 #pragma unroll
         for (int k = 0; k < PER / 4; ++k) {
             int e = (k * NT + t) * 4;
-            if (e < len)
-                __builtin_nontemporal_store(floatx4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]},
-                                            (floatx4 *)(yr + e));
+            // an ordinary store: the output stays in the Infinity Cache for its consumer (a
+            // nontemporal store streams it to HBM at once: 6.4 against 8.2 TB/s in a copy probe)
+            if (e < len) *(floatx4 *)(yr + e) = floatx4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
         }
     } else {
 #pragma unroll
