@@ -31,8 +31,7 @@ rowop_reg_kernel(const float *__restrict__ x, float *__restrict__ y, int len, lo
 #pragma unroll
         for (int k = 0; k < PER / 4; ++k) {
             int e = (k * NT + t) * 4;
-            // streaming access: non-temporal loads and stores measure ~10% faster than cached
-            // ones for an HBM-sized read+write pass on MI355X
+            // streaming input: non-temporal loads (the output is stored normally, below)
             floatx4 q = e < len ? __builtin_nontemporal_load((const floatx4 *)(xr + e)) : floatx4{0.f, 0.f, 0.f, 0.f};
             v[4 * k] = q[0]; v[4 * k + 1] = q[1]; v[4 * k + 2] = q[2]; v[4 * k + 3] = q[3];
         }
