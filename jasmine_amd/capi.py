@@ -107,7 +107,7 @@ EXPORTED = sorted(list(_sigs) + ["jas_last_error", "jas_version", "jas_default_s
 
 def check(code):
     if code != 0:
-        raise JasError(code, lib.jas_last_error().decode())
+        raise JasError(code, lib.jas_last_error().decode(errors="replace"))
 
 
 _DT = {np.dtype(np.float32): JAS_F32, np.dtype(np.float64): JAS_F64, np.dtype(np.int32): JAS_I32}

@@ -260,3 +260,40 @@ def test_save_is_atomic_on_bad_path(jas, tmp_path):
     with pytest.raises(jas.JasError):
         a.save(str(tmp_path / "no_such_dir" / "m.safetensors"))
     assert not os.path.exists(tmp_path / "no_such_dir")
+
+
+def test_header_parser_survives_corruption(tmp_path):
+    """Seeded byte flips, insertions and truncations of a valid file: the header parser
+    returns a status (success or an error code) for every one and never crashes."""
+    from safetensors.numpy import save_file
+    c = capi()
+    vals = (1, 2, 64, 2, 128, 100, 32, 2, 1e-6, 10000.0, 0, 0)
+    src = str(tmp_path / "ok.safetensors")
+    save_file({"lnf_g": np.ones((1, 1, 64), np.float32), "w_head": np.zeros((1, 100, 64), np.float32)}, src,
+              metadata=meta_for(vals))
+    good = open(src, "rb").read()
+    hlen = struct.unpack("<Q", good[:8])[0]
+    rng = np.random.default_rng(7)
+    p = str(tmp_path / "bad.safetensors")
+    outcomes = {0: 0, 1: 0, 2: 0}
+    for _ in range(400):
+        b = bytearray(good)
+        kind = rng.integers(4)
+        if kind == 0:  # flip bytes in the header
+            for _ in range(int(rng.integers(1, 6))):
+                b[8 + int(rng.integers(hlen))] = int(rng.integers(256))
+        elif kind == 1:  # truncate anywhere
+            b = b[:int(rng.integers(len(b)))]
+        elif kind == 2:  # corrupt the length field
+            b[int(rng.integers(8))] = int(rng.integers(256))
+        else:  # insert a structural character
+            i = 8 + int(rng.integers(hlen))
+            b = b[:i] + bytes([b'{}[]",:\\'[int(rng.integers(8))]]) + b[i:]
+        open(p, "wb").write(bytes(b))
+        try:
+            c.read_lm_config(p)
+            outcomes[0] += 1
+        except c.JasError as e:
+            assert e.code in (1, 2), str(e)
+            outcomes[e.code] += 1
+    assert outcomes[1] > 100
