@@ -601,14 +601,14 @@ __global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p
     p.O[decode_out_index(p, bh, D, tid)] = L > 0.f ? A / L : 0.f;
 }
 
-// Keys per split: a function of the (sequence, head) count only, never of the cache length,
-// so a given sequence's keys always fall into the same splits and a launch over a longer
-// max_len only adds empty trailing splits (whose zero weights leave the merge bit-identical).
-// 2*B*H keys per split (at least 192): many splits when few (sequence, head) pairs must fill
-// the chip, about three 1K-key splits per pair at the LLaMA-7B batch-16 shape (measured best).
-// bf16 caches take twice the keys per step (8 elements per lane), so their chunk is never
-// shorter and their split count never larger than the fp32 one: the fp32 workspace size
-// covers both.
+// Split count: about max_len / (2*B*H) keys per split (at least 192) -- many splits when few
+// (sequence, head) pairs must fill the chip, three at the LLaMA-7B batch-16 shape -- then
+// max_len is cut into that many equal splits, so no workgroup is left with a short tail
+// (1024 + 1024 + 249 keys at 2297 streamed at 6.41 TB/s, 3 x 768 at 6.53).  A sequence's keys
+// fall into the same splits for a given max_len (the runner always passes its max_ctx);
+// splits past a shorter sequence's length are empty and carry zero weight in the merge.
+// bf16 caches take twice the keys per step (8 elements per lane), so their split count is
+// never larger than the fp32 one: the fp32 workspace size covers both.
 // "wide" form: one 16-wave workgroup per (sequence, head) over the whole context -- no split
 // and no merge launch.  It needs few pairs (all of them resident at once) and wins when the
 // contexts are short: the decoder runner of a GPT-2 size model (about 500 keys per head at
@@ -632,8 +632,13 @@ static int decode_nsplit(int B, int H, int D, int max_len, int *chunk, bool kv_b
     const int keys_per_step = 4 * (WAVE / (D / (kv_bf16 ? 8 : 4))) * 4;  // NG * U
     int ch = std::max(2 * B * H, 192);
     ch = (ch + keys_per_step - 1) / keys_per_step * keys_per_step;
+    int ns = std::max(1, (max_len + ch - 1) / ch);
+    // then equal splits of max_len (e.g. 3 x 768 keys instead of 1024 + 1024 + 249)
+    ch = (max_len + ns - 1) / ns;
+    ch = (ch + keys_per_step - 1) / keys_per_step * keys_per_step;
+    ns = std::max(1, (max_len + ch - 1) / ch);
     *chunk = ch;
-    return std::max(1, (max_len + ch - 1) / ch);
+    return ns;
 }
 
 // the wide form exists for fp32 caches and D >= 64 only (decode_wide_ok)
