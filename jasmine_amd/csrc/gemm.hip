@@ -871,6 +871,12 @@ extern "C" jas_status jas_gemm(int M, int N, int K, const float *A, long as0, lo
         e.ldo = cs1;
         return skinny_gemm(A, nullptr, B, bs1, M, N, K, e, s, false, nullptr);
     }
+    // plain products of library size: rocBLAS (see blas.cpp)
+    if (blas_gemm(M, N, K, A, as0, as1, B, bs0, bs1, C, cs0, cs1, bias, bias_mode, act, accumulate, batch, abs_, bbs,
+                  cbs, biasbs, s)) {
+        JAS_LAUNCH_CHECK();
+        return JAS_OK;
+    }
     return gemm_general(M, N, K, A, as0, as1, B, bs0, bs1, C, cs0, cs1, bias, bias_mode, act, accumulate, batch, abs_,
                         bbs, cbs, biasbs, s, false);
 }

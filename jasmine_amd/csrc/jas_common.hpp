@@ -25,6 +25,11 @@ jas_status attn_decode_impl(const float *q, const void *K, const void *V, float 
                             int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, hipStream_t s,
                             int o_packed_d, bool kv_bf16 = false, bool wide = false);
 
+// jas_gemm's plain products on rocBLAS; false = not taken (the caller runs its own kernel)
+bool blas_gemm(int M, int N, int K, const float *A, long as0, long as1, const float *B, long bs0, long bs1, float *C,
+               long cs0, long cs1, const float *bias, int bias_mode, int act, int accumulate, int batch, long abs_,
+               long bbs, long cbs, long biasbs, hipStream_t s);
+
 // two-pass row argmax with caller-provided scratch of argmax_workspace_bytes(n, V) bytes
 size_t argmax_workspace_bytes(int n, int V);
 jas_status argmax_impl(const float *x, int n, int V, long ld, int32_t *out, void *work, hipStream_t s);

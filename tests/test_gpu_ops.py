@@ -305,6 +305,17 @@ def test_gemm_epilogues(jas, bias_mode, act, acc, batch):
     _gemm_case(jas, 150, 90, 70, bias_mode=bias_mode, act=act, acc=bool(acc), batch=batch)
 
 
+@pytest.mark.parametrize("ta,tb,col_c", [(0, 0, 0), (1, 0, 0), (0, 1, 0), (1, 1, 1), (0, 0, 1), (1, 0, 1)])
+@pytest.mark.parametrize("bias_mode,acc,batch", [(0, 0, 1), (1, 0, 2), (2, 0, 1), (0, 1, 3)])
+def test_gemm_library_sizes(jas, ta, tb, col_c, bias_mode, acc, batch):
+    """Plain products of at least 256 x 256 x 128 go to the BLAS library (no activation, no
+    bias together with accumulation); every operand layout, both bias modes, batches."""
+    _gemm_case(jas, 300, 260, 200, ta=bool(ta), tb=bool(tb), col_c=bool(col_c), bias_mode=bias_mode, acc=bool(acc),
+               batch=batch)
+    _gemm_case(jas, 257, 513, 129, ta=bool(ta), tb=bool(tb), col_c=bool(col_c), bias_mode=bias_mode, acc=bool(acc),
+               batch=batch, seed=1)
+
+
 @pytest.mark.parametrize("N", [1, 2, 5, 8, 16])
 @pytest.mark.parametrize("M,K", [(300, 64), (64, 100), (1000, 4096), (4096, 1024), (8200, 80), (25000, 64)])
 def test_gemm_skinny(jas, M, N, K):
