@@ -79,10 +79,15 @@ bool blas_gemm(int M, int N, int K, const float *A, long as0, long as1, const fl
     if (l1 > lim || l2 > lim || ldc > lim) return false;
     std::lock_guard<std::mutex> lk(g_blas_mu);
     if (g_blas_failed) return false;
-    if (!g_blas && rocblas_create_handle(&g_blas) != rocblas_status_success) {
-        g_blas_failed = true;
-        g_blas = nullptr;
-        return false;
+    if (!g_blas) {
+        // no atomics: every product is summed in a fixed order (run-to-run identical)
+        if (rocblas_create_handle(&g_blas) != rocblas_status_success ||
+            rocblas_set_atomics_mode(g_blas, rocblas_atomics_not_allowed) != rocblas_status_success) {
+            if (g_blas) (void)rocblas_destroy_handle(g_blas);
+            g_blas_failed = true;
+            g_blas = nullptr;
+            return false;
+        }
     }
     if (rocblas_set_stream(g_blas, s) != rocblas_status_success) return false;
     const float one = 1.f, beta = accumulate ? 1.f : 0.f;

@@ -568,3 +568,16 @@ def test_pool_reuses_and_trims(jas):
     assert n.value >= 2048
     jas.check(lib.jas_pool_trim(C.byref(n)))
     assert n.value == 0
+
+
+def test_gemm_library_is_deterministic(jas):
+    """Two runs of a library-sized product give identical bits (no atomic reductions)."""
+    M, N, K = 512, 384, 2048
+    A, B = normal((M, K), 35, 0), normal((K, N), 35, 1)
+    dA, dB = jas.to_device(A), jas.to_device(B)
+    outs = []
+    for _ in range(2):
+        dC = jas.DeviceArray((M, N))
+        jas.check(jas.lib.jas_gemm(M, N, K, dA.p, K, 1, dB.p, N, 1, dC.p, N, 1, None, 0, 0, 0, 1, 0, 0, 0, 0, None))
+        outs.append(dC.numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
