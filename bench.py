@@ -143,13 +143,23 @@ def run_gpt2(jas, cfg_args, B, P, seed, steps, warmup, graph=True):
     lm = jas.Lm(cfg)
     lm.use_graph(graph)
     lm.init_random(seed, 0.02)
-    lm.prefill(randint((B, P), V, seed))
+    prompt = randint((B, P), V, seed)
+    lm.prefill(prompt)  # first call: buffers and kernels warm
+    t0 = time.perf_counter()
+    lm.prefill(prompt)  # returns after the next ids are on the host
+    prefill_s = time.perf_counter() - t0
     lm.generate(warmup, B)
     t0 = time.perf_counter()
     lm.generate(steps, B)
     dt = time.perf_counter() - t0
     lm.close()
     mean_ctx = P + warmup + (steps + 1) / 2.0
+    # prefill flops: every projection of every prompt token, causal attention, the LM head
+    # for the last position of each sequence
+    pf = 2.0 * B * P * L * (4 * d * d + 2 * d * F) + 4.0 * B * L * (P * P / 2.0) * d + 2.0 * B * V * d
+    run_gpt2.last_prefill = {"tok_s": round(B * P / prefill_s, 1), "ms": round(1e3 * prefill_s, 3),
+                             "tflops": round(pf / prefill_s / 1e12, 2),
+                             "mfma_frac": round(pf / prefill_s / 1e12 / FP32_MFMA_TFLOPS, 4)}
     return B * steps / dt, 1e3 * dt / steps, gpt2_decode_bytes(L, d, F, V, B, mean_ctx)
 
 
@@ -554,9 +564,11 @@ def main():
             g_frac = g_bytes / (g_ms * 1e-3) / 1e9 / HBM_PEAK_GBS
             gpt2 = {"decode_tok_s": round(g_tok, 1), "ms_per_step": round(g_ms, 3),
                     "hbm_bytes_per_step": round(g_bytes), "step_hbm_frac": round(g_frac, 4),
+                    "prefill": dict(run_gpt2.last_prefill, workload="8 x 512 prompt tokens, fp32, wall time"),
                     "workload": "config4: GPT-2-small fp32, batch 8, 512-token prompts, greedy decode "
                                 "(32 timed steps after 4 warm-up)"}
-            log(f"[bench] gpt2-small decode: {g_tok:.1f} tok/s, {g_ms:.3f} ms/step, {100 * g_frac:.1f}% of HBM peak")
+            log(f"[bench] gpt2-small decode: {g_tok:.1f} tok/s, {g_ms:.3f} ms/step, {100 * g_frac:.1f}% of HBM peak; "
+                f"prefill {run_gpt2.last_prefill}")
             t_tok, t_ms, t_bytes = run_gpt2(jas, (2, 128, 4, 512, 256, 64), 1, 32, 0, 31, 1,
                                             graph=not args.no_graph)
             tiny = {"decode_tok_s": round(t_tok, 1), "ms_per_step": round(t_ms, 4),
