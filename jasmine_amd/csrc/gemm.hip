@@ -296,8 +296,10 @@ jas_status gemm_general(int M, int N, int K, const void *A, long as0, long as1, 
     int am = a_packed ? (a_bf16 ? LM_PKB : LM_PK) : pick_mode((const float *)A, as0, as1, M, K, abs_);
     int bm = pick_mode(B, bs1, bs0, N, K, bbs);
     bool c4 = cs0 == 1 && al16(C) && (cs1 % 4 == 0) && (cbs % 4 == 0);
-    // 64-wide tiles when 128-wide ones would leave CUs idle (fewer workgroups than CUs)
-    const bool small = (long)ceil_div(N, TBN) * ceil_div(M, TBM) * batch < 256;
+    // 64-wide tiles when 128-wide ones give at most three workgroups per CU: too few to fill
+    // the chip, or so few rounds that the last, partly empty one weighs (GPT-2-small prefill
+    // GEMMs of 576 and 768 such workgroups: 8.34 -> 8.05 ms per prefill)
+    const bool small = (long)ceil_div(N, TBN) * ceil_div(M, TBM) * batch <= 3 * 256;
     if (am == LM_PKB) launch_tile_b<LM_PKB>(p, bm, c4, small, batch, s);
     else if (am == LM_PK) launch_tile_b<LM_PK>(p, bm, c4, small, batch, s);
     else if (am == LM_KC) launch_tile_b<LM_KC>(p, bm, c4, small, batch, s);
