@@ -40,11 +40,10 @@ bool as_colmajor(long s_row, long s_col, int rows, int cols, rocblas_operation &
 __global__ void add_bias_kernel(float *C, int M, int N, long cs0, long cs1, long cbs, const float *bias, long bbs,
                                 int mode)
 {
-    const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long e = (long)blockIdx.x * blockDim.x + threadIdx.x;  // element of batch blockIdx.y
     const long per = (long)M * N;
-    if (g >= per * gridDim.y) return;
+    if (e >= per) return;
     const int z = blockIdx.y;
-    const long e = g % per;
     const int m = (int)(e / N), n = (int)(e % N);
     float *c = C + z * cbs + (long)m * cs0 + (long)n * cs1;
     *c += (bias + z * bbs)[mode == 1 ? m : n];
