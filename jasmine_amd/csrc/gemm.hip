@@ -602,7 +602,8 @@ SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split, bool wbf
     SkinnyTuning t;
     const int rt = (M + 15) / 16;
     if (wbf16) {  // bf16 weights (cold-weight sweep): half the bytes per tile, deeper rings
-        if (dual) { t.nt = 2; t.wpb = 4; t.depth = 3; }
+        if (dual && rt >= 512) { t.nt = 6; t.wpb = 4; t.depth = 2; }  // one round (fp32 note below)
+        else if (dual) { t.nt = 2; t.wpb = 4; t.depth = 3; }
         else if (split && rt >= 256) {
             if (K >= 8192) { t.nt = 4; t.wpb = 4; t.depth = 4; }
             else { t.nt = 2; t.wpb = 8; t.depth = 2; }
@@ -692,7 +693,7 @@ jas_status skinny_gemm(const void *W, const void *W2, const float *X, long ldx, 
         JAS_SKB(2, 4, true, 3) JAS_SKB(2, 4, true, 4) JAS_SKB(2, 4, false, 2) JAS_SKB(2, 4, false, 3)
         JAS_SKB(2, 4, false, 4) JAS_SKB(2, 8, false, 2) JAS_SKB(2, 8, false, 3) JAS_SKB(4, 4, false, 2)
         JAS_SKB(4, 4, false, 3) JAS_SKB(4, 4, false, 4) JAS_SKB(1, 8, false, 3) JAS_SKB(1, 8, false, 4)
-        JAS_SKB(3, 4, false, 3) JAS_SKB(3, 4, false, 4)
+        JAS_SKB(3, 4, false, 3) JAS_SKB(3, 4, false, 4) JAS_SKB(6, 4, true, 2)
 #undef JAS_SKB
         return fail(JAS_ERR_INVALID, "skinny_gemm: unsupported tuning for bf16 weights");
     }
