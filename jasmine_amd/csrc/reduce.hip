@@ -382,6 +382,15 @@ resid_norm_kernel(float *__restrict__ x, const float *__restrict__ part, int ks,
     const int n = blockIdx.x, t = threadIdx.x;
     float *xr = x + (long)n * d;
     float v[PER];
+    // the norm's gain (and bias) are requested together with the row, not after the
+    // reductions: one memory round trip fewer on the critical path
+    float4 gg[PER / 4], bb4[PER / 4];
+#pragma unroll
+    for (int k = 0; k < PER / 4; ++k) {
+        const int e = (k * 256 + t) * 4;
+        gg[k] = e < d ? *(const float4 *)(g + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+        bb4[k] = (!RMS && bta && e < d) ? *(const float4 *)(bta + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
 #pragma unroll
     for (int k = 0; k < PER / 4; ++k) {
         const int e = (k * 256 + t) * 4;
@@ -428,14 +437,13 @@ resid_norm_kernel(float *__restrict__ x, const float *__restrict__ part, int ks,
     for (int k = 0; k < PER / 4; ++k) {
         const int e = (k * 256 + t) * 4;
         if (e >= d) continue;
-        float4 gg = *(const float4 *)(g + e), o;
-        o.x = (v[4 * k] - mean) / den * gg.x;
-        o.y = (v[4 * k + 1] - mean) / den * gg.y;
-        o.z = (v[4 * k + 2] - mean) / den * gg.z;
-        o.w = (v[4 * k + 3] - mean) / den * gg.w;
+        float4 o;
+        o.x = (v[4 * k] - mean) / den * gg[k].x;
+        o.y = (v[4 * k + 1] - mean) / den * gg[k].y;
+        o.z = (v[4 * k + 2] - mean) / den * gg[k].z;
+        o.w = (v[4 * k + 3] - mean) / den * gg[k].w;
         if (!RMS && bta) {
-            float4 bb = *(const float4 *)(bta + e);
-            o.x += bb.x; o.y += bb.y; o.z += bb.z; o.w += bb.w;
+            o.x += bb4[k].x; o.y += bb4[k].y; o.z += bb4[k].z; o.w += bb4[k].w;
         }
         // packed: the 4 features e..e+3 of token n are one lane's B-operand float4
         const long yo = y_packed ? ((long)(e >> 4) * 64 + n + 16 * ((e & 15) >> 2)) * 4 : (long)n * d + e;
