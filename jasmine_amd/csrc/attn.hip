@@ -589,14 +589,36 @@ __global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p
 {
     const int bh = blockIdx.x, tid = threadIdx.x;
     const float *pp = p.part + (long)bh * p.nsplit * (D + 2);
+    // eight splits' values are requested at a time (one round trip per eight, not per split);
+    // the sums keep split order
+    constexpr int G = 8;
+    const int ns = p.nsplit;
     float M = -FLT_MAX;
-    for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, pp[s * (D + 2)]);
+    for (int s0 = 0; s0 < ns; s0 += G) {
+        float mv[G];
+#pragma unroll
+        for (int u = 0; u < G; ++u) mv[u] = s0 + u < ns ? pp[(s0 + u) * (D + 2)] : -FLT_MAX;
+#pragma unroll
+        for (int u = 0; u < G; ++u) M = fmaxf(M, mv[u]);
+    }
     float L = 0.f, A = 0.f;
-    for (int s = 0; s < p.nsplit; ++s) {
-        float ms = pp[s * (D + 2)];
-        float f = ms == -FLT_MAX ? 0.f : exp2f(ms - M);
-        L += pp[s * (D + 2) + 1] * f;
-        A += pp[s * (D + 2) + 2 + tid] * f;
+    for (int s0 = 0; s0 < ns; s0 += G) {
+        float mv[G], lv[G], av[G];
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+            const bool in = s0 + u < ns;
+            const float *q = pp + (s0 + u) * (D + 2);
+            mv[u] = in ? q[0] : -FLT_MAX;
+            lv[u] = in ? q[1] : 0.f;
+            av[u] = in ? q[2 + tid] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+            if (s0 + u >= ns) break;
+            const float f = mv[u] == -FLT_MAX ? 0.f : exp2f(mv[u] - M);
+            L += lv[u] * f;
+            A += av[u] * f;
+        }
     }
     p.O[decode_out_index(p, bh, D, tid)] = L > 0.f ? A / L : 0.f;
 }
