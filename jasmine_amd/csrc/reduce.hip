@@ -372,13 +372,13 @@ static jas_status reduce_t(const jas_leaf *in, int op, int axis, void *d_out, hi
 // partial sums of the projection that feeds the residual stream ([split][16][d], split
 // order), so the split-K reduction costs no launch of its own.  One workgroup per token.
 constexpr int RN_MAX_SPLITS = 8;  // the decode projections split K at most 8 ways
-template <int PER, bool RMS>
-__global__ void __launch_bounds__(256)
+template <int PER, bool RMS, int NT>
+__global__ void __launch_bounds__(NT)
 resid_norm_kernel(float *__restrict__ x, const float *__restrict__ part, int ks, const float *__restrict__ bias,
                   const float *__restrict__ g, const float *__restrict__ bta, float *__restrict__ y, int d, float eps,
                   int y_packed)
 {
-    __shared__ float red[4];
+    __shared__ float red[NT / 64];
     const int n = blockIdx.x, t = threadIdx.x;
     float *xr = x + (long)n * d;
     float v[PER];
@@ -387,13 +387,13 @@ resid_norm_kernel(float *__restrict__ x, const float *__restrict__ part, int ks,
     float4 gg[PER / 4], bb4[PER / 4];
 #pragma unroll
     for (int k = 0; k < PER / 4; ++k) {
-        const int e = (k * 256 + t) * 4;
+        const int e = (k * NT + t) * 4;
         gg[k] = e < d ? *(const float4 *)(g + e) : make_float4(0.f, 0.f, 0.f, 0.f);
         bb4[k] = (!RMS && bta && e < d) ? *(const float4 *)(bta + e) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
     for (int k = 0; k < PER / 4; ++k) {
-        const int e = (k * 256 + t) * 4;
+        const int e = (k * NT + t) * 4;
         float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
         if (e < d) {
             a = *(const float4 *)(xr + e);
@@ -423,19 +423,19 @@ resid_norm_kernel(float *__restrict__ x, const float *__restrict__ part, int ks,
         float sm = 0.f;
 #pragma unroll
         for (int k = 0; k < PER; ++k) sm += v[k];
-        mean = block_sum<256>(sm, red) / (float)d;
+        mean = block_sum<NT>(sm, red) / (float)d;
     }
     float s2 = 0.f;
 #pragma unroll
     for (int k = 0; k < PER; ++k) {
-        const int e = ((k / 4) * 256 + t) * 4;
+        const int e = ((k / 4) * NT + t) * 4;
         const float dv = e < d ? v[k] - mean : 0.f;
         s2 += dv * dv;
     }
-    const float den = sqrtf(block_sum<256>(s2, red) / (float)d + eps);
+    const float den = sqrtf(block_sum<NT>(s2, red) / (float)d + eps);
 #pragma unroll
     for (int k = 0; k < PER / 4; ++k) {
-        const int e = (k * 256 + t) * 4;
+        const int e = (k * NT + t) * 4;
         if (e >= d) continue;
         float4 o;
         o.x = (v[4 * k] - mean) / den * gg[k].x;
@@ -458,16 +458,18 @@ jas_status resid_norm(float *x, const float *part, int ks, const float *bias, co
     JAS_CHECK(ks <= RN_MAX_SPLITS, JAS_ERR_INVALID, "resid_norm: more K splits than supported");
     JAS_CHECK(!y_packed || d % 16 == 0, JAS_ERR_INVALID, "resid_norm: packed output needs d % 16 == 0");
     const int yp = y_packed ? 1 : 0;
-#define JAS_RN(PER)                                                                                              \
-    if (d <= PER * 256) {                                                                                        \
-        if (rms) hipLaunchKernelGGL((resid_norm_kernel<PER, true>), dim3(N), dim3(256), 0, s, x, part, ks, bias, \
-                                    g, b, y, d, eps, yp);                                                        \
-        else hipLaunchKernelGGL((resid_norm_kernel<PER, false>), dim3(N), dim3(256), 0, s, x, part, ks, bias, g, \
-                                b, y, d, eps, yp);                                                               \
-        JAS_LAUNCH_CHECK();                                                                                      \
-        return JAS_OK;                                                                                           \
+#define JAS_RN(PER, NT)                                                                                      \
+    if (d <= PER * NT) {                                                                                     \
+        if (rms) hipLaunchKernelGGL((resid_norm_kernel<PER, true, NT>), dim3(N), dim3(NT), 0, s, x, part, ks, \
+                                    bias, g, b, y, d, eps, yp);                                              \
+        else hipLaunchKernelGGL((resid_norm_kernel<PER, false, NT>), dim3(N), dim3(NT), 0, s, x, part, ks,   \
+                                bias, g, b, y, d, eps, yp);                                                  \
+        JAS_LAUNCH_CHECK();                                                                                  \
+        return JAS_OK;                                                                                       \
     }
-    JAS_RN(4) JAS_RN(8) JAS_RN(16) JAS_RN(32)
+    // one float4 per thread up to d = 4096 (more waves per token: the partial loads are
+    // spread over 16 waves instead of 4); wider rows take 8 features per thread
+    JAS_RN(4, 256) JAS_RN(4, 512) JAS_RN(4, 1024) JAS_RN(8, 1024)
 #undef JAS_RN
     return fail(JAS_ERR_INVALID, "resid_norm: d too large");
 }
