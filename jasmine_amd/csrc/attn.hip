@@ -589,21 +589,12 @@ __global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p
 {
     const int bh = blockIdx.x, tid = threadIdx.x;
     const float *pp = p.part + (long)bh * p.nsplit * (D + 2);
-    // eight splits' values are requested at a time (one round trip per eight, not per split);
-    // the sums keep split order
+    // eight splits' (max, sum, value) are requested at a time; with at most eight splits the
+    // whole merge is one memory round trip.  The sums keep split order.
     constexpr int G = 8;
     const int ns = p.nsplit;
-    float M = -FLT_MAX;
-    for (int s0 = 0; s0 < ns; s0 += G) {
-        float mv[G];
-#pragma unroll
-        for (int u = 0; u < G; ++u) mv[u] = s0 + u < ns ? pp[(s0 + u) * (D + 2)] : -FLT_MAX;
-#pragma unroll
-        for (int u = 0; u < G; ++u) M = fmaxf(M, mv[u]);
-    }
-    float L = 0.f, A = 0.f;
-    for (int s0 = 0; s0 < ns; s0 += G) {
-        float mv[G], lv[G], av[G];
+    float mv[G], lv[G], av[G];
+    auto load = [&](int s0) {
 #pragma unroll
         for (int u = 0; u < G; ++u) {
             const bool in = s0 + u < ns;
@@ -612,6 +603,15 @@ __global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p
             lv[u] = in ? q[1] : 0.f;
             av[u] = in ? q[2 + tid] : 0.f;
         }
+    };
+    load(0);
+    float M = -FLT_MAX;
+#pragma unroll
+    for (int u = 0; u < G; ++u) M = fmaxf(M, mv[u]);
+    for (int s0 = G; s0 < ns; ++s0) M = fmaxf(M, pp[s0 * (D + 2)]);
+    float L = 0.f, A = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += G) {
+        if (s0 > 0) load(s0);
 #pragma unroll
         for (int u = 0; u < G; ++u) {
             if (s0 + u >= ns) break;
