@@ -74,7 +74,10 @@ def test_llama_architecture_small(jas):
     run_parity(jas, cfg, seed=4, B=3, P=20, steps=8, prompt_seed=4)
 
 
-@pytest.mark.parametrize("kind,d,H,F,V", [(1, 128, 4, 208, 333), (0, 192, 3, 336, 77)])
+@pytest.mark.parametrize("kind,d,H,F,V", [(1, 128, 4, 208, 333), (0, 192, 3, 336, 77),
+                                          # residual + norm rows of 272 float4s over 512 threads,
+                                          # and of 8 features per thread (d > 4096)
+                                          (1, 1088, 17, 208, 64), (0, 4352, 34, 208, 64)])
 def test_ragged_chunk_widths(jas, kind, d, H, F, V):
     # FFN widths that are multiples of 16 but not of 64 (208 = 3*64 + 16, 336 = 5*64 + 16):
     # the down/proj projection's last K chunk is partial, also under its K split; and
