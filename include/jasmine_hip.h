@@ -291,6 +291,10 @@ jas_status jas_lm_generate(jas_lm *lm, int steps, int32_t *h_ids);
 jas_status jas_lm_use_graph(jas_lm *lm, int enable);
 /* Current sequence length (tokens in the KV cache). */
 int jas_lm_position(jas_lm *lm);
+/* Key splits of the runner's decode attention at batch B (1 = one pass, no merge launch;
+ * above 1 = split over the cache plus the log-sum-exp merge; 0 = bad argument).  A query
+ * for tests and tuning: no reference counterpart (jasmine has no KV cache). */
+int jas_lm_attn_splits(jas_lm *lm, int B);
 jas_stream_t jas_lm_stream(jas_lm *lm);
 /* Per-kernel-class GPU time (ms) accumulated with HIP events around every launch on the
  * runner's stream since the last reset; classes: 0 weight GEMM (decode), 1 attention decode,

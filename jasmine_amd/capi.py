@@ -97,12 +97,15 @@ lib.jas_attn_decode_workspace.restype = C.c_size_t
 lib.jas_attn_decode_workspace.argtypes = [I, I, I, I]
 lib.jas_lm_position.restype = I
 lib.jas_lm_position.argtypes = [VP]
+lib.jas_lm_attn_splits.restype = I
+lib.jas_lm_attn_splits.argtypes = [VP, I]
 lib.jas_lm_stream.restype = VP
 lib.jas_lm_stream.argtypes = [VP]
 
 # every symbol the C header declares (checked by the CPU test that the library exports them)
 EXPORTED = sorted(list(_sigs) + ["jas_last_error", "jas_version", "jas_default_stream",
-                                 "jas_attn_decode_workspace", "jas_ew_jit_mode", "jas_lm_position", "jas_lm_stream"])
+                                 "jas_attn_decode_workspace", "jas_ew_jit_mode", "jas_lm_position", "jas_lm_stream",
+                                 "jas_lm_attn_splits"])
 
 
 def check(code):
@@ -242,6 +245,10 @@ class Lm:
     @property
     def position(self):
         return lib.jas_lm_position(self.h)
+
+    def attn_splits(self, B):
+        """Key splits the decode attention takes at batch B (1: one pass, no merge)."""
+        return lib.jas_lm_attn_splits(self.h, int(B))
 
     def use_graph(self, enable):
         check(lib.jas_lm_use_graph(self.h, int(enable)))

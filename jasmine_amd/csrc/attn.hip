@@ -670,6 +670,13 @@ static void launch_decode_wide(dim3 grid, hipStream_t s, const DecodeArgs &p)
     if constexpr (D >= 64) hipLaunchKernelGGL((attn_decode_kernel<D, false, 16>), grid, dim3(1024), 0, s, p);
 }
 
+int attn_decode_splits(int B, int H, int D, int max_len, bool kv_bf16, bool wide)
+{
+    if (B <= 0 || H <= 0 || max_len <= 0 || (D != 32 && D != 64 && D != 128)) return 0;
+    int chunk;
+    return decode_nsplit(B, H, D, max_len, &chunk, kv_bf16, wide && decode_wide_ok(B, H, D, max_len, kv_bf16));
+}
+
 jas_status attn_decode_impl(const float *q, const void *K, const void *V, float *O, const int32_t *seqlens, int B,
                             int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, hipStream_t s,
                             int o_packed_d, bool kv_bf16, bool wide)

@@ -24,6 +24,8 @@ jas_status resid_norm(float *x, const float *part, int ks, const float *bias, co
 jas_status attn_decode_impl(const float *q, const void *K, const void *V, float *O, const int32_t *seqlens, int B,
                             int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, hipStream_t s,
                             int o_packed_d, bool kv_bf16 = false, bool wide = false);
+// key splits attn_decode_impl launches for this shape (1: no merge launch; 0: bad shape)
+int attn_decode_splits(int B, int H, int D, int max_len, bool kv_bf16, bool wide);
 
 // jas_gemm's plain products on rocBLAS; false = not taken (the caller runs its own kernel)
 bool blas_gemm(int M, int N, int K, const float *A, long as0, long as1, const float *B, long bs0, long bs1, float *C,

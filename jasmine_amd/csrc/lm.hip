@@ -715,6 +715,13 @@ jas_status jas_lm_generate(jas_lm *lm, int steps, int32_t *h_ids)
 
 int jas_lm_position(jas_lm *lm) { return lm ? lm->position : -1; }
 
+int jas_lm_attn_splits(jas_lm *lm, int B)
+{
+    if (!lm || B <= 0 || B > lm->cfg.max_batch) return 0;
+    const jas_lm_config &c = lm->cfg;
+    return attn_decode_splits(B, c.n_head, c.d_model / c.n_head, c.max_ctx, c.kv_bf16 != 0, true);
+}
+
 jas_status jas_lm_use_graph(jas_lm *lm, int enable)
 {
     JAS_CHECK(lm, JAS_ERR_INVALID, "jas_lm_use_graph: null model");

@@ -31,7 +31,7 @@ public:
     using val_type = typename base_type::val_type;
     mse_loss_t() = default;
     mat_t<val_type> backward(const mat_t<val_type> &) const { jas::detail::no_training("mse_loss_t::backward"); }
-    // mean squared error against a target (mat_loss_t.hpp:503-506)
+    // mean squared error against a target (mat_loss_t.hpp:42-45)
     val_type loss(const mat_t<val_type> &target) const { return mean(pow(base_type::m_input - target)); }
     std::string net_type(int const &indent = 0) const { return print_indent(indent) + "mse_loss_t"; }
     template <typename init_type>

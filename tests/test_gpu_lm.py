@@ -105,9 +105,10 @@ def test_bf16_storage(jas, kind, wb, kb):
 @pytest.mark.parametrize("kind,bf16", [(1, 0), (0, 0), (1, 1)])
 def test_full_batch_16(jas, kind, bf16):
     """max_batch 16 -- the headline's batch -- fills all 16 token columns of the packed
-    activation operand and of every MFMA tile.  The LLaMA kind (head dim 128, 16 x 16 = 256
-    (sequence, head) pairs) takes the split-K attention with its merge; the GPT-2 kind
-    (16 x 4 = 64 pairs) the unsplit 16-wave form."""
+    activation operand and of every MFMA tile.  With a 40-key cache the attention runs in
+    one pass per (sequence, head): the LLaMA kind (16 x 16 = 256 pairs) in the 4-wave split
+    form with a single split, the GPT-2 kind (16 x 4 = 64 pairs) in the unsplit 16-wave form.
+    The multi-split attention and its merge are covered by the test_split_decode_* cases."""
     if kind == 1:
         cfg = jas.LmConfig(1, 2, 2048, 16, 512, 300, 40, 16, 1e-6, 10000.0, bf16, bf16)
     else:
@@ -251,3 +252,76 @@ def test_weight_set_get_roundtrip(jas):
         lm.set_weight(name, a)
         assert np.array_equal(lm.weight(name), a), name
     assert lm.weight_shape("w_gate") == (0, 0, 0)
+
+
+# ---------------------------------------------------------------------------------------
+# Multi-split decode attention inside the runner.  The headline decode (LLaMA-7B shape,
+# B = 16, H = 32, d_h 128, cache of about 2100 keys) splits each (sequence, head) over the
+# cache and merges the splits by log-sum-exp into the packed O-projection operand; batch 1
+# takes about 11 splits.  These cases force that path (asserted through jas_lm_attn_splits)
+# with prompts long enough that several splits hold keys, and check the logits of every
+# step against the oracle.  The oracle runs the sequences named in `check` (sequences are
+# independent, so a subset pins the batch); its cost is the prompt length times the weights.
+
+def run_parity_subset(jas, cfg, seed, B, P, steps, prompt_seed, check, want_splits):
+    lm = jas.Lm(cfg)
+    lm.init_random(seed, 0.02)
+    got_splits = lm.attn_splits(B)
+    assert got_splits >= want_splits, f"expected >= {want_splits} attention splits, runner takes {got_splits}"
+    ocfg, ow, keep = oracle_for(jas, lm, cfg)
+    prompt = randint((B, P), cfg.vocab, prompt_seed)
+    check = list(check)
+    cpu_ids = np.zeros((len(check), steps), np.int32)
+    cpu_logits = np.zeros((steps, len(check), cfg.vocab), np.float32)
+    for i, b in enumerate(check):  # one sequence per call: the oracle's GEMVs go parallel
+        ids1 = np.zeros((1, steps), np.int32)
+        lg1 = np.zeros((steps, 1, cfg.vocab), np.float32)
+        orc.orc_lm_generate(ocfg, ow, 1, P, ip(np.ascontiguousarray(prompt[b:b + 1])), steps, None, ip(ids1),
+                            fp(lg1), 16)
+        cpu_ids[i] = ids1[0]
+        cpu_logits[:, i] = lg1[:, 0]
+    nxt, lg = lm.prefill(prompt, want_logits=True)
+    gpu_logits = [lg[check]]
+    feed = nxt.copy()
+    for s in range(1, steps):
+        feed[check] = cpu_ids[:, s - 1]  # teacher forcing on the checked sequences
+        nxt, lg = lm.decode(feed, want_logits=True)
+        gpu_logits.append(lg[check])
+        feed = nxt.copy()
+    close(np.stack(gpu_logits), cpu_logits)
+    return lm
+
+
+@pytest.mark.parametrize("kv_bf16", [0, 1])
+def test_split_decode_b16_h32(jas, kv_bf16):
+    """B = 16, H = 32, d_h 128 (the headline's attention shape, d_model 4096), fp32 and bf16
+    KV cache: a 1100-key cache gives two splits of the cache (the fp32 one: 2 x 576 keys),
+    and the 600-token prompt puts keys in both; the merge writes the packed operand of the
+    O projection.  Oracle on sequences 0 and 15 (fp32 cache) or 7 (bf16 cache)."""
+    cfg = jas.LmConfig(1, 2, 4096, 32, 64, 96, 1100, 16, 1e-6, 10000.0, 0, kv_bf16)
+    run_parity_subset(jas, cfg, seed=31, B=16, P=600, steps=3, prompt_seed=31, check=(7,) if kv_bf16 else (0, 15),
+                      want_splits=2)
+
+
+@pytest.mark.parametrize("kv_bf16", [0, 1])
+def test_split_decode_batch1_many_splits(jas, kv_bf16):
+    """Batch 1 at the LLaMA-7B head shape (32 heads of 128): a 2100-key cache is cut into
+    11 splits of 192 keys (the batch-1 headline), of which the 600-token prompt fills four."""
+    cfg = jas.LmConfig(1, 2, 4096, 32, 64, 96, 2100, 1, 1e-6, 10000.0, 0, kv_bf16)
+    run_parity_subset(jas, cfg, seed=32, B=1, P=600, steps=3, prompt_seed=32, check=(0,),
+                      want_splits=10)
+
+
+def test_split_decode_real_width_b16(jas):
+    """B = 16 at the full LLaMA-7B width (d 4096, 32 heads, SwiGLU 11008, vocab 32000),
+    2 layers, with the cache long enough for two attention splits; oracle on sequence 15
+    with a 560-token prompt (keys in both splits)."""
+    cfg = jas.LmConfig(1, 2, 4096, 32, 11008, 32000, 1100, 16, 1e-6, 10000.0)
+    run_parity_subset(jas, cfg, seed=4, B=16, P=560, steps=2, prompt_seed=4, check=(15,), want_splits=2)
+
+
+def test_split_decode_gpt2_kind(jas):
+    """The GPT-2 block (LayerNorm, GELU, biases, learned positions) through the split path:
+    B = 8, 12 heads of 64 with a cache above 1024 keys (the unsplit form stops there)."""
+    cfg = jas.LmConfig(0, 2, 768, 12, 256, 128, 1200, 8, 1e-5, 10000.0)
+    run_parity_subset(jas, cfg, seed=33, B=8, P=700, steps=3, prompt_seed=33, check=(0, 5), want_splits=2)
