@@ -223,6 +223,20 @@ jas_status jas_attn_decode(const float *d_q, const float *d_K, const float *d_V,
                            const int32_t *d_seqlens, int B, int H, int D, int max_len,
                            long k_sb, long k_sh, float scale, void *d_work, jas_stream_t stream);
 
+/* jas_attn_decode without a workspace and without any device allocation: no counterpart in
+ * the reference (jasmine allocates per matrix).  It is for callers that cannot allocate --
+ * code under HIP graph capture, serving loops, harnesses that forbid hipMalloc.  The split
+ * partials go to a static device array of jas_attn_decode_scratch_max() bytes (8 MiB) per
+ * GPU, held until the process ends; shapes whose partials
+ * (jas_attn_decode_workspace(B, H, D, max_len)) exceed it are rejected with JAS_ERR_INVALID.
+ * Every call on one GPU shares that array: calls that overlap on one GPU (two streams, or
+ * two host threads) race.  Results are identical to jas_attn_decode's. */
+#define JAS_DECODE_SCRATCH_BYTES ((size_t)8 << 20)
+size_t jas_attn_decode_scratch_max(void);
+jas_status jas_attn_decode_noalloc(const float *d_q, const float *d_K, const float *d_V, float *d_O,
+                                   const int32_t *d_seqlens, int B, int H, int D, int max_len,
+                                   long k_sb, long k_sh, float scale, jas_stream_t stream);
+
 /* ------------------------------------------------------------------ RoPE, embeddings, argmax */
 /* jasmine RoPE_net_t::forward (mat_RoPE_t.hpp:166-188) with mat_RoPE_t::init angles
  * (mat_RoPE_t.hpp:107-131); x, y row-major [d, T] feature-major. */

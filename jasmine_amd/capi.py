@@ -65,6 +65,7 @@ _sigs = {
     "jas_gemm_f64": [I, I, I, VP, L, L, VP, L, L, VP, L, L, VP, I, VP],
     "jas_attn_prefill": [VP, VP, VP, VP, I, I, I, I, I, L, L, L, L, L, L, L, L, L, C.c_float, I, I, VP],
     "jas_attn_decode": [VP, VP, VP, VP, VP, I, I, I, I, L, L, C.c_float, VP, VP],
+    "jas_attn_decode_noalloc": [VP, VP, VP, VP, VP, I, I, I, I, L, L, C.c_float, VP],
     "jas_rope_jasmine": [VP, VP, I, I, VP],
     "jas_rope_jasmine_f64": [VP, VP, I, I, VP],
     "jas_rope_llama": [VP, VP, I, I, I, L, C.c_float, VP],
@@ -95,6 +96,8 @@ lib.jas_ew_jit_mode.restype = C.c_int
 lib.jas_ew_jit_mode.argtypes = [C.c_int]
 lib.jas_attn_decode_workspace.restype = C.c_size_t
 lib.jas_attn_decode_workspace.argtypes = [I, I, I, I]
+lib.jas_attn_decode_scratch_max.restype = C.c_size_t
+lib.jas_attn_decode_scratch_max.argtypes = []
 lib.jas_lm_position.restype = I
 lib.jas_lm_position.argtypes = [VP]
 lib.jas_lm_attn_splits.restype = I
@@ -104,7 +107,7 @@ lib.jas_lm_stream.argtypes = [VP]
 
 # every symbol the C header declares (checked by the CPU test that the library exports them)
 EXPORTED = sorted(list(_sigs) + ["jas_last_error", "jas_version", "jas_default_stream",
-                                 "jas_attn_decode_workspace", "jas_ew_jit_mode", "jas_lm_position", "jas_lm_stream",
+                                 "jas_attn_decode_workspace", "jas_attn_decode_scratch_max", "jas_ew_jit_mode", "jas_lm_position", "jas_lm_stream",
                                  "jas_lm_attn_splits"])
 
 

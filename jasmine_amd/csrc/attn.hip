@@ -13,6 +13,7 @@
 #include "jas_common.hpp"
 
 #include <cfloat>
+#include <mutex>
 
 namespace jas {
 
@@ -707,6 +708,32 @@ jas_status attn_decode_impl(const float *q, const void *K, const void *V, float 
 }
 
 
+// Static scratch of the allocation-free decode entry point: the split partials live in a
+// file-scope device array (one copy per GPU, held until the process ends) instead of a
+// caller workspace.  Host code never passes the array's name to a kernel (on the host it is
+// only a stand-in for the symbol); its device address is looked up once per device with that
+// device current and kept here.
+static __device__ __align__(256) float scratch[JAS_DECODE_SCRATCH_BYTES / sizeof(float)];
+constexpr int MAX_DEVICES = 64;
+static void *scratch_dev_ptr[MAX_DEVICES];
+static std::mutex scratch_mu;
+
+static jas_status decode_scratch_ptr(void **out)
+{
+    int dev = 0;
+    JAS_HIP(hipGetDevice(&dev));
+    JAS_CHECK(dev >= 0 && dev < MAX_DEVICES, JAS_ERR_INVALID, "jas_attn_decode_noalloc: device index out of range");
+    std::lock_guard<std::mutex> g(scratch_mu);
+    if (!scratch_dev_ptr[dev]) {
+        void *ptr = nullptr;
+        JAS_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        JAS_CHECK(ptr, JAS_ERR_HIP, "jas_attn_decode_noalloc: no device address for the scratch array");
+        scratch_dev_ptr[dev] = ptr;
+    }
+    *out = scratch_dev_ptr[dev];
+    return JAS_OK;
+}
+
 } // namespace jas
 
 using namespace jas;
@@ -788,6 +815,24 @@ jas_status jas_attn_decode(const float *q, const float *K, const float *V, float
                            int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work,
                            jas_stream_t stream)
 {
+    return attn_decode_impl(q, K, V, O, seqlens, B, H, D, max_len, k_sb, k_sh, scale, work, stream_or_default(stream), 0);
+}
+
+size_t jas_attn_decode_scratch_max(void) { return JAS_DECODE_SCRATCH_BYTES; }
+
+jas_status jas_attn_decode_noalloc(const float *q, const float *K, const float *V, float *O, const int32_t *seqlens,
+                                   int B, int H, int D, int max_len, long k_sb, long k_sh, float scale,
+                                   jas_stream_t stream)
+{
+    const size_t need = jas_attn_decode_workspace(B, H, D, max_len);
+    JAS_CHECK(need <= JAS_DECODE_SCRATCH_BYTES, JAS_ERR_INVALID,
+              "jas_attn_decode_noalloc: split partials exceed the static scratch (B*H*splits*(D+2)*4 > "
+              "jas_attn_decode_scratch_max()); use jas_attn_decode with a workspace");
+    void *work = nullptr;
+    if (need) {
+        const jas_status st = decode_scratch_ptr(&work);
+        if (st != JAS_OK) return st;
+    }
     return attn_decode_impl(q, K, V, O, seqlens, B, H, D, max_len, k_sb, k_sh, scale, work, stream_or_default(stream), 0);
 }
 
