@@ -242,6 +242,19 @@ def run_kernel_legs(jas, reps=10):
                                                        C.c_float(0.125), ws.p, None)), reps * 5)
     out["attn_decode_f32"] = line("attn_decode_kernel<64> + merge, 1 query over 1024 cached keys, B8 H12",
                                   ms, 2 * ne * 4)
+    del Q, K, V, O
+
+    # mat_dot_t / weight_net_t products (mat_express_t.hpp:730-736): row-major fp32 A [M][K]
+    # times B [K][N] into C [M][N], on gemm_dma_kernel
+    for nn in (1024, 4096):
+        Ga, Gb, Gc = (jas.DeviceArray((nn, nn)) for _ in range(3))
+        chk(lib.jas_fill_normal(Ga.p, nn * nn, 5, 0, 0.0, 1.0, None))
+        chk(lib.jas_fill_normal(Gb.p, nn * nn, 5, 1, 0.0, 1.0, None))
+        ms = time_launches(lambda: chk(lib.jas_gemm(nn, nn, nn, Ga.p, nn, 1, Gb.p, nn, 1, Gc.p, nn, 1, None, 0, 0, 0,
+                                                    1, 0, 0, 0, 0, None)), reps * 2)
+        out[f"gemm_{nn}"] = line(f"gemm_dma_kernel fp32, row-major {nn}^3 (mat_dot_t)", ms, None, "mfma",
+                                 2.0 * nn ** 3, FP32_MFMA_TFLOPS)
+        del Ga, Gb, Gc
     return out
 
 

@@ -280,12 +280,382 @@ static int pick_mode(const float *X, long so, long sk, int O, int K, long bstrid
     return LM_GEN;
 }
 
+// ---------------------------------------------------------------- direct-to-LDS GEMM
+// The main fp32 GEMM for operands that are contiguous in one dimension.  K slabs of
+// 16 * KB are moved from global memory straight into LDS (global_load_lds_dwordx4: each
+// wave instruction writes 64 lanes x 16 B contiguously at a wave-uniform LDS base), so no
+// register staging and no LDS store instructions sit in the loop.  ST stage buffers keep
+// ST - 1 slabs in flight; one barrier per slab.
+//
+// LDS layouts, chosen so that every fragment read is one conflict-free ds_read_b128:
+//  * K-contiguous operand X(o, k) (and the packed weight layout): per 16 x 16 block, the 64
+//    lanes' float4s in MFMA operand order -- lane r + 16 g holds X(16 b + r, 4 g .. 4 g + 3).
+//    Sub-step t of the four 16x16x4 MFMAs per block takes element t, so k-slot g of
+//    sub-step t is k = 4 g + t, a permutation of K applied to both operands alike.
+//  * Outer-contiguous operand: rows [k][o] as in memory.  Lane (g, r) reads the float4
+//    X(o0 + 4 r .. 4 r + 3, k = 4 g + t): its four elements feed four different 16-wide
+//    blocks (block e takes outer index 4 r + e), so one read serves four MFMAs, and the
+//    output of those blocks comes out as four consecutive columns per lane.
+// The compiler cannot see the LDS writes of the DMA (they are issued as asm, so its
+// wait-count pass does not serialise the LDS reads behind every load in flight); the loop
+// waits on vmcnt itself before each barrier.
+enum DmaMode : int { DM_KC = 0, DM_OC = 1, DM_PK = 2 };
+
+struct DmaArgs {
+    const float *A, *B;
+    float *C;
+    const float *bias;
+    long as0, as1, bs0, bs1, cs0, cs1;
+    long abs_, bbs, cbs, biasbs;
+    int M, N, K;
+    int bias_mode, act, accumulate;
+    int c_vec;  // 1: row-major C with float4 stores over n; 2: column-major C, float4 over m
+};
+
+// M0 is a reserved register to the compiler; nothing else in these kernels uses it (no
+// relative register indexing, no other LDS DMA), which the AMD assembly of the build shows.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const float *src, float *lds_dst)
+{
+    const unsigned la = (unsigned)(size_t)(__attribute__((address_space(3))) float *)lds_dst;
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(la), "v"(src) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Global address of lane `lane`'s 16 bytes for DMA instruction `ins` of the slab at k0, and
+// whether the slab element group lies inside K (only the tail slab can leave K).
+// X(o, k) = X[o * so + k * sk]; Olim = rows (outer extent); RG = packed row tiles.
+template <int MODE, int O, int KWT>
+__device__ __forceinline__ const float *dma_src(const float *X, long so, long sk, int o0, int Olim, int K, int k0,
+                                                int ins, int lane, int &kfirst)
+{
+    if (MODE == DM_OC) {
+        const int f = 256 * ins + 4 * lane, k = k0 + f / O;
+        int o = o0 + f % O;
+        o = o <= Olim - 4 ? o : Olim - 4;  // clamped groups only feed discarded outputs
+        kfirst = k;
+        return X + (long)(k < K ? k : K - 1) * sk + o;
+    }
+    constexpr int RB = O / 16;
+    const int kb = ins / RB, rb = ins % RB;
+    if (MODE == DM_PK) {
+        const long RG = (Olim + 15) >> 4;
+        const long rt = min((long)(o0 >> 4) + rb, RG - 1);
+        const int kblk = (k0 >> 4) + kb;
+        kfirst = 16 * kblk;
+        return X + weight_tile_offset(rt, kblk < (K >> 4) ? kblk : (K >> 4) - 1, K >> 4, RG) + lane * 4;
+    }
+    int o = o0 + 16 * rb + (lane & 15);
+    o = o < Olim ? o : Olim - 1;
+    kfirst = k0 + 16 * kb + 4 * (lane >> 4);
+    return X + (long)o * so + (kfirst < K ? kfirst : 0);
+}
+
+template <int MODE, int O, int KWT, int NW>
+__device__ __forceinline__ void dma_slab(const float *X, long so, long sk, int o0, int Olim, int K, int k0, float *lds,
+                                         int w, int lane)
+{
+    constexpr int NI = O * KWT / 256;  // 1 KB instructions per slab
+    static_assert(NI % NW == 0, "slab instructions spread evenly over the waves");
+#pragma unroll
+    for (int q = 0; q < NI / NW; ++q) {
+        const int ins = w * (NI / NW) + q;  // wave-uniform
+        int kf;
+        lds_dma16(dma_src<MODE, O, KWT>(X, so, sk, o0, Olim, K, k0, ins, lane, kf), lds + 256 * ins);
+    }
+}
+
+// The last, partial slab (K % (16 KB) != 0): ordinary loads with zeros past K, stored in the
+// same layout.
+template <int MODE, int O, int KWT, int NW>
+__device__ __forceinline__ void tail_slab(const float *X, long so, long sk, int o0, int Olim, int K, int k0, float *lds,
+                                          int w, int lane)
+{
+    constexpr int NI = O * KWT / 256;
+#pragma unroll
+    for (int q = 0; q < NI / NW; ++q) {
+        const int ins = w * (NI / NW) + q;
+        int kf;
+        const float *src = dma_src<MODE, O, KWT>(X, so, sk, o0, Olim, K, k0, ins, lane, kf);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (MODE == DM_KC) {  // per element: K need not be a multiple of 4
+            float e[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) e[u] = kf + u < K ? src[u] : 0.f;
+            v = make_float4(e[0], e[1], e[2], e[3]);
+        } else if (kf < K) {
+            v = *(const float4 *)src;
+        }
+        *(float4 *)(lds + 256 * ins + 4 * lane) = v;
+    }
+}
+
+// Fragment values of sub-step t of 16-block kb for the NB blocks of this wave
+// (outer offset woff within the tile).
+template <int MODE, int NB, int O>
+__device__ __forceinline__ void dma_frag(const float *s, int kb, int t, int woff, int lane, float (&v)[NB],
+                                         float4 (&blk)[NB])
+{
+    const int r16 = lane & 15, g = lane >> 4;
+    if (MODE != DM_OC) {
+        if (t == 0) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) blk[i] = *(const float4 *)(s + (kb * (O / 16) + woff / 16 + i) * 256 + lane * 4);
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) v[i] = blk[i][t];
+    } else {
+        constexpr int G = NB < 4 ? NB : 4;
+        const float *row = s + (16 * kb + 4 * g + t) * O + woff;
+#pragma unroll
+        for (int q = 0; q < NB / G; ++q) {
+            if constexpr (G == 4) {
+                const float4 x = *(const float4 *)(row + 64 * q + 4 * r16);
+                v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+            } else if constexpr (G == 2) {
+                const float2 x = *(const float2 *)(row + 32 * q + 2 * r16);
+                v[2 * q] = x.x; v[2 * q + 1] = x.y;
+            } else {
+                v[q] = row[16 * q + r16];
+            }
+        }
+    }
+}
+
+// outer index (within the wave tile) of MFMA row/column ii of block i
+template <int MODE, int NB>
+__device__ __forceinline__ int dma_outer(int i, int ii)
+{
+    constexpr int G = NB < 4 ? NB : 4;
+    return MODE != DM_OC ? 16 * i + ii : 16 * G * (i / G) + G * ii + (i % G);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier()
+{
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// TM x TN tile, NW waves in a WGM x (NW / WGM) grid, ST stages of 16 * KB wide K slabs.
+// Workgroup ids are remapped so that each of the 8 XCDs (ids go round-robin over them)
+// works on a contiguous range of tiles, walked 4 tile rows at a time: the A rows and B
+// columns its workgroups share stay in that XCD's L2.
+template <int AM, int BM, int TM, int TN, int NW, int WGM, int ST, int KB>
+__global__ void __launch_bounds__(NW * 64) gemm_dma_kernel(const DmaArgs p)
+{
+    constexpr int WGN = NW / WGM, WTM = TM / WGM, WTN = TN / WGN, NBI = WTM / 16, NBJ = WTN / 16;
+    constexpr int KWT = 16 * KB, SA = TM * KWT, SB = TN * KWT;
+    constexpr int PER = (SA / 256 + SB / 256) / NW;  // DMA instructions per thread and slab
+    static_assert(PER * (ST - 2) <= 63, "vmcnt range");
+    static_assert(AM != DM_OC || NBI % 4 == 0 || NBI < 4, "outer-contiguous groups");
+    __shared__ __attribute__((aligned(1024))) float lds[ST * (SA + SB)];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = w / WGN, wn = w % WGN, r16 = lane & 15, g = lane >> 4;
+
+    int bx = blockIdx.x, by = blockIdx.y;
+    {
+        constexpr int XG = 4;
+        const int gx = gridDim.x, nt = gx * gridDim.y, per = nt / 8;
+        const int id = blockIdx.y * gx + blockIdx.x;
+        // a permutation of the ids: the first 8 * per go XCD-contiguous, the rest stay
+        const int lid = id < 8 * per ? (id % 8) * per + id / 8 : id;
+        const int grp = lid / (XG * gx), gy0 = grp * XG, rows = min(XG, (int)gridDim.y - gy0);
+        const int in = lid - grp * XG * gx;
+        by = gy0 + in % rows;
+        bx = in / rows;
+    }
+    const int m0 = by * TM, n0 = bx * TN;
+    const long bz = blockIdx.z;
+    const float *A = p.A + bz * p.abs_;
+    const float *B = p.B + bz * p.bbs;
+    const int K = p.K, nk = K / KWT;
+    const bool tail = nk * KWT < K;
+
+    auto issue = [&](int kt) {
+        float *sa = lds + (kt % ST) * (SA + SB), *sb = sa + SA;
+        dma_slab<AM, TM, KWT, NW>(A, p.as0, p.as1, m0, p.M, K, kt * KWT, sa, w, lane);
+        dma_slab<BM, TN, KWT, NW>(B, p.bs1, p.bs0, n0, p.N, K, kt * KWT, sb, w, lane);
+    };
+    floatx4 acc[NBI][NBJ];
+#pragma unroll
+    for (int i = 0; i < NBI; ++i)
+#pragma unroll
+        for (int j = 0; j < NBJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    auto compute = [&](const float *sa) {
+        const float *sb = sa + SA;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            float4 ablk[NBI], bblk[NBJ];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                float av[NBI], bv[NBJ];
+                dma_frag<AM, NBI, TM>(sa, kb, t, wm * WTM, lane, av, ablk);
+                dma_frag<BM, NBJ, TN>(sb, kb, t, wn * WTN, lane, bv, bblk);
+#pragma unroll
+                for (int i = 0; i < NBI; ++i)
+#pragma unroll
+                    for (int j = 0; j < NBJ; ++j) acc[i][j] = mfma4(av[i], bv[j], acc[i][j]);
+            }
+        }
+    };
+
+#pragma unroll
+    for (int s = 0; s < ST - 1; ++s)
+        if (s < nk) issue(s);
+    for (int kt = 0; kt < nk; ++kt) {
+        // slab kt has landed (this thread's loads: the later slabs may still be in flight);
+        // the barrier makes every wave's part visible and retires the reads of the buffer
+        // the next issue overwrites (last read in iteration kt - 1)
+        const int ahead = min(ST - 2, nk - 1 - kt);
+        if (ahead >= 2) wait_vm_barrier<2 * PER>();
+        else if (ahead == 1) wait_vm_barrier<PER>();
+        else wait_vm_barrier<0>();
+        if (kt + ST - 1 < nk) issue(kt + ST - 1);
+        compute(lds + (kt % ST) * (SA + SB));
+    }
+    if (tail) {
+        // stage nk % ST was last read in iteration nk - ST, which every wave finished before
+        // the barrier of iteration nk - 1
+        float *sa = lds + (nk % ST) * (SA + SB), *sb = sa + SA;
+        tail_slab<AM, TM, KWT, NW>(A, p.as0, p.as1, m0, p.M, K, nk * KWT, sa, w, lane);
+        tail_slab<BM, TN, KWT, NW>(B, p.bs1, p.bs0, n0, p.N, K, nk * KWT, sb, w, lane);
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        compute(sa);
+    }
+
+    // epilogue: block (i, j), lane (g, r16), register r holds MFMA row 4 g + r, column r16
+    float *C = p.C + bz * p.cbs;
+    const float *bias = p.bias ? p.bias + bz * p.biasbs : nullptr;
+    auto finish = [&](float x, int m, int n, float *cp) {
+        if (bias) x = x + (p.bias_mode == 1 ? bias[m] : bias[n]);
+        x = apply_act(x, p.act);
+        return p.accumulate ? *cp + x : x;
+    };
+    const int mw = m0 + wm * WTM, nw = n0 + wn * WTN;
+    if (BM == DM_OC && NBJ >= 4 && p.c_vec == 1) {  // row-major C: four consecutive n per lane
+#pragma unroll
+        for (int i = 0; i < NBI; ++i)
+#pragma unroll
+            for (int q = 0; q < NBJ / 4; ++q)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = mw + dma_outer<AM, NBI>(i, 4 * g + r), n = nw + 64 * q + 4 * r16;
+                    if (m >= p.M || n >= p.N) continue;
+                    float *cp = C + (long)m * p.cs0 + n;
+                    float4 o;
+                    o.x = finish(acc[i][4 * q][r], m, n, cp);
+                    o.y = finish(acc[i][4 * q + 1][r], m, n + 1, cp + 1);
+                    o.z = finish(acc[i][4 * q + 2][r], m, n + 2, cp + 2);
+                    o.w = finish(acc[i][4 * q + 3][r], m, n + 3, cp + 3);
+                    *(float4 *)cp = o;
+                }
+    } else if (AM != DM_OC && p.c_vec == 2) {  // column-major C: four consecutive m per lane
+#pragma unroll
+        for (int i = 0; i < NBI; ++i)
+#pragma unroll
+            for (int j = 0; j < NBJ; ++j) {
+                const int m = mw + 16 * i + 4 * g, n = nw + dma_outer<BM, NBJ>(j, r16);
+                if (n >= p.N || m >= p.M) continue;
+                float *cp = C + m + (long)n * p.cs1;
+                if (m + 3 < p.M) {
+                    float4 o;
+                    o.x = finish(acc[i][j][0], m, n, cp);
+                    o.y = finish(acc[i][j][1], m + 1, n, cp + 1);
+                    o.z = finish(acc[i][j][2], m + 2, n, cp + 2);
+                    o.w = finish(acc[i][j][3], m + 3, n, cp + 3);
+                    *(float4 *)cp = o;
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (m + r < p.M) cp[r] = finish(acc[i][j][r], m + r, n, cp + r);
+                }
+            }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NBI; ++i)
+#pragma unroll
+            for (int j = 0; j < NBJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = mw + dma_outer<AM, NBI>(i, 4 * g + r), n = nw + dma_outer<BM, NBJ>(j, r16);
+                    if (m >= p.M || n >= p.N) continue;
+                    float *cp = C + (long)m * p.cs0 + (long)n * p.cs1;
+                    *cp = finish(acc[i][j][r], m, n, cp);
+                }
+    }
+}
+
+// Geometry: 256 x 256 tiles (8 waves, 3 stages) when they give every CU a workgroup,
+// else 128 x 128 (4 waves, 4 stages), else 64 x 64 (4 waves, 4 stages of 32-wide slabs).
+// MI355X, fp32: 4096^3 at 134-137 TFLOP/s, 2048^3 at 116, 1024^3 at 88.
+template <int AM, int BM>
+static void launch_dma(const DmaArgs &p, int batch, hipStream_t s)
+{
+    auto tiles = [&](int t) { return (long)ceil_div(p.M, t) * ceil_div(p.N, t) * batch; };
+    if (tiles(256) >= 256) {
+        const dim3 grid(ceil_div(p.N, 256), ceil_div(p.M, 256), batch);
+        hipLaunchKernelGGL((gemm_dma_kernel<AM, BM, 256, 256, 8, 2, 3, 1>), grid, dim3(512), 0, s, p);
+    } else if (tiles(128) >= 256) {
+        const dim3 grid(ceil_div(p.N, 128), ceil_div(p.M, 128), batch);
+        hipLaunchKernelGGL((gemm_dma_kernel<AM, BM, 128, 128, 4, 2, 4, 1>), grid, dim3(256), 0, s, p);
+    } else {
+        const dim3 grid(ceil_div(p.N, 64), ceil_div(p.M, 64), batch);
+        hipLaunchKernelGGL((gemm_dma_kernel<AM, BM, 64, 64, 4, 2, 4, 2>), grid, dim3(256), 0, s, p);
+    }
+}
+
+// DMA load mode of operand X(o, k) = X[o * so + k * sk] (batch stride bst), or -1
+static int dma_mode(const float *X, long so, long sk, int O, long bst)
+{
+    if (((uintptr_t)X & 15) || bst % 4) return -1;
+    if (sk == 1 && so % 4 == 0) return DM_KC;
+    if (so == 1 && sk % 4 == 0 && O % 4 == 0) return DM_OC;
+    return -1;
+}
+
+static bool gemm_dma(int M, int N, int K, const void *A, long as0, long as1, const float *B, long bs0, long bs1,
+                     float *C, long cs0, long cs1, const float *bias, int bias_mode, int act, int accumulate, int batch,
+                     long abs_, long bbs, long cbs, long biasbs, hipStream_t s, bool a_packed, bool a_bf16)
+{
+    if (a_bf16 || K <= 0) return false;
+    int am = a_packed ? DM_PK : dma_mode((const float *)A, as0, as1, M, abs_);
+    if (a_packed && (((uintptr_t)A & 15) || K % 16 || batch != 1)) return false;
+    const int bm = dma_mode(B, bs1, bs0, N, bbs);
+    if (am < 0 || bm < 0) return false;
+    DmaArgs p;
+    p.A = (const float *)A; p.B = B; p.C = C; p.bias = bias_mode ? bias : nullptr;
+    p.as0 = as0; p.as1 = as1; p.bs0 = bs0; p.bs1 = bs1; p.cs0 = cs0; p.cs1 = cs1;
+    p.abs_ = abs_; p.bbs = bbs; p.cbs = cbs; p.biasbs = biasbs;
+    p.M = M; p.N = N; p.K = K;
+    p.bias_mode = bias_mode; p.act = act; p.accumulate = accumulate;
+    const bool ca = ((uintptr_t)C & 15) == 0 && cbs % 4 == 0;
+    p.c_vec = 0;
+    if (ca && cs1 == 1 && cs0 % 4 == 0 && N % 4 == 0) p.c_vec = 1;
+    else if (ca && cs0 == 1 && cs1 % 4 == 0) p.c_vec = 2;
+#define JAS_DMA_B(AMV)                                                                                 \
+    if (bm == DM_KC) launch_dma<AMV, DM_KC>(p, batch, s);                                             \
+    else launch_dma<AMV, DM_OC>(p, batch, s);
+    if (am == DM_PK) { JAS_DMA_B(DM_PK) }
+    else if (am == DM_KC) { JAS_DMA_B(DM_KC) }
+    else { JAS_DMA_B(DM_OC) }
+#undef JAS_DMA_B
+    return true;
+}
+
 jas_status gemm_general(int M, int N, int K, const void *A, long as0, long as1, const float *B, long bs0, long bs1,
                         float *C, long cs0, long cs1, const float *bias, int bias_mode, int act, int accumulate,
                         int batch, long abs_, long bbs, long cbs, long biasbs, hipStream_t s, bool a_packed,
                         bool a_bf16)
 {
     JAS_CHECK(!a_bf16 || a_packed, JAS_ERR_INVALID, "gemm: bf16 A only in the packed layout");
+    JAS_CHECK(!a_packed || (K % 16 == 0 && batch == 1), JAS_ERR_INVALID, "gemm: packed A needs K % 16 == 0");
+    if (gemm_dma(M, N, K, A, as0, as1, B, bs0, bs1, C, cs0, cs1, bias, bias_mode, act, accumulate, batch, abs_, bbs,
+                 cbs, biasbs, s, a_packed, a_bf16)) {
+        JAS_LAUNCH_CHECK();
+        return JAS_OK;
+    }
     TileArgs p;
     p.A = (const float *)A; p.B = B; p.C = C; p.bias = bias_mode ? bias : nullptr;
     p.as0 = as0; p.as1 = as1; p.bs0 = bs0; p.bs1 = bs1; p.cs0 = cs0; p.cs1 = cs1;
@@ -882,12 +1252,6 @@ extern "C" jas_status jas_gemm(int M, int N, int K, const float *A, long as0, lo
         e.out = C;
         e.ldo = cs1;
         return skinny_gemm(A, nullptr, B, bs1, M, N, K, e, s, false, nullptr);
-    }
-    // plain products of library size: rocBLAS (see blas.cpp)
-    if (blas_gemm(M, N, K, A, as0, as1, B, bs0, bs1, C, cs0, cs1, bias, bias_mode, act, accumulate, batch, abs_, bbs,
-                  cbs, biasbs, s)) {
-        JAS_LAUNCH_CHECK();
-        return JAS_OK;
     }
     return gemm_general(M, N, K, A, as0, as1, B, bs0, bs1, C, cs0, cs1, bias, bias_mode, act, accumulate, batch, abs_,
                         bbs, cbs, biasbs, s, false);

@@ -27,10 +27,6 @@ jas_status attn_decode_impl(const float *q, const void *K, const void *V, float 
 // key splits attn_decode_impl launches for this shape (1: no merge launch; 0: bad shape)
 int attn_decode_splits(int B, int H, int D, int max_len, bool kv_bf16, bool wide);
 
-// jas_gemm's plain products on rocBLAS; false = not taken (the caller runs its own kernel)
-bool blas_gemm(int M, int N, int K, const float *A, long as0, long as1, const float *B, long bs0, long bs1, float *C,
-               long cs0, long cs1, const float *bias, int bias_mode, int act, int accumulate, int batch, long abs_,
-               long bbs, long cbs, long biasbs, hipStream_t s);
 
 // two-pass row argmax with caller-provided scratch of argmax_workspace_bytes(n, V) bytes
 size_t argmax_workspace_bytes(int n, int V);

@@ -53,11 +53,31 @@ class EventTimer:
                     _hip.hipEventDestroy(e)
 
 
-def time_launches(fn, reps, warmup=2, stream=None):
-    """Average GPU milliseconds per call of fn() (each call enqueues the launches to time)."""
+_gate_buf = None
+
+
+def busy_gate(stream=None, elems=1 << 28):
+    """Enqueue about a millisecond of device work (a seeded normal fill of `elems` floats)
+    so that launches enqueued right after it queue up behind it and then run back to back:
+    the events that follow measure device time, not the host's launch rate."""
+    global _gate_buf
+    if _gate_buf is None:
+        p = C.c_void_p()
+        _ok(lib.jas_malloc(C.byref(p), elems * 4), "jas_malloc")
+        _gate_buf = p
+    _ok(lib.jas_fill_normal(_gate_buf, elems, 0, 0, C.c_float(0.0), C.c_float(1.0),
+                            stream if stream is not None else None), "jas_fill_normal")
+
+
+def time_launches(fn, reps, warmup=2, stream=None, gate=True):
+    """Average GPU milliseconds per call of fn() (each call enqueues the launches to time).
+    With `gate`, the timed launches are queued behind busy_gate(), so short kernels are timed
+    back to back instead of at the host's launch rate."""
     for _ in range(warmup):
         fn()
     t = EventTimer(stream)
+    if gate:
+        busy_gate(stream)
     t.start()
     for _ in range(reps):
         fn()

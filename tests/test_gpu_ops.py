@@ -308,12 +308,37 @@ def test_gemm_epilogues(jas, bias_mode, act, acc, batch):
 @pytest.mark.parametrize("ta,tb,col_c", [(0, 0, 0), (1, 0, 0), (0, 1, 0), (1, 1, 1), (0, 0, 1), (1, 0, 1)])
 @pytest.mark.parametrize("bias_mode,acc,batch", [(0, 0, 1), (1, 0, 2), (2, 0, 1), (0, 1, 3)])
 def test_gemm_library_sizes(jas, ta, tb, col_c, bias_mode, acc, batch):
-    """Plain products of at least 256 x 256 x 128 go to the BLAS library (no activation, no
-    bias together with accumulation); every operand layout, both bias modes, batches."""
+    """Library-size products on the direct-to-LDS kernel (gemm_dma_kernel): every operand
+    layout, both bias modes, accumulation, batches; K of 200 and 129 leave a partial slab."""
     _gemm_case(jas, 300, 260, 200, ta=bool(ta), tb=bool(tb), col_c=bool(col_c), bias_mode=bias_mode, acc=bool(acc),
                batch=batch)
     _gemm_case(jas, 257, 513, 129, ta=bool(ta), tb=bool(tb), col_c=bool(col_c), bias_mode=bias_mode, acc=bool(acc),
                batch=batch, seed=1)
+
+
+@pytest.mark.parametrize("ta,tb,col_c", [(0, 0, 0), (1, 1, 0), (0, 1, 1), (1, 0, 1)])
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 40), (2048, 2100, 70), (1024, 1024, 1024)])
+def test_gemm_dma_geometries(jas, ta, tb, col_c, M, N, K):
+    """The three tile geometries of the direct-to-LDS kernel (256 x 256 with 8 waves when they
+    give every CU a workgroup, 128 x 128, 64 x 64) over every operand layout, with ragged M/N
+    edges and partial K slabs."""
+    _gemm_case(jas, M, N, K, ta=bool(ta), tb=bool(tb), col_c=bool(col_c), bias_mode=1, acc=True)
+
+
+def test_gemm_dma_k_tail_padded_rows(jas):
+    """K not a multiple of 4 with 16-byte aligned, padded rows (K-contiguous operands take the
+    direct-to-LDS path): the tail slab reads element by element and zero-fills past K."""
+    M, N, K, Kp = 300, 260, 147, 152
+    A = np.zeros((M, Kp), np.float32)
+    Bt = np.zeros((N, Kp), np.float32)
+    A[:, :K] = normal((M, K), 36, 0)
+    Bt[:, :K] = normal((N, K), 36, 1)
+    A[:, K:] = np.nan  # padding must never be read
+    Bt[:, K:] = np.nan
+    dA, dB, dC = jas.to_device(A), jas.to_device(Bt), jas.DeviceArray((M, N))
+    jas.check(jas.lib.jas_gemm(M, N, K, dA.p, Kp, 1, dB.p, 1, Kp, dC.p, N, 1, None, 0, 0, 0, 1, 0, 0, 0, 0, None))
+    ref = A[:, :K].astype(np.float64) @ Bt[:, :K].astype(np.float64).T
+    close(dC.numpy(), ref.astype(np.float32), atol=1e-5 * np.sqrt(K) + 1e-5, rtol=1e-5)
 
 
 @pytest.mark.parametrize("N", [1, 2, 5, 8, 16])
