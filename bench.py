@@ -14,8 +14,9 @@ length).  One step = one token for each of the 16 sequences through the whole mo
 from a second timed pass of K steps (positions right after the first) with HIP events
 recorded around every launch on the runner's stream: per-launch events serialise the
 queue and cost ~13% of step time, so they are kept out of the headline number.  cpu_baseline times the jasmine
-reference itself (oracle/_ref, its weight_net_t::forward at the real 4096x4096 projection
-shape, 16 columns) on one host core and extrapolates by FLOPs to a whole decode step.
+reference itself (oracle/_ref, one host core) on one decode layer of one sequence at the real
+shape and the LM-head GEMV, and extrapolates to a step of 16 sequences x 32 layers; cpu_configs
+holds its config 2 / 3 timings.
 """
 import argparse
 import json
@@ -89,42 +90,67 @@ def weight_bytes_per_step(L, d, F, V):
     return 4 * (L * (3 * d * d + d * d + 3 * d * F) + V * d)
 
 
-def cpu_baseline(step_flops, B):
-    """Time the reference CPU path (jasmine compiled from its sources) on a bounded sample."""
+def host_cpu():
+    """Host CPU model and the logical CPUs this process may use."""
+    model = "unknown"
     try:
-        from oracle_lib import ref, orc
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return model, n
+
+
+def cpu_baseline(B, ctx):
+    """The reference CPU path (jasmine compiled from its own sources into oracle/_ref, -O2,
+    one thread: the reference has no threading), timed on bounded samples at the real
+    shapes and extrapolated:
+      * one LLaMA-7B layer of one sequence's decode step over a `ctx`-key cache (seven
+        weight_net_t::forward GEMVs, per-head mat_dot_t scores, hsoftmax, V P^T) and the
+        32000 x 4096 LM-head GEMV; a step of B sequences costs B x (32 layers + head), since
+        jasmine's mat_dot_t streams the weight once per output column;
+      * config 2: the fused expression and hsoftmax at the full 8192^2;
+      * config 3: one causal head (S 1024, D 64) of scores, mask, softmax and weighted sum,
+        times the 96 heads.
+    About 20 s of CPU work.  Returns (headline dict, per-config dict) or (None, None)."""
+    import ctypes as C
+    try:
+        from oracle_lib import ref
     except Exception as e:  # pragma: no cover
         log("cpu baseline unavailable:", e)
-        return None
-    out, inn, T = 4096, 4096, B
-    flops_one = 2.0 * out * inn * T
-    if ref is not None:
-        kind, fn = "reference", lambda: ref.ref_time_linear(out, inn, T, 1)
-        what = "jasmine weight_net_t::forward (oracle/_ref, -O2, 1 thread)"
-    else:
-        import ctypes
-        import numpy as np
-        W = np.full((out, inn), 0.01, np.float32)
-        X = np.full((inn, T), 0.02, np.float32)
-        Y = np.zeros((out, T), np.float32)
-        from oracle_lib import fp
-
-        def fn():
-            t0 = time.perf_counter()
-            orc.orc_linear(fp(W), None, fp(X), out, inn, T, fp(Y))
-            return time.perf_counter() - t0
-        kind, what = "port", "oracle orc_linear (C restatement, 1 thread)"
-    t_total, reps = 0.0, 0
-    while t_total < 8.0 and reps < 8:
-        t_total += fn()
-        reps += 1
-    per = t_total / reps
-    rate = flops_one / per
-    step_s = step_flops / rate
-    return {"value": B / step_s, "unit": "tok/s", "cores": 1, "kind": kind,
-            "sample": f"{what} at W[4096x4096] x X[4096x{T}] ({reps} reps, {t_total:.1f} s, "
-                      f"{rate / 1e9:.3f} GFLOP/s), extrapolated by FLOPs to one decode step "
-                      f"({step_flops / 1e9:.1f} GFLOP: all projections + attention + LM head)"}
+        return None, None
+    if ref is None:
+        log("cpu baseline unavailable: oracle/_ref/libjasref.so not built")
+        return None, None
+    model, ncpu = host_cpu()
+    attn = C.c_double()
+    t_layer = ref.ref_time_llama_layer(4096, 32, 11008, ctx, C.byref(attn))
+    t_head = ref.ref_time_linear(32000, 4096, 1, 1)
+    step_s = B * (32 * t_layer + t_head)
+    head = {"value": round(B / step_s, 6), "unit": "tok/s", "cores": 1, "kind": "reference",
+            "host_cpu": model, "host_logical_cpus": ncpu,
+            "sample": f"jasmine (oracle/_ref, g++ -O2, 1 thread) at the config-5 shape: one decode layer of one "
+                      f"sequence over a {ctx}-key cache {t_layer:.2f} s (attention {attn.value:.2f} s), LM-head "
+                      f"GEMV {t_head:.2f} s; extrapolated to a step of {B} sequences x 32 layers "
+                      f"({step_s:.0f} s per step). jasmine itself has no KV cache: its decode loop recomputes the "
+                      f"prefix, which at this context would cost a full prefill per token"}
+    per = {}
+    try:
+        t_expr = ref.ref_time_cfg2(8192, 8192, 1)
+        t_sm = ref.ref_time_hsoftmax(8192, 8192, 1)
+        t_ah = ref.ref_time_attention_head(64, 1024)
+        per = {"config2_expr_s": round(t_expr, 3), "config2_hsoftmax_s": round(t_sm, 3),
+               "config2_expr_gbs": round(4 * 8192 * 8192 * 4 / t_expr / 1e9, 3),
+               "config3_causal_attention_s": round(96 * t_ah, 2),
+               "config3_note": "one head timed (scores, mask, hsoftmax, V P^T of mat_head_gen_t), x 96 heads",
+               "config5_layer_s": round(t_layer, 3), "config5_lm_head_s": round(t_head, 3),
+               "cores": 1, "host_cpu": model}
+    except Exception as e:  # pragma: no cover
+        log("[bench] cpu config lines failed:", e)
+    return head, per
 
 
 def gpt2_decode_bytes(L, d, F, V, B, ctx):
@@ -299,6 +325,8 @@ def summarize_pmc(fetch_csv, write_csv, cfetch_csv, cwrite_csv, args):
     B, H, dh = args.batch, 32, 128
     out["algorithmic"] = {"attention": B * H * profiled_mean_ctx(args) * dh * 8, "weight_gemm": None}
     out["run"] = {"batch": B, "prompt": args.prompt, "steps": args.steps, "warmup": args.warmup}
+    out["shape"] = {"batch": B, "heads": H, "head_dim": dh, "kv": "f32"}
+    out["mean_ctx"] = profiled_mean_ctx(args)
     return out
 
 
@@ -358,17 +386,28 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": COPY_BYTES, "repeats": 5}))
 
 
-def load_traffic(args, dom_kernel_class):
-    """Measured HBM bytes per launch of the dominant class, if a summary for this exact
-    workload (batch, prompt, steps, warmup) was committed; else None."""
+def load_traffic(args, dom_kernel_class, bytes_per_launch):
+    """Measured HBM bytes per launch of the dominant class, scaled to this run.  The committed
+    summary holds FETCH_SIZE + WRITE_SIZE per launch for a counter run of the same kernels at
+    the same per-launch shape (batch, heads, head dim, cache element type) and its algorithmic
+    bytes; the measured/algorithmic ratio is applied to this run's algorithmic bytes per
+    launch (the context length only scales both).  None if no summary matches the shape."""
     try:
         t = json.load(open(TRAFFIC_FILE))
     except (OSError, ValueError):
-        return None
-    if t.get("run") != {"batch": args.batch, "prompt": args.prompt, "steps": args.steps, "warmup": args.warmup}:
-        return None
+        return None, None
+    shape = t.get("shape", {})
+    if shape != {"batch": args.batch, "heads": 32, "head_dim": 128, "kv": "f32"}:
+        return None, None
     c = t.get("classes", {}).get(dom_kernel_class)
-    return None if c is None else round(c["bytes_per_launch"])
+    alg = (t.get("algorithmic") or {}).get(dom_kernel_class)
+    if c is None or not alg:
+        return None, None
+    ratio = c["bytes_per_launch"] / alg
+    basis = (f"{TRAFFIC_FILE.split(os.sep)[-1]}: rocprofv3 FETCH_SIZE + WRITE_SIZE of the {dom_kernel_class} "
+             f"kernels at this launch shape, mean context {t.get('mean_ctx')}, measured/algorithmic "
+             f"{ratio:.4f}, applied to this run's bytes per launch")
+    return round(ratio * bytes_per_launch), basis
 
 
 def encdec_flops(d, H, ne, nd, T):
@@ -525,7 +564,9 @@ def main():
     dom = max(classes, key=lambda c: c["gpu_ms"])
     other = min(classes, key=lambda c: c["gpu_ms"])
     roof = {"bound": "hbm", "achieved": round(dom["achieved"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4), "traffic": load_traffic(args, dom["cls"]),
+            "frac": round(dom["achieved"] / HBM_PEAK_GBS, 4),
+            "traffic": load_traffic(args, dom["cls"], dom["bytes"] / max(dom["launches"], 1))[0],
+            "traffic_basis": load_traffic(args, dom["cls"], dom["bytes"] / max(dom["launches"], 1))[1],
             "kernel": dom["kernel"],
             "bytes_per_launch": dom["bytes"] / max(dom["launches"], 1),
             "avg_launch_us": 1e3 * dom["gpu_ms"] / max(dom["launches"], 1)}
@@ -555,8 +596,7 @@ def main():
     except Exception as e:  # the headline number stands on its own
         log("[bench] batch-1 leg failed:", e)
 
-    step_flops = 2.0 * B * (L * (3 * d * d + d * d + 3 * d * F) + V * d) + 4.0 * B * L * H * (P + 64) * dh
-    cpu = None if args.no_cpu else cpu_baseline(step_flops, B)
+    cpu, cpu_configs = (None, None) if args.no_cpu else cpu_baseline(B, pos0 + args.steps // 2)
 
     # prefill: all projections of every prompt token, causal attention, the LM head for the
     # last position of each sequence
@@ -631,6 +671,7 @@ def main():
                          "frac": round(prefill_flops / prefill_s / 1e12 / 157.3, 4),
                          "flops": prefill_flops, "note": "fp32 MFMA peak; wall time of the whole prefill"},
         "cpu_baseline": cpu,
+        "cpu_configs": cpu_configs,
         "llama7b_batch1": b1,
         "llama7b_bf16_storage": llama_bf16,
         "gpt2_small": gpt2,

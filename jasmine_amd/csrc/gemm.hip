@@ -587,17 +587,31 @@ __global__ void __launch_bounds__(NW * 64) gemm_dma_kernel(const DmaArgs p)
     }
 }
 
-// Geometry: 256 x 256 tiles (8 waves, 3 stages) when they give every CU a workgroup,
-// else 128 x 128 (4 waves, 4 stages), else 64 x 64 (4 waves, 4 stages of 32-wide slabs).
-// MI355X, fp32: 4096^3 at 134-137 TFLOP/s, 2048^3 at 116, 1024^3 at 88.
+// Geometry: 256 x 256 tiles (8 waves, 3 stages) when they give every CU a workgroup, else
+// 128 x 128 (4 waves, 4 stages) when those give every CU at least four, else 64 x 64 (4
+// waves, 4 stages of 32-wide slabs).  64 x 64 tiles win wherever the 128-wide ones would
+// leave a partly filled last round (GPT-2-small prefill QKV 2304 x 4096 x 768: 90 against
+// 75 TFLOP/s; FC 3072 x 4096 x 768: 92 against 84).  MI355X fp32: 4096^3 at 130-137
+// TFLOP/s, 2048^3 at 113, 1024^3 at 82-89.
+// JAS_GEMM_GEOMETRY=256|128|64 forces one geometry (a tuning knob; default: the rule above).
+static int forced_geometry()
+{
+    static const int g = [] {
+        const char *e = getenv("JAS_GEMM_GEOMETRY");
+        return e ? atoi(e) : 0;
+    }();
+    return g;
+}
+
 template <int AM, int BM>
 static void launch_dma(const DmaArgs &p, int batch, hipStream_t s)
 {
     auto tiles = [&](int t) { return (long)ceil_div(p.M, t) * ceil_div(p.N, t) * batch; };
-    if (tiles(256) >= 256) {
+    const int fg = forced_geometry();
+    if (fg == 256 || (fg == 0 && tiles(256) >= 256)) {
         const dim3 grid(ceil_div(p.N, 256), ceil_div(p.M, 256), batch);
         hipLaunchKernelGGL((gemm_dma_kernel<AM, BM, 256, 256, 8, 2, 3, 1>), grid, dim3(512), 0, s, p);
-    } else if (tiles(128) >= 256) {
+    } else if (fg == 128 || (fg == 0 && tiles(128) >= 1024)) {
         const dim3 grid(ceil_div(p.N, 128), ceil_div(p.M, 128), batch);
         hipLaunchKernelGGL((gemm_dma_kernel<AM, BM, 128, 128, 4, 2, 4, 1>), grid, dim3(256), 0, s, p);
     } else {

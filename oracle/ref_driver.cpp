@@ -79,6 +79,28 @@ static void from_mat(const M &m, float *out)
 template <typename T>
 using upd_t = sgd_t<T>;
 
+struct hash_init_t;
+template <>
+struct init_t<hash_init_t>
+{
+    template <typename mat_type>
+    requires is_matrix<mat_type>
+    static void cal(mat_type &m)
+    {
+        for (int i = 0; i < m.row_num(); ++i)
+            for (int j = 0; j < m.col_num(); ++j)
+                m(i, j) = (float)(((uint32_t)(i * 2654435761u) ^ (uint32_t)(j * 40503u)) % 2001 - 1000) * 2e-5f;
+    }
+};
+
+static void rms_rows(mat_t<float> &h, const mat_t<float> &x, int d)
+{
+    double ss = 0;
+    for (int i = 0; i < d; ++i) ss += (double)x(i, 0) * x(i, 0);
+    const float r = (float)(1.0 / std::sqrt(ss / d + 1e-6));
+    for (int i = 0; i < d; ++i) h(i, 0) = x(i, 0) * r;
+}
+
 extern "C" {
 
 // mat_t::dot -> mat_dot_t clone (mat_express_t.hpp:730-776)
@@ -337,6 +359,85 @@ double ref_time_head(int dh, int T, int reps)
     }
     auto t1 = std::chrono::steady_clock::now();
     return std::chrono::duration<double>(t1 - t0).count() / reps;
+}
+
+
+// ---- one LLaMA-shaped decode step of one sequence, on jasmine's own objects ----
+// jasmine has no KV cache, RMSNorm, RoPE or SwiGLU (its decode loop recomputes the prefix,
+// transformer_test.hpp:194-242).  The step is timed as jasmine code would compute it with
+// a cache held in mat_t: the seven projections through weight_net_t::forward
+// (mat_net_t.hpp:38-49), per head S = q^T K / sqrt(d_h) with mat_dot_t and the double
+// division (mat_mha_t.hpp:53), hsoftmax (mat_express_t.hpp:681-694) and V P^T
+// (mat_mha_t.hpp:71); the O(d) glue (RMSNorm, rotary, SiLU gate, residual adds) as plain
+// loops.  Only the time is used.
+// seconds for one layer of one sequence's decode step over a T-key cache; *attn_s gets the
+// attention part (scores, softmax, weighted sum over all heads)
+double ref_time_llama_layer(int d, int H, int F, int T, double *attn_s)
+{
+    using M = mat_t<float>;
+    const int dh = d / H;
+    weight_net_t<M, upd_t> wq(d, d), wk(d, d), wv(d, d), wo(d, d), wg(d, F), wu(d, F), wd(F, d);
+    // weights and cache keep mat_t's zero initialisation: filling 1.3 G elements through
+    // operator() would take longer than the timed step, and x86 fp32 arithmetic time does not
+    // depend on the values (no denormals arise from zeros)
+    std::vector<M> kc, vc;
+    for (int h = 0; h < H; ++h) {
+        kc.emplace_back(dh, T);
+        vc.emplace_back(dh, T);
+    }
+    M x(d, 1), hbuf(d, 1), att(d, 1);
+    for (int i = 0; i < d; ++i) x(i, 0) = 0.01f * (float)(i % 17);
+    volatile float sink = 0;
+    auto t0 = std::chrono::steady_clock::now();
+    rms_rows(hbuf, x, d);
+    M q = wq.forward(hbuf), k = wk.forward(hbuf), v = wv.forward(hbuf);
+    for (int i = 0; i < d; i += 2) {  // rotary on q and k (position T)
+        const double a = T / std::pow(10000.0, (double)(i % dh) / dh);
+        const float c = (float)std::cos(a), s = (float)std::sin(a);
+        const float q0 = q(i, 0), q1 = q(i + 1, 0), k0 = k(i, 0), k1 = k(i + 1, 0);
+        q(i, 0) = q0 * c - q1 * s; q(i + 1, 0) = q0 * s + q1 * c;
+        k(i, 0) = k0 * c - k1 * s; k(i + 1, 0) = k0 * s + k1 * c;
+    }
+    auto ta = std::chrono::steady_clock::now();
+    for (int h = 0; h < H; ++h) {
+        M qh = q.view(h * dh, 0, dh, 1);
+        auto scores = (qh.t().dot(kc[h]) / sqrt(dh)).clone();
+        auto p = hsoftmax(scores);
+        auto o = vc[h].dot(p.t()).clone();
+        for (int e = 0; e < dh; ++e) att(h * dh + e, 0) = o(e, 0);
+    }
+    auto tb = std::chrono::steady_clock::now();
+    M o = wo.forward(att);
+    for (int i = 0; i < d; ++i) x(i, 0) = x(i, 0) + o(i, 0);
+    rms_rows(hbuf, x, d);
+    M g = wg.forward(hbuf), u = wu.forward(hbuf);
+    M ff(F, 1);
+    for (int i = 0; i < F; ++i) ff(i, 0) = g(i, 0) / (1.0f + std::exp(-g(i, 0))) * u(i, 0);
+    M dn = wd.forward(ff);
+    for (int i = 0; i < d; ++i) x(i, 0) = x(i, 0) + dn(i, 0);
+    sink = sink + x(0, 0) + (float)k(0, 0) + (float)v(0, 0);
+    auto t1 = std::chrono::steady_clock::now();
+    if (attn_s) *attn_s = std::chrono::duration<double>(tb - ta).count();
+    return std::chrono::duration<double>(t1 - t0).count();
+}
+
+// one causal attention head of S tokens at head dim dh without its projections (the
+// scores, mask, softmax and weighted sum of mat_head_gen_t::forward, mat_mha_t.hpp:53-71)
+double ref_time_attention_head(int dh, int S)
+{
+    using M = mat_t<float>;
+    M q(dh, S), k(dh, S), v(dh, S);
+    init_matrix<hash_init_t>(q); init_matrix<hash_init_t>(k); init_matrix<hash_init_t>(v);
+    volatile float sink = 0;
+    auto t0 = std::chrono::steady_clock::now();
+    auto scores = (q.t().dot(k) / sqrt(dh)).clone();
+    for (int i = 0; i < scores.row_num(); ++i)
+        for (int j = i + 1; j < scores.col_num(); ++j) scores(i, j) = -std::numeric_limits<float>::infinity();
+    auto p = hsoftmax(scores);
+    auto o = v.dot(p.t()).clone();
+    sink = sink + o(0, 0);
+    auto t1 = std::chrono::steady_clock::now();
+    return std::chrono::duration<double>(t1 - t0).count();
 }
 
 } // extern "C"

@@ -114,9 +114,12 @@ if ref is not None:
     ref.ref_predict_loop.argtypes = [FP, C.c_int, FP, C.c_int, C.c_int, C.c_int, C.c_int, FP, C.c_int, FP]
     ref.ref_transformer_nparams.restype = C.c_long
     ref.ref_transformer_nparams.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int]
-    for n, k in (("ref_time_linear", 4), ("ref_time_cfg2", 3), ("ref_time_hsoftmax", 3), ("ref_time_head", 3)):
+    for n, k in (("ref_time_linear", 4), ("ref_time_cfg2", 3), ("ref_time_hsoftmax", 3), ("ref_time_head", 3),
+                 ("ref_time_attention_head", 2)):
         getattr(ref, n).restype = C.c_double
         getattr(ref, n).argtypes = [C.c_int] * k
+    ref.ref_time_llama_layer.restype = C.c_double
+    ref.ref_time_llama_layer.argtypes = [C.c_int] * 4 + [C.POINTER(C.c_double)]
 
 
 def normal(shape, seed, stream=0, mean=0.0, std=1.0):
