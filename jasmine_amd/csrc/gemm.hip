@@ -310,6 +310,8 @@ struct DmaArgs {
     int M, N, K;
     int bias_mode, act, accumulate;
     int c_vec;  // 1: row-major C with float4 stores over n; 2: column-major C, float4 over m
+    // fused prefill epilogues (packed weights, token-major output, c_vec == 2)
+    DmaFused fz;
 };
 
 // M0 is a reserved register to the compiler; nothing else in these kernels uses it (no
@@ -327,8 +329,8 @@ __device__ __forceinline__ void lds_dma16(const float *src, float *lds_dst)
 // whether the slab element group lies inside K (only the tail slab can leave K).
 // X(o, k) = X[o * so + k * sk]; Olim = rows (outer extent); RG = packed row tiles.
 template <int MODE, int O, int KWT>
-__device__ __forceinline__ const float *dma_src(const float *X, long so, long sk, int o0, int Olim, int K, int k0,
-                                                int ins, int lane, int &kfirst)
+__device__ __forceinline__ const float *dma_src(const float *X, const float *X2, long so, long sk, int o0, int Olim,
+                                                int K, int k0, int ins, int lane, int &kfirst)
 {
     if (MODE == DM_OC) {
         const int f = 256 * ins + 4 * lane, k = k0 + f / O;
@@ -341,10 +343,17 @@ __device__ __forceinline__ const float *dma_src(const float *X, long so, long sk
     const int kb = ins / RB, rb = ins % RB;
     if (MODE == DM_PK) {
         const long RG = (Olim + 15) >> 4;
-        const long rt = min((long)(o0 >> 4) + rb, RG - 1);
+        long rt = min((long)(o0 >> 4) + rb, RG - 1);
         const int kblk = (k0 >> 4) + kb;
         kfirst = 16 * kblk;
-        return X + weight_tile_offset(rt, kblk < (K >> 4) ? kblk : (K >> 4) - 1, K >> 4, RG) + lane * 4;
+        const float *Xm = X;
+        long RGm = RG;
+        if (X2) {  // SwiGLU: virtual row tile 2f is gate tile f, 2f + 1 up tile f
+            Xm = rt & 1 ? X2 : X;
+            rt >>= 1;
+            RGm = RG >> 1;
+        }
+        return Xm + weight_tile_offset(rt, kblk < (K >> 4) ? kblk : (K >> 4) - 1, K >> 4, RGm) + lane * 4;
     }
     int o = o0 + 16 * rb + (lane & 15);
     o = o < Olim ? o : Olim - 1;
@@ -353,8 +362,8 @@ __device__ __forceinline__ const float *dma_src(const float *X, long so, long sk
 }
 
 template <int MODE, int O, int KWT, int NW>
-__device__ __forceinline__ void dma_slab(const float *X, long so, long sk, int o0, int Olim, int K, int k0, float *lds,
-                                         int w, int lane)
+__device__ __forceinline__ void dma_slab(const float *X, const float *X2, long so, long sk, int o0, int Olim, int K,
+                                         int k0, float *lds, int w, int lane)
 {
     constexpr int NI = O * KWT / 256;  // 1 KB instructions per slab
     static_assert(NI % NW == 0, "slab instructions spread evenly over the waves");
@@ -362,22 +371,22 @@ __device__ __forceinline__ void dma_slab(const float *X, long so, long sk, int o
     for (int q = 0; q < NI / NW; ++q) {
         const int ins = w * (NI / NW) + q;  // wave-uniform
         int kf;
-        lds_dma16(dma_src<MODE, O, KWT>(X, so, sk, o0, Olim, K, k0, ins, lane, kf), lds + 256 * ins);
+        lds_dma16(dma_src<MODE, O, KWT>(X, X2, so, sk, o0, Olim, K, k0, ins, lane, kf), lds + 256 * ins);
     }
 }
 
 // The last, partial slab (K % (16 KB) != 0): ordinary loads with zeros past K, stored in the
 // same layout.
 template <int MODE, int O, int KWT, int NW>
-__device__ __forceinline__ void tail_slab(const float *X, long so, long sk, int o0, int Olim, int K, int k0, float *lds,
-                                          int w, int lane)
+__device__ __forceinline__ void tail_slab(const float *X, const float *X2, long so, long sk, int o0, int Olim, int K,
+                                          int k0, float *lds, int w, int lane)
 {
     constexpr int NI = O * KWT / 256;
 #pragma unroll
     for (int q = 0; q < NI / NW; ++q) {
         const int ins = w * (NI / NW) + q;
         int kf;
-        const float *src = dma_src<MODE, O, KWT>(X, so, sk, o0, Olim, K, k0, ins, lane, kf);
+        const float *src = dma_src<MODE, O, KWT>(X, X2, so, sk, o0, Olim, K, k0, ins, lane, kf);
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (MODE == DM_KC) {  // per element: K need not be a multiple of 4
             float e[4];
@@ -475,8 +484,8 @@ __global__ void __launch_bounds__(NW * 64) gemm_dma_kernel(const DmaArgs p)
 
     auto issue = [&](int kt) {
         float *sa = lds + (kt % ST) * (SA + SB), *sb = sa + SA;
-        dma_slab<AM, TM, KWT, NW>(A, p.as0, p.as1, m0, p.M, K, kt * KWT, sa, w, lane);
-        dma_slab<BM, TN, KWT, NW>(B, p.bs1, p.bs0, n0, p.N, K, kt * KWT, sb, w, lane);
+        dma_slab<AM, TM, KWT, NW>(A, p.fz.A2, p.as0, p.as1, m0, p.M, K, kt * KWT, sa, w, lane);
+        dma_slab<BM, TN, KWT, NW>(B, nullptr, p.bs1, p.bs0, n0, p.N, K, kt * KWT, sb, w, lane);
     };
     floatx4 acc[NBI][NBJ];
 #pragma unroll
@@ -519,8 +528,8 @@ __global__ void __launch_bounds__(NW * 64) gemm_dma_kernel(const DmaArgs p)
         // stage nk % ST was last read in iteration nk - ST, which every wave finished before
         // the barrier of iteration nk - 1
         float *sa = lds + (nk % ST) * (SA + SB), *sb = sa + SA;
-        tail_slab<AM, TM, KWT, NW>(A, p.as0, p.as1, m0, p.M, K, nk * KWT, sa, w, lane);
-        tail_slab<BM, TN, KWT, NW>(B, p.bs1, p.bs0, n0, p.N, K, nk * KWT, sb, w, lane);
+        tail_slab<AM, TM, KWT, NW>(A, p.fz.A2, p.as0, p.as1, m0, p.M, K, nk * KWT, sa, w, lane);
+        tail_slab<BM, TN, KWT, NW>(B, nullptr, p.bs1, p.bs0, n0, p.N, K, nk * KWT, sb, w, lane);
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         compute(sa);
     }
@@ -551,6 +560,61 @@ __global__ void __launch_bounds__(NW * 64) gemm_dma_kernel(const DmaArgs p)
                     o.w = finish(acc[i][4 * q + 3][r], m, n + 3, cp + 3);
                     *(float4 *)cp = o;
                 }
+    } else if (AM != DM_OC && p.c_vec == 2 && p.fz.mode == FZ_SWIGLU) {
+        // virtual rows: block 2k holds gate features, block 2k + 1 the up features of the same
+        // 16 outputs, so both products of an output sit in one lane: out = silu(gate) * up
+#pragma unroll
+        for (int i = 0; i < NBI; i += 2)
+#pragma unroll
+            for (int j = 0; j < NBJ; ++j) {
+                const int mv = mw + 16 * i + 4 * g, n = nw + dma_outer<BM, NBJ>(j, r16);
+                const int f = (mv >> 5) * 16 + (mv & 15);  // output feature of this lane's first row
+                if (n >= p.N || 2 * f >= p.M) continue;
+                float4 o;
+                o.x = silu_f(acc[i][j][0]) * acc[i + 1][j][0];
+                o.y = silu_f(acc[i][j][1]) * acc[i + 1][j][1];
+                o.z = silu_f(acc[i][j][2]) * acc[i + 1][j][2];
+                o.w = silu_f(acc[i][j][3]) * acc[i + 1][j][3];
+                *(float4 *)(C + f + (long)n * p.cs1) = o;
+            }
+    } else if (AM != DM_OC && p.c_vec == 2 && p.fz.mode == FZ_QKV) {
+        // rows [0, d) q, [d, 2d) k, [2d, 3d) v of token n: bias, rotary on q and k (pairs
+        // (2i, 2i+1) of a head are registers (0, 1) and (2, 3) of one lane), the row, and k / v
+        // into the KV cache at the token's position
+        const DmaFused &z = p.fz;
+#pragma unroll
+        for (int i = 0; i < NBI; ++i)
+#pragma unroll
+            for (int j = 0; j < NBJ; ++j) {
+                const int m = mw + 16 * i + 4 * g, n = nw + dma_outer<BM, NBJ>(j, r16);
+                if (n >= p.N || m >= p.M) continue;
+                float v[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] = bias ? acc[i][j][r] + bias[m + r] : acc[i][j][r];
+                const int sec = m / z.d, e = m % z.dh, hh = (m % z.d) / z.dh;
+                const int t = z.pos[n];
+                if (z.rope && sec < 2) {
+#pragma unroll
+                    for (int pr = 0; pr < 2; ++pr) {
+                        const double2 cs = z.rope_tab[(long)t * (z.dh / 2) + (e >> 1) + pr];
+                        const double x0 = v[2 * pr], x1 = v[2 * pr + 1];
+                        v[2 * pr] = (float)(x0 * cs.x - x1 * cs.y);
+                        v[2 * pr + 1] = (float)(x0 * cs.y + x1 * cs.x);
+                    }
+                }
+                *(float4 *)(C + m + (long)n * p.cs1) = make_float4(v[0], v[1], v[2], v[3]);
+                if (sec >= 1) {
+                    const int bseq = n / z.P;
+                    const long dst = (((long)bseq * z.H + hh) * z.ctx + t) * z.dh + e;
+                    void *cache = sec == 1 ? z.kc : z.vc;
+                    if (z.kv_bf16)
+                        *(u32x2 *)((uint16_t *)cache + dst) =
+                            u32x2{(uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                                  (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16)};
+                    else
+                        *(float4 *)((float *)cache + dst) = make_float4(v[0], v[1], v[2], v[3]);
+                }
+            }
     } else if (AM != DM_OC && p.c_vec == 2) {  // column-major C: four consecutive m per lane
 #pragma unroll
         for (int i = 0; i < NBI; ++i)
@@ -631,7 +695,8 @@ static int dma_mode(const float *X, long so, long sk, int O, long bst)
 
 static bool gemm_dma(int M, int N, int K, const void *A, long as0, long as1, const float *B, long bs0, long bs1,
                      float *C, long cs0, long cs1, const float *bias, int bias_mode, int act, int accumulate, int batch,
-                     long abs_, long bbs, long cbs, long biasbs, hipStream_t s, bool a_packed, bool a_bf16)
+                     long abs_, long bbs, long cbs, long biasbs, hipStream_t s, bool a_packed, bool a_bf16,
+                     const DmaFused *fz = nullptr)
 {
     if (a_bf16 || K <= 0) return false;
     int am = a_packed ? DM_PK : dma_mode((const float *)A, as0, as1, M, abs_);
@@ -648,6 +713,10 @@ static bool gemm_dma(int M, int N, int K, const void *A, long as0, long as1, con
     p.c_vec = 0;
     if (ca && cs1 == 1 && cs0 % 4 == 0 && N % 4 == 0) p.c_vec = 1;
     else if (ca && cs0 == 1 && cs1 % 4 == 0) p.c_vec = 2;
+    if (fz) {
+        if (!a_packed || p.c_vec != 2 || batch != 1 || accumulate || act != JAS_ACT_NONE) return false;
+        p.fz = *fz;
+    }
 #define JAS_DMA_B(AMV)                                                                                 \
     if (bm == DM_KC) launch_dma<AMV, DM_KC>(p, batch, s);                                             \
     else launch_dma<AMV, DM_OC>(p, batch, s);
@@ -656,6 +725,18 @@ static bool gemm_dma(int M, int N, int K, const void *A, long as0, long as1, con
     else { JAS_DMA_B(DM_OC) }
 #undef JAS_DMA_B
     return true;
+}
+
+bool gemm_prefill_fused(int M, int N, int K, const void *A, const float *X, float *C, long ldc, const float *bias,
+                        const DmaFused &fz, hipStream_t s)
+{
+    // SwiGLU: M virtual rows = 2 x the output features (gate / up tiles interleaved)
+    if (fz.mode == FZ_SWIGLU && (M % 32 || !fz.A2 || bias)) return false;
+    if (fz.mode == FZ_QKV && (fz.d % 16 || fz.dh % 16 || M != 3 * fz.d || !fz.pos || (fz.rope && !fz.rope_tab)))
+        return false;
+    const bool ok = gemm_dma(M, N, K, A, K, 1, X, 1, K, C, 1, ldc, bias, bias ? 1 : 0, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0,
+                             s, true, false, &fz);
+    return ok && hipGetLastError() == hipSuccess;
 }
 
 jas_status gemm_general(int M, int N, int K, const void *A, long as0, long as1, const float *B, long bs0, long bs1,

@@ -133,6 +133,27 @@ jas_status skinny_gemm(const void *W, const void *W2, const float *X, long ldx, 
                        const SkinnyEpiArgs &epi, hipStream_t s, bool packed = false,
                        const SkinnyTuning *tune = nullptr, bool wbf16 = false);
 
+// Fused epilogues of the prefill GEMMs on packed fp32 weights (token-major output).
+enum FusedMode : int { FZ_NONE = 0, FZ_QKV = 1, FZ_SWIGLU = 2 };
+struct DmaFused {
+    int mode = FZ_NONE;
+    const float *A2 = nullptr;  // FZ_SWIGLU: the up weights (A: the gate weights)
+    // FZ_QKV: rows [0, d) q, [d, 2d) k, [2d, 3d) v; rotary on q and k from rope_tab
+    // ([position][dh / 2] (cos, sin)) when rope; k and v also go to the cache at
+    // ((seq * H + head) * ctx + pos) * dh, sequence = token / P
+    const int32_t *pos = nullptr;
+    const double2 *rope_tab = nullptr;
+    int rope = 0;
+    void *kc = nullptr, *vc = nullptr;
+    int kv_bf16 = 0;
+    int d = 0, dh = 0, H = 0, P = 0, ctx = 0;
+};
+// C[n][m] for packed weights A [M][K] and token-major X [N][K], with a fused epilogue;
+// false when the product does not qualify (the caller then runs the unfused sequence).
+// FZ_SWIGLU: M = 2 x the output features, C [N][M / 2] = silu(gate) * up.
+bool gemm_prefill_fused(int M, int N, int K, const void *A, const float *X, float *C, long ldc, const float *bias,
+                        const DmaFused &fz, hipStream_t s);
+
 // General strided GEMM (see jas_gemm in jasmine_hip.h).
 jas_status gemm_general(int M, int N, int K, const void *A, long as0, long as1, const float *B, long bs0, long bs1,
                         float *C, long cs0, long cs1, const float *bias, int bias_mode, int act, int accumulate,

@@ -574,18 +574,31 @@ jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_
         }
         TRY(norm_rows(lm, lm->pX, lm->pH, (int)T, d, l, 1));
         const float *bq = lm->LW("b_qkv", l);
-        // QKV[n][m] = sum_k w_qkv[m][k] H[n][k] (+ b[m]); weights in the packed layout
-        TRY(gemm_general(3 * d, (int)T, d, lm->LW("w_qkv", l), d, 1, lm->pH, 1, d, lm->pQKV, 1, 3L * d, bq,
-                         bq ? 1 : 0, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
-        if (c.kind == 1)  // q and k sections are 2H consecutive heads of each row
-            TRY(jas_rope_llama(lm->pQKV, lm->pPos, (int)T, 2 * H, dh, 3L * d, c.rope_theta, s));
         float *kcl = lm->kv_layer_ptr(lm->kc, l), *vcl = lm->kv_layer_ptr(lm->vc, l);
-        if (c.kv_bf16)
-            hipLaunchKernelGGL(kv_scatter_kernel<true>, dim3(ceil_div(T * (d / 4), 256)), dim3(256), 0, s, lm->pQKV,
-                               kcl, vcl, B, P, H, dh, c.max_ctx);
-        else
-            hipLaunchKernelGGL(kv_scatter_kernel<false>, dim3(ceil_div(T * (d / 4), 256)), dim3(256), 0, s, lm->pQKV,
-                               kcl, vcl, B, P, H, dh, c.max_ctx);
+        // QKV[n][m] = sum_k w_qkv[m][k] H[n][k] (+ b[m]); weights in the packed layout.  On fp32
+        // weights the GEMM's epilogue also applies the rotary (LLaMA) and writes k and v into
+        // the KV cache; bf16 weights take the GEMM, then the rotary and scatter kernels.
+        DmaFused fq;
+        fq.mode = FZ_QKV;
+        fq.pos = lm->pPos;
+        fq.rope_tab = lm->rope_tab;
+        fq.rope = c.kind == 1;
+        fq.kc = kcl;
+        fq.vc = vcl;
+        fq.kv_bf16 = c.kv_bf16;
+        fq.d = d, fq.dh = dh, fq.H = H, fq.P = P, fq.ctx = c.max_ctx;
+        if (lm->wbf16() || !gemm_prefill_fused(3 * d, (int)T, d, lm->LW("w_qkv", l), lm->pH, lm->pQKV, 3L * d, bq, fq, s)) {
+            TRY(gemm_general(3 * d, (int)T, d, lm->LW("w_qkv", l), d, 1, lm->pH, 1, d, lm->pQKV, 1, 3L * d, bq,
+                             bq ? 1 : 0, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
+            if (c.kind == 1)  // q and k sections are 2H consecutive heads of each row
+                TRY(jas_rope_llama(lm->pQKV, lm->pPos, (int)T, 2 * H, dh, 3L * d, c.rope_theta, s));
+            if (c.kv_bf16)
+                hipLaunchKernelGGL(kv_scatter_kernel<true>, dim3(ceil_div(T * (d / 4), 256)), dim3(256), 0, s,
+                                   lm->pQKV, kcl, vcl, B, P, H, dh, c.max_ctx);
+            else
+                hipLaunchKernelGGL(kv_scatter_kernel<false>, dim3(ceil_div(T * (d / 4), 256)), dim3(256), 0, s,
+                                   lm->pQKV, kcl, vcl, B, P, H, dh, c.max_ctx);
+        }
         // the prompt attends over the keys/values just computed (fp32, in the QKV rows);
         // the cache keeps them for the decode steps (rounded when it is bf16)
         const long qs = (long)P * 3 * d;
@@ -601,12 +614,19 @@ jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_
             TRY(gemm_general(d, (int)T, F, lm->LW("w_proj", l), F, 1, lm->pG, 1, F, lm->pX, 1, d,
                              lm->LW("b_proj", l), 1, JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
         } else {
-            TRY(gemm_general(F, (int)T, d, lm->LW("w_gate", l), d, 1, lm->pH, 1, d, lm->pG, 1, F, nullptr, 0,
-                             JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
-            TRY(gemm_general(F, (int)T, d, lm->LW("w_up", l), d, 1, lm->pH, 1, d, lm->pU, 1, F, nullptr, 0,
-                             JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
-            hipLaunchKernelGGL(swiglu_kernel, dim3(ceil_div(T * F, 256)), dim3(256), 0, s, lm->pG, lm->pU, lm->pFF,
-                               T * F);
+            // SwiGLU: gate and up in one GEMM whose epilogue writes silu(gate) * up (fp32 weights)
+            DmaFused fs;
+            fs.mode = FZ_SWIGLU;
+            fs.A2 = lm->LW("w_up", l);
+            if (lm->wbf16() ||
+                !gemm_prefill_fused(2 * F, (int)T, d, lm->LW("w_gate", l), lm->pH, lm->pFF, F, nullptr, fs, s)) {
+                TRY(gemm_general(F, (int)T, d, lm->LW("w_gate", l), d, 1, lm->pH, 1, d, lm->pG, 1, F, nullptr, 0,
+                                 JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
+                TRY(gemm_general(F, (int)T, d, lm->LW("w_up", l), d, 1, lm->pH, 1, d, lm->pU, 1, F, nullptr, 0,
+                                 JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
+                hipLaunchKernelGGL(swiglu_kernel, dim3(ceil_div(T * F, 256)), dim3(256), 0, s, lm->pG, lm->pU,
+                                   lm->pFF, T * F);
+            }
             TRY(gemm_general(d, (int)T, F, lm->LW("w_down", l), F, 1, lm->pFF, 1, F, lm->pX, 1, d, nullptr, 0,
                              JAS_ACT_NONE, 1, 1, 0, 0, 0, 0, s, true, lm->wbf16()));
         }
