@@ -93,6 +93,23 @@ int api_gemm_tn(int M, int N, int K, const float *A, const float *B, float *C)
     });
 }
 
+// An expression kept in a variable and evaluated statements later (`auto e = A*B + A;`):
+// the reference's nodes hold sub-expressions by reference, so this dangles there; these
+// headers hold them by value.  The sanitizer build checks that nothing is read after scope.
+int api_expr_deferred(const float *A, const float *B, float *out, int R, int Cc)
+{
+    return guarded([&] {
+        auto a = to_mat(A, R, Cc), b = to_mat(B, R, Cc);
+        auto e = a * b + a * 0.5f - (b + 1.0f) * 2.0f;
+        {
+            auto other = (a - b).clone();  // reuses the stack the temporaries of e had
+            (void)other;
+        }
+        mat_t<float> r = e.clone();
+        from_mat(r, out);
+    });
+}
+
 int api_cfg2_expr(const float *A, const float *B, const float *C, float *D, int R, int Cc)
 {
     return guarded([&] {

@@ -10,7 +10,8 @@ import os
 import numpy as np
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
+# JAS_ORACLE_SO selects another build of the restatement (the sanitizer build, oracle/_san)
+ORACLE_SO = os.environ.get("JAS_ORACLE_SO") or os.path.join(ROOT, "oracle", "liboracle.so")
 REF_SO = os.path.join(ROOT, "oracle", "_ref", "libjasref.so")
 
 FP = C.POINTER(C.c_float)

@@ -18,7 +18,8 @@ import pytest
 from oracle_lib import fp, ip
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB = os.path.join(HERE, "cpp", "libjasapi.so")
+# JAS_API_SO selects another build of the driver (the sanitizer build, libjasapi_san.so)
+LIB = os.environ.get("JAS_API_SO") or os.path.join(HERE, "cpp", "libjasapi.so")
 GOLD = os.path.join(HERE, "golden", "jasmine_golden.npz")
 
 
@@ -62,7 +63,8 @@ def bitexact(a, b):
 def test_api_library_exports(api):
     for name in ("api_gemm", "api_gemm_tn", "api_cfg2_expr", "api_expr", "api_hsoftmax", "api_softmax_global",
                  "api_reductions", "api_linear", "api_relu", "api_sigmoid", "api_layernorm_cols", "api_head",
-                 "api_mha", "api_rope", "api_transformer", "api_transformer_nparams", "api_last_error", "api_set_fused_heads", "api_transformer_reencode", "api_predict_loop"):
+                 "api_mha", "api_rope", "api_transformer", "api_transformer_nparams", "api_last_error", "api_set_fused_heads", "api_transformer_reencode", "api_predict_loop",
+                 "api_expr_deferred"):
         assert hasattr(api, name), name
 
 
@@ -108,6 +110,20 @@ def test_api_cfg2_expression(api, g):
     d = np.zeros_like(a)
     ok(api, api.api_cfg2_expr(fp(a), fp(b), fp(c), fp(d), a.shape[0], a.shape[1]))
     close(d, want)
+
+
+@pytest.mark.gpu
+def test_api_expression_kept_in_a_variable(api):
+    """`auto e = a * b + a * 0.5f - (b + 1.0f) * 2.0f;` evaluated statements later (after other
+    temporaries reused the stack): the nodes hold their sub-expressions by value."""
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((37, 29)).astype(np.float32)
+    b = rng.standard_normal((37, 29)).astype(np.float32)
+    out = np.zeros_like(a)
+    ok(api, api.api_expr_deferred(fp(a), fp(b), fp(out), 37, 29))
+    f = np.float32
+    want = (a * b + a * f(0.5)) - (b + f(1.0)) * f(2.0)
+    assert bitexact(out, want)
 
 
 @pytest.mark.gpu
