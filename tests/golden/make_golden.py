@@ -111,9 +111,10 @@ def main():
     ref.ref_transformer(fp(en), Te, fp(np.ascontiguousarray(de[:, :3])), 3, d, H, ne, nd, fp(Wt), fp(Yp))
     g["tf_prefix3"] = Yp
 
-    # head dims the fused all-heads path takes (32, 64): self attention with the mask, cross
+    # head dims the fused all-heads path takes (32, 64, 128): self attention with the mask, cross
     # attention, and an encoder-decoder stack with its causal-prefix invariant
-    for tag, (d2, H2, T2, Tk2, seed) in {"mha32": (64, 2, 40, 23, 70), "mha64": (128, 2, 33, 19, 74)}.items():
+    for tag, (d2, H2, T2, Tk2, seed) in {"mha32": (64, 2, 40, 23, 70), "mha64": (128, 2, 33, 19, 74),
+                                                  "mha128": (128, 1, 29, 21, 90)}.items():
         n2 = 3 * H2 * ((d2 // H2) ** 2 + d2 // H2) + d2 * d2 + d2
         W2 = normal(n2, 1, seed, std=0.1)
         X2, K2 = normal((d2, T2), 1, seed + 1), normal((d2, Tk2), 1, seed + 2)

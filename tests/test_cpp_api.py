@@ -226,10 +226,10 @@ def _mha_case(api, g, tag, cross):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("tag", ["mha32", "mha64"])
+@pytest.mark.parametrize("tag", ["mha32", "mha64", "mha128"])
 @pytest.mark.parametrize("cross", [0, 1])
 def test_api_mha_fused_heads(api, g, tag, cross):
-    """Head dims 32 / 64: every head in batched projections plus the flash kernel, against
+    """Head dims 32 / 64 / 128: every head in batched projections plus the flash kernel, against
     the reference's outputs; the per-head path (materialised scores) agrees with both."""
     Y = _mha_case(api, g, tag, cross)
     close(Y, g[f"{tag}_cross" if cross else f"{tag}_self"])

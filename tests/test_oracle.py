@@ -105,6 +105,15 @@ def test_golden_attention(g):
     Y = np.zeros((d, T), np.float32)
     orc.orc_jas_mha(fp(Xm), fp(Xm), d, 3, T, T, fp(Wm), 1, fp(Y))
     assert bits_equal(Y, g["mha_y"])
+    # the fused-heads fixtures (head dims 32, 64, 128): masked self and cross attention
+    for tag in ("mha32", "mha64", "mha128"):
+        d2, H2, T2, Tk2 = (int(v) for v in g[f"{tag}_dims"])
+        W2, X2, K2 = g[f"{tag}_w"], g[f"{tag}_x"], g[f"{tag}_xk"]
+        Ys, Yc = np.zeros((d2, T2), np.float32), np.zeros((d2, T2), np.float32)
+        orc.orc_jas_mha(fp(X2), fp(X2), d2, H2, T2, T2, fp(W2), 1, fp(Ys))
+        orc.orc_jas_mha(fp(X2), fp(K2), d2, H2, T2, Tk2, fp(W2), 0, fp(Yc))
+        assert bits_equal(Ys, g[f"{tag}_self"]), tag
+        assert bits_equal(Yc, g[f"{tag}_cross"]), tag
 
 
 def test_golden_rope_and_transformer(g):
