@@ -116,7 +116,9 @@ def check(code):
         raise JasError(code, lib.jas_last_error().decode(errors="replace"))
 
 
-_DT = {np.dtype(np.float32): JAS_F32, np.dtype(np.float64): JAS_F64, np.dtype(np.int32): JAS_I32}
+# uint16 device arrays hold bf16 bit patterns
+_DT = {np.dtype(np.float32): JAS_F32, np.dtype(np.float64): JAS_F64, np.dtype(np.int32): JAS_I32,
+       np.dtype(np.uint16): JAS_BF16}
 
 
 class DeviceArray:

@@ -9,7 +9,9 @@
 //
 // Numerics follow jasmine's typing: every node carries its C++ ele_type; float nodes are
 // computed in float and double nodes in double, and each node's value is rounded to its
-// type before its parent uses it (the typed work() parameters do exactly that).
+// type before its parent uses it (the typed work() parameters do exactly that).  bf16
+// nodes (mat_t<jas::bf16>) compute in float and round the result to bf16, nearest even --
+// the arithmetic of the host jas::bf16 type.
 #include "jas_leaf.hpp"
 
 namespace jas {
@@ -32,15 +34,29 @@ constexpr int VEC = 4;
 typedef double regfile_t __attribute__((ext_vector_type(JAS_EW_MAX_STACK * VEC)));
 static_assert(JAS_EW_MAX_STACK * VEC == 16, "one 1024-bit register bank");
 
+__device__ __forceinline__ float round_bf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
 __device__ __forceinline__ double round_to(double v, int dt)
 {
     if (dt == JAS_F32) return (double)(float)v;
     if (dt == JAS_I32) return (double)(int32_t)v;
+    if (dt == JAS_BF16) return (double)round_bf16((float)v);
     return v;
 }
 
 __device__ __forceinline__ double binop(int op, int dt, double x, double y)
 {
+    if (dt == JAS_BF16) {
+        float a = (float)x, b = (float)y;
+        switch (op) {
+        case JAS_OP_ADD: return (double)round_bf16(a + b);
+        case JAS_OP_SUB: return (double)round_bf16(a - b);
+        case JAS_OP_MUL: return (double)round_bf16(a * b);
+        case JAS_OP_DIV: return (double)round_bf16(a / b);
+        case JAS_OP_GT: return a > b ? 1.0 : 0.0;
+        default: return a < b ? 1.0 : 0.0;
+        }
+    }
     if (dt == JAS_F32) {
         float a = (float)x, b = (float)y;
         switch (op) {
@@ -75,18 +91,19 @@ __device__ __forceinline__ double binop(int op, int dt, double x, double y)
 
 __device__ __forceinline__ double unop(int op, int dt, double x, double imm)
 {
-    if (dt == JAS_F32) {
-        float a = (float)x;
+    if (dt == JAS_F32 || dt == JAS_BF16) {
+        float a = (float)x, r;
         switch (op) {
-        case JAS_OP_EXP: return (double)expf(a);
-        case JAS_OP_SIGMOID: return (double)(float)(1.0 / (1.0 + (double)expf(-a)));
-        case JAS_OP_TANH: return (double)tanhf(a);
-        case JAS_OP_GELU: return (double)gelu_f(a);
-        case JAS_OP_SILU: return (double)silu_f(a);
-        case JAS_OP_SQRT: return (double)sqrtf(a);
-        case JAS_OP_POW: return (double)(float)pow((double)a, imm);
-        default: return (double)(-a);
+        case JAS_OP_EXP: r = expf(a); break;
+        case JAS_OP_SIGMOID: r = (float)(1.0 / (1.0 + (double)expf(-a))); break;
+        case JAS_OP_TANH: r = tanhf(a); break;
+        case JAS_OP_GELU: r = gelu_f(a); break;
+        case JAS_OP_SILU: r = silu_f(a); break;
+        case JAS_OP_SQRT: r = sqrtf(a); break;
+        case JAS_OP_POW: r = (float)pow((double)a, imm); break;
+        default: r = -a; break;
         }
+        return dt == JAS_BF16 ? (double)round_bf16(r) : (double)r;
     }
     switch (op) {
     case JAS_OP_EXP: return exp(x);
@@ -181,6 +198,9 @@ __global__ void __launch_bounds__(256) ew_eval_kernel(const EwArgs A)
     } else if (A.out_dtype == JAS_I32) {
         int32_t *o = (int32_t *)A.out + lin0;
         for (int e = 0; e < nv; ++e) o[e] = (int32_t)res[e];
+    } else if (A.out_dtype == JAS_BF16) {
+        uint16_t *o = (uint16_t *)A.out + lin0;
+        for (int e = 0; e < nv; ++e) o[e] = f32_to_bf16((float)res[e]);
     } else {
         float *o = (float *)A.out + lin0;
         if (A.contig_vec) {
@@ -196,6 +216,7 @@ __device__ __forceinline__ void store_elem(void *p, long idx, int dtype, double 
     switch (dtype) {
     case JAS_F64: ((double *)p)[idx] = v; break;
     case JAS_I32: ((int32_t *)p)[idx] = (int32_t)v; break;
+    case JAS_BF16: ((uint16_t *)p)[idx] = f32_to_bf16((float)v); break;
     default: ((float *)p)[idx] = (float)v; break;
     }
 }
@@ -255,8 +276,8 @@ extern "C" jas_status jas_ew_eval(const jas_ew_ins *prog, int n_ins, const jas_l
             return fail(JAS_ERR_INVALID, "jas_ew_eval: unknown op");
         }
         JAS_CHECK(sp <= JAS_EW_MAX_STACK, JAS_ERR_INVALID, "jas_ew_eval: expression too deep");
-        JAS_CHECK(in.dtype == JAS_F32 || in.dtype == JAS_F64 || in.dtype == JAS_I32, JAS_ERR_INVALID,
-                  "jas_ew_eval: bad node dtype");
+        JAS_CHECK(in.dtype == JAS_F32 || in.dtype == JAS_F64 || in.dtype == JAS_I32 || in.dtype == JAS_BF16,
+                  JAS_ERR_INVALID, "jas_ew_eval: bad node dtype");
     }
     JAS_CHECK(sp == 1, JAS_ERR_INVALID, "jas_ew_eval: program must leave exactly one value");
 
@@ -267,6 +288,8 @@ extern "C" jas_status jas_ew_eval(const jas_ew_ins *prog, int n_ins, const jas_l
     A.col_chunks = (cols + VEC - 1) / VEC;
     A.out = d_out;
     A.out_dtype = out_dtype;
+    JAS_CHECK(out_dtype == JAS_F32 || out_dtype == JAS_F64 || out_dtype == JAS_I32 || out_dtype == JAS_BF16,
+              JAS_ERR_INVALID, "jas_ew_eval: bad output dtype");
     bool vec = (cols % VEC) == 0 && ((uintptr_t)d_out % 16) == 0 && out_dtype == JAS_F32;
     for (int k = 0; k < n_leaves; ++k) {
         JAS_CHECK(leaves[k].d_data && leaves[k].rows > 0 && leaves[k].cols > 0, JAS_ERR_INVALID,

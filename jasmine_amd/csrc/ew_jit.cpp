@@ -36,6 +36,15 @@ struct JitArgs {
 
 static const char *kPrelude = R"JAS(
 typedef float fx4 __attribute__((ext_vector_type(4)));
+// bf16 elements: widened exactly; narrowed to nearest even (NaN stays a quiet NaN)
+__device__ __forceinline__ float bf2f(unsigned short v) { return __uint_as_float((unsigned)v << 16); }
+__device__ __forceinline__ unsigned short f2bf(float f)
+{
+    const unsigned u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)(((u >> 16) & 0x8000u) | 0x7fc0u);
+    return (unsigned short)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 struct JitLeaf { const void *p; long rs, cs; int rows, cols, row_first, roff, coff, transposed; };
 struct JitArgs { JitLeaf leaf[8]; void *out; int rows, cols, col_chunks; };
 __device__ __forceinline__ long gen_index(const JitLeaf &L, int i, int j)
@@ -67,7 +76,10 @@ __device__ __forceinline__ float silu_f(float x)
 static int g_jit_mode = 2;  // 0 never, 1 always, 2 large outputs only
 static constexpr long kAutoMinElems = 1L << 20;
 
+// C type of a node's value (bf16 nodes hold their rounded value in a float)
 static const char *ctype(int dt) { return dt == JAS_F64 ? "double" : dt == JAS_I32 ? "int" : "float"; }
+// C type of a stored element
+static const char *stype(int dt) { return dt == JAS_BF16 ? "unsigned short" : ctype(dt); }
 
 static std::string hexlit(double v)
 {
@@ -125,8 +137,9 @@ static Gen generate(const jas_ew_ins *prog, int n_ins, const LeafDev *leaves, in
     // leaf loads (each distinct operand once)
     for (int s = 0; s < g.n_slots; ++s) {
         const LeafDev &L = leaves[slot_src[s]];
-        const char *T = ctype(L.dtype);
-        o << "    " << T << " l" << s << "[4];\n    {\n        const " << T << " *p = (const " << T << " *)A.leaf[" << s
+        const char *T = ctype(L.dtype), *ST = stype(L.dtype);
+        const bool wb = L.dtype == JAS_BF16;
+        o << "    " << T << " l" << s << "[4];\n    {\n        const " << ST << " *p = (const " << ST << " *)A.leaf[" << s
           << "].p;\n";
         if (L.kind == LK_CONTIG && vec && L.dtype == JAS_F32) {
             o << "        const fx4 v = __builtin_nontemporal_load((const fx4 *)(p + lin0));\n"
@@ -134,13 +147,15 @@ static Gen generate(const jas_ew_ins *prog, int n_ins, const LeafDev *leaves, in
         } else {
             o << "#pragma unroll\n        for (int e = 0; e < 4; ++e) {\n";
             o << (vec ? "            const int ee = e;\n" : "            const int ee = e < nv ? e : 0;\n");
+            const char *w0 = wb ? "bf2f(" : "", *w1 = wb ? ")" : "";
             if (L.kind == LK_CONTIG)
-                o << "            l" << s << "[e] = p[lin0 + ee];\n";
+                o << "            l" << s << "[e] = " << w0 << "p[lin0 + ee]" << w1 << ";\n";
             else if (L.kind == LK_STRIDED)
-                o << "            l" << s << "[e] = p[(long)i * A.leaf[" << s << "].rs + (long)(j0 + ee) * A.leaf[" << s
-                  << "].cs];\n";
+                o << "            l" << s << "[e] = " << w0 << "p[(long)i * A.leaf[" << s << "].rs + (long)(j0 + ee) * A.leaf["
+                  << s << "].cs]" << w1 << ";\n";
             else
-                o << "            l" << s << "[e] = p[gen_index(A.leaf[" << s << "], i, j0 + ee)];\n";
+                o << "            l" << s << "[e] = " << w0 << "p[gen_index(A.leaf[" << s << "], i, j0 + ee)]" << w1
+                  << ";\n";
             o << "        }\n";
         }
         o << "    }\n";
@@ -154,10 +169,13 @@ static Gen generate(const jas_ew_ins *prog, int n_ins, const LeafDev *leaves, in
         const int dt = in.dtype;
         int vt = dt;
         std::ostringstream rhs;
+        // bf16 nodes: the float value rounded to bf16 (interpreter: round_to / binop / unop)
+        const bool nb = dt == JAS_BF16;
+        const char *r0 = nb ? "rbf(" : "", *r1 = nb ? ")" : "";
         if (in.op == JAS_OP_LEAF) {
-            rhs << "(" << ctype(dt) << ")l" << g.leaf_slot[in.arg] << "[e]";
+            rhs << r0 << "(" << ctype(dt) << ")l" << g.leaf_slot[in.arg] << "[e]" << r1;
         } else if (in.op == JAS_OP_CONST) {
-            rhs << "(" << ctype(dt) << ")" << hexlit(in.imm);
+            rhs << r0 << "(" << ctype(dt) << ")" << hexlit(in.imm) << r1;
         } else if (in.op >= JAS_OP_ADD && in.op <= JAS_OP_LT) {
             int hi = stack.back();
             stack.pop_back();
@@ -174,14 +192,15 @@ static Gen generate(const jas_ew_ins *prog, int n_ins, const LeafDev *leaves, in
             } else if (in.op == JAS_OP_DIV && dt == JAS_I32) {
                 rhs << "(" << b << ") ? " << a << " / " << b << " : 0";
             } else {
-                rhs << a << " " << op << " " << b;
+                rhs << r0 << a << " " << op << " " << b << r1;
             }
         } else {
             int x = stack.back();
             stack.pop_back();
             std::string xs = "v" + std::to_string(x);
-            if (dt == JAS_F32) {
+            if (dt == JAS_F32 || dt == JAS_BF16) {
                 std::string a = "(float)" + xs;
+                rhs << r0;
                 switch (in.op) {
                 case JAS_OP_EXP: rhs << "expf(" << a << ")"; break;
                 case JAS_OP_SIGMOID: rhs << "(float)(1.0 / (1.0 + (double)expf(-" << a << ")))"; break;
@@ -192,6 +211,7 @@ static Gen generate(const jas_ew_ins *prog, int n_ins, const LeafDev *leaves, in
                 case JAS_OP_POW: rhs << "(float)pow((double)" << a << ", " << hexlit(in.imm) << ")"; break;
                 default: rhs << "-" << a; break;
                 }
+                rhs << r1;
             } else {
                 // fp64 nodes (and int nodes, whose transcendental results stay unrounded)
                 std::string a = "(double)" + xs;
@@ -222,6 +242,8 @@ static Gen generate(const jas_ew_ins *prog, int n_ins, const LeafDev *leaves, in
     if (vec && out_dtype == JAS_F32) {
         o << "        ov[e] = res;\n    }\n"
              "    *(fx4 *)((float *)A.out + lin0) = fx4{ov[0], ov[1], ov[2], ov[3]};\n}\n";
+    } else if (out_dtype == JAS_BF16) {
+        o << "        if (" << (vec ? "true" : "e < nv") << ") ((unsigned short *)A.out)[lin0 + e] = f2bf(res);\n    }\n}\n";
     } else {
         o << "        if (" << (vec ? "true" : "e < nv") << ") ((" << OT << " *)A.out)[lin0 + e] = res;\n    }\n}\n";
     }

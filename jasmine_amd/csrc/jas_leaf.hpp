@@ -19,6 +19,7 @@ __device__ __forceinline__ double load_elem(const void *p, long idx, int dtype)
     switch (dtype) {
     case JAS_F64: return ((const double *)p)[idx];
     case JAS_I32: return (double)((const int32_t *)p)[idx];
+    case JAS_BF16: return (double)bf16_to_f32(((const uint16_t *)p)[idx]);
     default: return (double)((const float *)p)[idx];
     }
 }
@@ -63,7 +64,7 @@ static inline LeafDev classify(const jas_leaf &l, int rows, int cols)
         if (l.rows == 1) { a_i = a_j = 0; a0 = 0; }
         if (l.cols == 1) { b_i = b_j = 0; b0 = 0; }
         d.kind = LK_STRIDED;
-        long esz = l.dtype == JAS_F64 ? 8 : 4;
+        long esz = l.dtype == JAS_F64 ? 8 : l.dtype == JAS_BF16 ? 2 : 4;
         d.p = (const char *)l.d_data + (a0 * sa + b0 * sb) * esz;
         d.rs = a_i * sa + b_i * sb;
         d.cs = a_j * sa + b_j * sb;

@@ -10,8 +10,9 @@ operand first, swap flag on the binary op) so the device stack stays within 4 sl
 from dataclasses import dataclass, field
 from typing import Optional
 
-F32, F64, I32 = 0, 1, 2
-RANK = {I32: 0, F32: 1, F64: 2}
+F32, F64, I32, BF16 = 0, 1, 2, 3
+# bf16 with bf16 or int stays bf16; with float or double it widens (jas::bf16's common_type)
+RANK = {I32: 0, BF16: 1, F32: 2, F64: 3}
 OPS = {"leaf": 0, "const": 1, "+": 2, "-": 3, "*": 4, "/": 5, ">": 6, "<": 7, "exp": 8, "sigmoid": 9,
        "tanh": 10, "gelu": 11, "silu": 12, "sqrt": 13, "pow": 14, "neg": 15}
 
@@ -112,7 +113,7 @@ def evaluate(jas, root, out_dtype=None):
 
     prog, leaves = lower(root)
     dt = root.dtype if out_dtype is None else out_dtype
-    npdt = {F32: np.float32, F64: np.float64, I32: np.int32}[dt]
+    npdt = {F32: np.float32, F64: np.float64, I32: np.int32, BF16: np.uint16}[dt]
     out = DeviceArray((root.rows, root.cols), npdt)
     pa = (Ins * len(prog))(*[Ins(o, d, a, 0, i) for o, d, a, i in prog])
     la = (Leaf * max(1, len(leaves)))(*leaves)

@@ -6,6 +6,7 @@
 #include <atomic>
 #include <cstdint>
 #include <cstring>
+#include <ostream>
 #include <stdexcept>
 #include <string>
 #include <type_traits>
@@ -43,10 +44,45 @@ inline void ensure_init()
     }
 }
 
+// bf16 element type of mat_t<jas::bf16> (the reference gates mat_t on std::is_arithmetic_v,
+// mat_t.hpp:15-16, which no 16-bit float type passes).  Storage is the upper half of an
+// IEEE float; values convert to float exactly and from float round to nearest even (NaN
+// stays a quiet NaN).  Arithmetic on bf16 matrices is float arithmetic rounded to bf16 per
+// node, on the host and in the kernels alike.
+struct bf16 {
+    uint16_t bits = 0;
+    constexpr bf16() = default;
+    bf16(float f) : bits(from_float(f)) {}
+    template <typename T>
+    requires(std::is_arithmetic_v<T> && !std::is_same_v<T, float>)
+    bf16(T v) : bf16(static_cast<float>(v)) {}
+    operator float() const
+    {
+        const uint32_t u = (uint32_t)bits << 16;
+        float f;
+        std::memcpy(&f, &u, 4);
+        return f;
+    }
+    static uint16_t from_float(float f)
+    {
+        uint32_t u;
+        std::memcpy(&u, &f, 4);
+        if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)(((u >> 16) & 0x8000u) | 0x7fc0u);
+        return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    }
+};
+static_assert(sizeof(bf16) == 2 && std::is_trivially_copyable_v<bf16>, "bf16 is a 2-byte value");
+inline std::ostream &operator<<(std::ostream &o, bf16 v) { return o << static_cast<float>(v); }
+
+// element types mat_t accepts: jasmine's arithmetic types plus bf16
+template <typename T>
+constexpr bool element_v = std::is_arithmetic_v<T> || std::is_same_v<T, bf16>;
+
 template <typename T>
 constexpr int dtype_of()
 {
-    if constexpr (std::is_same_v<T, float>) return JAS_F32;
+    if constexpr (std::is_same_v<T, bf16>) return JAS_BF16;
+    else if constexpr (std::is_same_v<T, float>) return JAS_F32;
     else if constexpr (std::is_same_v<T, double>) return JAS_F64;
     else if constexpr (std::is_integral_v<T> && sizeof(T) == 4 && std::is_signed_v<T>) return JAS_I32;
     else return -1;
@@ -96,5 +132,23 @@ public:
 };
 
 } // namespace jas
+
+// promotion with bf16 operands (the node element type of jasmine's expression trees is the
+// std::common_type of its operands, mat_express_t.hpp:18-33): bf16 with bf16 or an integer
+// stays bf16; with float or double it widens to that type
+template <>
+struct std::common_type<jas::bf16, jas::bf16> {
+    using type = jas::bf16;
+};
+template <typename T>
+requires std::is_arithmetic_v<T>
+struct std::common_type<jas::bf16, T> {
+    using type = std::conditional_t<std::is_floating_point_v<T>, std::common_type_t<float, T>, jas::bf16>;
+};
+template <typename T>
+requires std::is_arithmetic_v<T>
+struct std::common_type<T, jas::bf16> {
+    using type = typename std::common_type<jas::bf16, T>::type;
+};
 
 #endif

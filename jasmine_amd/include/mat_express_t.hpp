@@ -69,7 +69,8 @@ using store_t = std::conditional_t<is_mat_v<T>, const T &, T>;
 template <typename T>
 constexpr int code_of()
 {
-    if constexpr (std::is_same_v<T, float>) return JAS_F32;
+    if constexpr (std::is_same_v<T, jas::bf16>) return JAS_BF16;
+    else if constexpr (std::is_same_v<T, float>) return JAS_F32;
     else if constexpr (std::is_floating_point_v<T>) return JAS_F64;
     else return JAS_I32;
 }
@@ -512,7 +513,16 @@ public:
     const mat_t<ele_type> &evaluate() const
     {
         if (m_cache) return *m_cache;
-        static_assert(std::is_same_v<ele_type, float> || std::is_same_v<ele_type, double>,
+        if constexpr (std::is_same_v<ele_type, jas::bf16>) {
+            // bf16 products: both operands widened exactly to float, fp32 MFMA GEMM with fp32
+            // accumulation, the result rounded to bf16
+            mat_t<float> af(jas::materialize(m_lval)), bf(jas::materialize(m_rval));
+            mat_t<float> cf = ::dot(af, bf).clone();
+            m_cache = std::make_shared<mat_t<ele_type>>(mat_t<ele_type>(cf));
+            return *m_cache;
+        }
+        static_assert(std::is_same_v<ele_type, float> || std::is_same_v<ele_type, double> ||
+                          std::is_same_v<ele_type, jas::bf16>,
                       "mat_dot_t runs on the fp32 / fp64 GEMM only");
         const int M = row_num(), N = col_num(), K = m_lval.col_num();
         auto a = jas::gemm_operand<ele_type>(m_lval);
@@ -530,7 +540,7 @@ public:
         if constexpr (std::is_same_v<ele_type, float>)
             jas::check(jas_gemm(M, N, K, a.p, a.s0, a.s1, b.p, b.s0, b.s1, c, N, 1, nullptr, 0, JAS_ACT_NONE, 0, 1,
                                 0, 0, 0, 0, nullptr));
-        else
+        else if constexpr (std::is_same_v<ele_type, double>)
             jas::check(jas_gemm_f64(M, N, K, a.p, a.s0, a.s1, b.p, b.s0, b.s1, c, N, 1, nullptr, 0, nullptr));
         if (M == 1 && N == 1) {
             ele_type v{};
@@ -574,7 +584,7 @@ auto jas::detail::unary_node<Derived, V, OP, OutT>::dot(const other_type &m) con
 }
 
 template <typename val_type>
-requires std::is_arithmetic_v<val_type>
+requires jas::element_v<val_type>
 template <typename other_type>
 requires is_matrix<other_type>
 auto mat_t<val_type>::dot(const other_type &m) const
@@ -592,7 +602,7 @@ auto mat_view_t<agent_type>::dot(const other_type &m) const
 
 // ---------------------------------------------------------------- mat_t members needing kernels
 template <typename val_type>
-requires std::is_arithmetic_v<val_type>
+requires jas::element_v<val_type>
 template <typename scalar_type>
 requires std::is_arithmetic_v<scalar_type>
 mat_t<val_type> &mat_t<val_type>::operator=(scalar_type s)
@@ -621,7 +631,7 @@ mat_t<val_type> &mat_t<val_type>::operator=(scalar_type s)
 }
 
 template <typename val_type>
-requires std::is_arithmetic_v<val_type>
+requires jas::element_v<val_type>
 template <typename other_val_type>
 requires std::is_convertible_v<other_val_type, val_type>
 mat_t<val_type>::mat_t(const mat_t<other_val_type> &m)
@@ -652,7 +662,7 @@ mat_t<val_type>::mat_t(const mat_t<other_val_type> &m)
 }
 
 template <typename val_type>
-requires std::is_arithmetic_v<val_type>
+requires jas::element_v<val_type>
 mat_t<val_type> &mat_t<val_type>::t_()
 {
     if (m_scalar) return *this;
@@ -663,11 +673,26 @@ mat_t<val_type> &mat_t<val_type>::t_()
 
 // ---------------------------------------------------------------- reductions
 namespace jas::detail {
+template <typename T, typename E>
+mat_t<T> reduce_as(const E &val, int op, int axis);
+
 // jas_reduce over any matrix operand; returns a device matrix of shape (rows_out, cols_out)
 template <typename E>
 mat_t<ele_of<E>> reduce(const E &val, int op, int axis)
 {
     using T = ele_of<E>;
+    if constexpr (std::is_same_v<T, jas::bf16>) {
+        // bf16 operands are read as such and summed in float; the result is rounded to bf16
+        mat_t<float> r = reduce_as<float>(val, op, axis);
+        return mat_t<jas::bf16>(r);
+    } else {
+        return reduce_as<T>(val, op, axis);
+    }
+}
+
+template <typename T, typename E>
+mat_t<T> reduce_as(const E &val, int op, int axis)
+{
     static_assert(std::is_same_v<T, float> || std::is_same_v<T, double>, "reductions run in float or double");
     std::shared_ptr<const void> hold;
     jas_leaf lf;
@@ -676,7 +701,7 @@ mat_t<ele_of<E>> reduce(const E &val, int op, int axis)
         if constexpr (is_mat_v<E>)
             if (val.is_scalar()) lf.rows = lf.cols = lf.vrows = lf.vcols = 1;
     } else {
-        auto m = std::make_shared<mat_t<T>>(materialize(val));
+        auto m = std::make_shared<mat_t<ele_of<E>>>(materialize(val));
         lf = m->leaf();
         hold = m;
     }

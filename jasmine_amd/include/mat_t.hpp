@@ -23,11 +23,11 @@ template <typename val_type>
 class mat_view_t;
 
 template <typename val_type>
-requires std::is_arithmetic_v<val_type>
+requires jas::element_v<val_type>
 class mat_t
 {
     template <typename U>
-    requires std::is_arithmetic_v<U>
+    requires jas::element_v<U>
     friend class mat_t;
 
 public:

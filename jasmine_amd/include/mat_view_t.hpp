@@ -123,21 +123,21 @@ public:
 
 // ---- mat_t's view factories (mat_view_t.hpp:137-243) ----
 template <typename val_type>
-requires std::is_arithmetic_v<val_type>
+requires jas::element_v<val_type>
 mat_view_t<mat_t<val_type>> mat_t<val_type>::t() noexcept
 {
     return mat_view_t<mat_t<val_type>>(*this).t();
 }
 
 template <typename val_type>
-requires std::is_arithmetic_v<val_type>
+requires jas::element_v<val_type>
 mat_view_t<mat_t<val_type>> mat_t<val_type>::view(int const &ro, int const &co, int const &rs, int const &cs) noexcept
 {
     return mat_view_t<mat_t<val_type>>(*this, ro, co, rs, cs);
 }
 
 template <typename val_type>
-requires std::is_arithmetic_v<val_type>
+requires jas::element_v<val_type>
 mat_view_t<const mat_t<val_type>> mat_t<val_type>::view(int const &ro, int const &co, int const &rs,
                                                         int const &cs) const noexcept
 {
@@ -146,13 +146,13 @@ mat_view_t<const mat_t<val_type>> mat_t<val_type>::view(int const &ro, int const
 
 #define JAS_VIEW_FACTORY(NAME, RO, CO, RS, CS)                                                                       \
     template <typename val_type>                                                                                     \
-    requires std::is_arithmetic_v<val_type>                                                                          \
+    requires jas::element_v<val_type>                                                                          \
     mat_view_t<mat_t<val_type>> mat_t<val_type>::NAME() noexcept                                                     \
     {                                                                                                                \
         return mat_view_t<mat_t<val_type>>(*this, RO, CO, RS, CS);                                                   \
     }                                                                                                                \
     template <typename val_type>                                                                                     \
-    requires std::is_arithmetic_v<val_type>                                                                          \
+    requires jas::element_v<val_type>                                                                          \
     mat_view_t<const mat_t<val_type>> mat_t<val_type>::NAME() const noexcept                                         \
     {                                                                                                                \
         return mat_view_t<const mat_t<val_type>>(*this, RO, CO, RS, CS);                                             \
@@ -164,28 +164,28 @@ JAS_VIEW_FACTORY(front_row, 0, 0, 1, col_num())
 #undef JAS_VIEW_FACTORY
 
 template <typename val_type>
-requires std::is_arithmetic_v<val_type>
+requires jas::element_v<val_type>
 mat_view_t<mat_t<val_type>> mat_t<val_type>::col(int const &idx) noexcept
 {
     return mat_view_t<mat_t<val_type>>(*this, 0, idx, row_num(), 1);
 }
 
 template <typename val_type>
-requires std::is_arithmetic_v<val_type>
+requires jas::element_v<val_type>
 mat_view_t<const mat_t<val_type>> mat_t<val_type>::col(int const &idx) const noexcept
 {
     return mat_view_t<const mat_t<val_type>>(*this, 0, idx, row_num(), 1);
 }
 
 template <typename val_type>
-requires std::is_arithmetic_v<val_type>
+requires jas::element_v<val_type>
 mat_view_t<mat_t<val_type>> mat_t<val_type>::row(int const &idx) noexcept
 {
     return mat_view_t<mat_t<val_type>>(*this, idx, 0, 1, col_num());
 }
 
 template <typename val_type>
-requires std::is_arithmetic_v<val_type>
+requires jas::element_v<val_type>
 mat_view_t<const mat_t<val_type>> mat_t<val_type>::row(int const &idx) const noexcept
 {
     return mat_view_t<const mat_t<val_type>>(*this, idx, 0, 1, col_num());

@@ -377,4 +377,84 @@ long api_transformer_nparams(int d, int H, int n_enc, int n_dec)
     return n;
 }
 
+// ---- mat_t<jas::bf16>: the same user code with bf16 matrices (inputs rounded from float,
+// outputs widened back to float) ----
+using bmat = mat_t<jas::bf16>;
+static bmat to_bmat(const float *p, int R, int C)
+{
+    bmat m(R, C);
+    for (int i = 0; i < R; ++i)
+        for (int j = 0; j < C; ++j) m(i, j) = p[(long)i * C + j];
+    return m;
+}
+
+int api_bf16_expr(int id, const float *A, int ar, int ac, const float *B, int br, int bc, float *out, int *out_r,
+                  int *out_c)
+{
+    return guarded([&] {
+        auto a = to_bmat(A, ar, ac), b = to_bmat(B, br, bc);
+        auto put = [&](const auto &r) {
+            *out_r = r.row_num();
+            *out_c = r.col_num();
+            if (out) from_mat(r, out);
+        };
+        switch (id) {  // the element type of each result follows the promotion rule
+        case 0: { bmat r = (a + b).clone(); put(r); break; }
+        case 1: { bmat r = (a - b * 2).clone(); put(r); break; }
+        case 2: { mat_t<double> r = (a * b / (b + 3.0)).clone(); put(r); break; }
+        case 3: { bmat r = exp(a - b).clone(); put(r); break; }
+        case 4: { bmat r = sigmoid(a * b).clone(); put(r); break; }
+        case 5: { bmat r = ((a > b) * a + (a < b) * b).clone(); put(r); break; }
+        case 6: { bmat r = ((a + b - a) * b / a).clone(); put(r); break; }
+        case 7: { mat_t<float> r = (a - 1.5f).clone(); put(r); break; }
+        case 8: { bmat r = (2 - a).clone(); put(r); break; }
+        case 9: { mat_t<double> r = (a.t() * 0.25 + b).clone(); put(r); break; }
+        default: throw std::invalid_argument("api_bf16_expr id");
+        }
+    });
+}
+
+int api_bf16_gemm(int M, int N, int K, const float *A, const float *B, float *C)
+{
+    return guarded([&] {
+        auto a = to_bmat(A, M, K), b = to_bmat(B, K, N);
+        bmat c = a.dot(b).clone();
+        from_mat(c, C);
+    });
+}
+
+int api_bf16_hsoftmax(const float *X, int R, int C, float *Y)
+{
+    return guarded([&] {
+        bmat y = hsoftmax(to_bmat(X, R, C));
+        from_mat(y, Y);
+    });
+}
+
+int api_bf16_reductions(const float *X, int R, int C, float *hs, float *vs, float *hm, float *scalars)
+{
+    return guarded([&] {
+        auto x = to_bmat(X, R, C);
+        from_mat(hsum(x), hs);
+        from_mat(vsum(x), vs);
+        from_mat(hmax(x), hm);
+        scalars[0] = sum(x);
+        scalars[1] = max(x);
+    });
+}
+
+int api_bf16_linear(const float *W, const float *b, const float *X, int out, int in, int T, float *Y)
+{
+    return guarded([&] {
+        weight_net_t<bmat, upd_t> net(in, out);
+        std::vector<float> buf((size_t)out * in + out);
+        std::memcpy(buf.data(), W, sizeof(float) * out * in);
+        std::memcpy(buf.data() + (size_t)out * in, b, sizeof(float) * out);
+        g_fixture = buf.data();
+        g_fixture_pos = 0;
+        net.init_weight<api_fixture_init_t>();
+        from_mat(net.forward(to_bmat(X, in, T)), Y);
+    });
+}
+
 }  // extern "C"

@@ -64,7 +64,8 @@ def test_api_library_exports(api):
     for name in ("api_gemm", "api_gemm_tn", "api_cfg2_expr", "api_expr", "api_hsoftmax", "api_softmax_global",
                  "api_reductions", "api_linear", "api_relu", "api_sigmoid", "api_layernorm_cols", "api_head",
                  "api_mha", "api_rope", "api_transformer", "api_transformer_nparams", "api_last_error", "api_set_fused_heads", "api_transformer_reencode", "api_predict_loop",
-                 "api_expr_deferred"):
+                 "api_expr_deferred", "api_bf16_expr", "api_bf16_gemm", "api_bf16_hsoftmax", "api_bf16_reductions",
+                 "api_bf16_linear"):
         assert hasattr(api, name), name
 
 
@@ -285,3 +286,118 @@ def test_api_predict_loop(api, g, tag):
     ok(api, api.api_predict_loop(fp(g[f"{tag}_en"]), Te, fp(g[f"{tag}_de0"]), d, H, ne, nd, fp(g[f"{tag}_w"]), steps,
                                  fp(Y)))
     close(Y, g[f"{tag}_y"])
+
+
+# ------------------------------------------------------------------ mat_t<jas::bf16>
+# The same user code with bf16 matrices.  Two checks per operation:
+#  * against a numpy model of bf16 arithmetic (float32 operation, then round to nearest even,
+#    per node, with the promotion rule: bf16 with bf16 or an integer stays bf16, with float or
+#    double widens) -- bit-exact where only + - * / and comparisons are involved, within one
+#    bf16 ulp where a libm-class function or an fp32 accumulation sits before the rounding;
+#  * against the reference's own fp32 outputs (golden) at the bf16 tolerance 5e-2 + 2e-2 |ref|.
+BF_ATOL, BF_RTOL = 5e-2, 2e-2
+
+
+def rb(x):
+    """float32 -> bf16 -> float32, round to nearest even (finite inputs)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return u.astype(np.uint32).view(np.float32)
+
+
+def bcast(x, R, C):  # jasmine's modulo broadcast (mat_t.hpp:304-305)
+    return x[np.arange(R)[:, None] % x.shape[0], np.arange(C)[None, :] % x.shape[1]]
+
+
+def within_ulp(got, want):
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    return np.all(np.abs(got - want) <= 2.0 ** -7 * np.abs(want) + 1e-30)
+
+
+def bf16_model(eid, a, b, R, C):
+    f32, f64 = np.float32, np.float64
+    if eid == 9:
+        A, B = bcast(rb(a).T, R, C), bcast(rb(b), R, C)
+        return A.astype(f64) * 0.25 + B.astype(f64)
+    A, B = bcast(rb(a), R, C), bcast(rb(b), R, C)
+    with np.errstate(all="ignore"):
+        if eid == 0: return rb(A + B)
+        if eid == 1: return rb(A - rb(B * f32(2)))
+        if eid == 2: return rb(A * B).astype(f64) / (B.astype(f64) + 3.0)
+        if eid == 3: return rb(np.exp(rb(A - B)))
+        if eid == 4: return rb((1.0 / (1.0 + np.exp(-rb(A * B)).astype(f64))).astype(f32))
+        if eid == 5: return rb(rb((A > B).astype(f32) * A) + rb((A < B).astype(f32) * B))
+        if eid == 6: return rb(rb(rb(rb(A + B) - A) * B) / A)
+        if eid == 7: return A - f32(1.5)
+        if eid == 8: return rb(f32(2) - A)
+    raise ValueError(eid)
+
+
+@pytest.mark.gpu
+def test_api_bf16_expressions(api, g):
+    n = 0
+    while f"expr{n}_id" in g:
+        eid = int(g[f"expr{n}_id"])
+        a, b, want = g[f"expr{n}_a"], g[f"expr{n}_b"], g[f"expr{n}_out"]
+        r, c = np.zeros(1, np.int32), np.zeros(1, np.int32)
+        out = np.zeros(want.shape, np.float32)
+        ok(api, api.api_bf16_expr(eid, fp(a), a.shape[0], a.shape[1], fp(b), b.shape[0], b.shape[1], fp(out), ip(r),
+                                  ip(c)))
+        assert (r[0], c[0]) == want.shape
+        model = np.asarray(bf16_model(eid, a, b, *want.shape), np.float32)
+        if eid in (3, 4):
+            assert within_ulp(out, model), (n, eid)
+        else:
+            assert bitexact(out, model), (n, eid)
+        if eid != 6:  # (a + b - a) cancels in bf16
+            close(out, want, atol=BF_ATOL, rtol=BF_RTOL)
+        n += 1
+    assert n >= 13
+
+
+@pytest.mark.gpu
+def test_api_bf16_gemm_linear_softmax_reductions(api, g):
+    A, B, want = g["gemm_a"], g["gemm_b"], g["gemm_c"]
+    M, K = A.shape
+    N = B.shape[1]
+    C = np.zeros((M, N), np.float32)
+    ok(api, api.api_bf16_gemm(M, N, K, fp(A), fp(B), fp(C)))
+    exact = (rb(A).astype(np.float64) @ rb(B).astype(np.float64)).astype(np.float32)
+    assert within_ulp(C, rb(exact))
+    close(C, want, atol=BF_ATOL, rtol=BF_RTOL)
+
+    W, b, X, want = g["linear_w"], g["linear_b"], g["linear_x"], g["linear_y"]
+    Y = np.zeros_like(want)
+    ok(api, api.api_bf16_linear(fp(W), fp(b), fp(X), W.shape[0], W.shape[1], X.shape[1], fp(Y)))
+    prod = rb((rb(W).astype(np.float64) @ rb(X).astype(np.float64)).astype(np.float32))
+    model = rb(prod + rb(b).reshape(-1, 1))
+    assert np.all(np.abs(Y - model) <= 2.0 ** -6 * np.abs(model) + 1e-30)  # two roundings
+    close(Y, want, atol=BF_ATOL, rtol=BF_RTOL)
+
+    x = g["x"]
+    R, Cc = x.shape
+    Ys = np.zeros_like(x)
+    ok(api, api.api_bf16_hsoftmax(fp(x), R, Cc, fp(Ys)))
+    xb = rb(x)
+    m = xb.max(1, keepdims=True)
+    e = rb(np.exp(rb(xb - m)))
+    s = np.zeros((R, 1), np.float32)
+    for j in range(Cc):  # the row sum runs in float, column by column
+        s[:, 0] = s[:, 0] + e[:, j]
+    model = rb(e / rb(s))
+    assert np.all(np.abs(Ys - model) <= 2.0 ** -6 * np.abs(model) + 1e-30)
+    close(Ys, g["hsoftmax"], atol=1e-2, rtol=BF_RTOL)
+    assert np.allclose(Ys.sum(1), 1.0, atol=3e-2)
+
+    hs, vs, hm = np.zeros(R, np.float32), np.zeros(Cc, np.float32), np.zeros(R, np.float32)
+    sc = np.zeros(2, np.float32)
+    ok(api, api.api_bf16_reductions(fp(x), R, Cc, fp(hs), fp(vs), fp(hm), fp(sc)))
+    rs = np.zeros(R, np.float32)
+    for j in range(Cc):
+        rs = rs + xb[:, j]
+    cs = np.zeros(Cc, np.float32)
+    for i in range(R):
+        cs = cs + xb[i, :]
+    assert bitexact(hs, rb(rs)) and bitexact(vs, rb(cs)) and bitexact(hm, xb.max(1))
+    close(hs, g["hsum"].reshape(hs.shape), atol=BF_ATOL, rtol=BF_RTOL)
+    assert sc[1] == xb.max()

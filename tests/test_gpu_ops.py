@@ -163,6 +163,54 @@ def test_ew_jit_equals_interpreter(jas):
     assert np.array_equal(a.view(np.uint8), b.view(np.uint8))
 
 
+def _rb(x):
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return (((u + 0x7FFF + ((u >> 16) & 1)) >> 16)).astype(np.uint16)
+
+
+def _wide(u16):
+    return (u16.astype(np.uint32) << 16).view(np.float32)
+
+
+def test_ew_bf16_leaves_and_nodes(jas):
+    """bf16 leaves and nodes (mat_t<jas::bf16>): float operation then round to nearest even
+    per node; interpreter and specialised kernel bit-identical; bf16 with an int constant stays
+    bf16, with a float leaf it widens."""
+    x, y = normal((300, 1030), 6, 0), normal((300, 1030), 6, 1)
+    bx, by = _rb(x), _rb(y)
+    dx, dy, df = jas.to_device(bx), jas.to_device(by), jas.to_device(y)
+    X, Y, Fy = E.leaf(dx, dtype=E.BF16), E.leaf(dy, dtype=E.BF16), E.leaf(df)
+    t = (X * Y + X) / (Y * 2 + 3) - (X > Y) * X
+    assert t.dtype == E.BF16
+    xf, yf = _wide(bx), _wide(by)
+    r = lambda v: _wide(_rb(v))
+    with np.errstate(all="ignore"):
+        want = r(r(r(r(xf * yf) + xf) / r(r(yf * np.float32(2)) + np.float32(3))) - r((xf > yf).astype(np.float32) * xf))
+    outs = []
+    for mode in (0, 1):
+        jas.lib.jas_ew_jit_mode(mode)
+        try:
+            outs.append(E.evaluate(jas, t))
+        finally:
+            jas.lib.jas_ew_jit_mode(2)
+    assert outs[0].dtype == np.uint16
+    assert np.array_equal(outs[0], outs[1])
+    assert np.array_equal(_wide(outs[0]), want)
+    mixed = X * Fy + E.un("exp", X * 0.5)  # float leaf and a double constant widen the tree
+    assert mixed.dtype == E.F64
+    got = []
+    for mode in (0, 1):
+        jas.lib.jas_ew_jit_mode(mode)
+        try:
+            got.append(E.evaluate(jas, mixed, out_dtype=E.BF16))
+        finally:
+            jas.lib.jas_ew_jit_mode(2)
+    a, b = got
+    assert np.array_equal(a, b)
+    ref = (xf.astype(np.float64) * y.astype(np.float64) + np.exp(xf.astype(np.float64) * 0.5))
+    assert np.all(np.abs(_wide(a) - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-6)
+
+
 def test_ew_rejects_bad_programs(jas):
     import ctypes as C
     from jasmine_amd.capi import Ins, Leaf, DeviceArray, lib
