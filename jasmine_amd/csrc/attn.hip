@@ -113,6 +113,9 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
     using T = typename std::conditional<BF16, uint16_t, float>::type;
     constexpr int EPC = 16 / (int)sizeof(T);    // elements per 16-byte chunk
     constexpr int KLD = D + (BF16 ? 8 : 4);    // padded row strides (elements)
+    // bf16 V rows are read with the transposing ds_read_b64_tr_b16: 16 rows x 4 column chunks
+    // per 16 lanes; a 40-dword row stride puts the four rows of a lane quad on disjoint banks
+    constexpr int KLDV = BF16 ? D + 16 : KLD;
     constexpr int CPR = D / EPC;                // 16-byte chunks per key row
     constexpr int NCH = BK * CPR;            // 16-byte chunks per tile and tensor
     constexpr int NLD = (NCH + NT - 1) / NT;    // chunks per thread per tensor and tile
@@ -123,7 +126,7 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
     __shared__ __attribute__((aligned(16))) T Ks[2][BK * KLD];
     // V row-major [BK][D] like K: the O = P V product reads its operand per key row (fp32:
     // one float per lane and key; bf16: the LDS transpose read, ds_read_b64_tr_b16)
-    __shared__ __attribute__((aligned(16))) T Vt[2][BK * KLD];
+    __shared__ __attribute__((aligned(16))) T Vt[2][BK * KLDV];
 
     const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, g = lane >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
@@ -202,7 +205,7 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
         const int idx = tid + it * NT, key = idx / CPR, ch = idx % CPR;                    \
         if (NCH % NT != 0 && idx >= NCH) break;                                            \
         *(u32x4 *)(&Ks[BUF][key * KLD + ch * EPC]) = KR[it];                               \
-        *(u32x4 *)(&Vt[BUF][key * KLD + ch * EPC]) = VR[it];                               \
+        *(u32x4 *)(&Vt[BUF][key * KLDV + ch * EPC]) = VR[it];                              \
     }
 
     // Pipeline: tile t is computed from LDS buffer t%2 while tile t+1 waits in registers
@@ -242,9 +245,9 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
             for (int c = 0; c < NC; ++c)
 #pragma unroll
                 for (int m = 0; m < NJ / 2; ++m) {
-                    const uint16_t *v0 = Vc + (32 * m + 4 * g + (r16 >> 2)) * KLD + 16 * c + 4 * (r16 & 3);
+                    const uint16_t *v0 = Vc + (32 * m + 4 * g + (r16 >> 2)) * KLDV + 16 * c + 4 * (r16 & 3);
                     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)v0);
-                    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(v0 + 16 * KLD));
+                    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(v0 + 16 * KLDV));
                     vfr[c][m] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 }
         }
@@ -347,7 +350,7 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
             for (int j = 0; j < NJ; ++j)
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    const float *vrow = Vc + (16 * j + 4 * g + t) * KLD + r16;
+                    const float *vrow = Vc + (16 * j + 4 * g + t) * KLDV + r16;
 #pragma unroll
                     for (int c = 0; c < NC; ++c) oacc[c] = mfma4(s[j][t], vrow[16 * c], oacc[c]);
                 }
