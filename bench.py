@@ -286,7 +286,7 @@ def run_kernel_legs(jas, reps=10):
 
 # ---------------------------------------------------------------- rocprofv3 summaries
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "llama7b_decode_b16_traffic.json")
-KCLASS = {"attention": ("attn_decode_kernel<128>", "attn_decode_merge_kernel<128>"), "weight_gemm": ("skinny_kernel<",)}
+KCLASS = {"attention": ("attn_decode_kernel<128,", "attn_decode_merge_kernel<128>")}
 
 
 def _pmc_per_kernel(csv_path, counter):
@@ -299,6 +299,22 @@ def _pmc_per_kernel(csv_path, counter):
         per.setdefault(r["Kernel_Name"], {}).setdefault(r["Dispatch_Id"], 0.0)
         per[r["Kernel_Name"]][r["Dispatch_Id"]] += float(r["Counter_Value"])
     return {k: list(v.values()) for k, v in per.items()}
+
+
+def _pmc_dispatches(fetch_csv, write_csv, pattern):
+    """[(FETCH_SIZE, WRITE_SIZE, kernel name)] per dispatch of kernels matching `pattern`, in
+    dispatch order (the two runs launch the same sequence)."""
+    import csv
+    def per(path, counter):
+        d = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] == counter and pattern in r["Kernel_Name"]:
+                k = int(r["Dispatch_Id"])
+                d.setdefault(k, [0.0, r["Kernel_Name"]])
+                d[k][0] += float(r["Counter_Value"])
+        return [d[k] for k in sorted(d)]
+    f, w = per(fetch_csv, "FETCH_SIZE"), per(write_csv, "WRITE_SIZE")
+    return [(a[0], b[0], a[1]) for a, b in zip(f, w)]
 
 
 def summarize_pmc(fetch_csv, write_csv, cfetch_csv, cwrite_csv, args):
@@ -322,8 +338,25 @@ def summarize_pmc(fetch_csv, write_csv, cfetch_csv, cwrite_csv, args):
                     n = (n or 0) + len(fk)
         if n:
             out["classes"][cls] = {"bytes_per_launch": tot / n, "launches": n}
+    # the skinny dispatches come in PROJ_ORDER, five each
+    sk = _pmc_dispatches(fetch_csv, write_csv, "skinny_kernel<")
+    per = {}
+    for i, (name, K, M) in enumerate(PROJ_ORDER):
+        rows = sk[5 * i:5 * i + 5]
+        if len(rows) == 5:
+            fb = np.mean([r[0] for r in rows]) * fcal * 1024.0
+            wb = np.mean([r[1] for r in rows]) * wcal * 1024.0
+            alg = 4.0 * M * K * (2 if name == "w_gate_up" else 1)
+            per[name] = {"fetch_bytes": fb, "write_bytes": wb, "weight_bytes": alg, "ratio": (fb + wb) / alg,
+                         "kernel": rows[0][2]}
+    out["weight_gemms"] = per
+    if per:
+        tot = sum(v["fetch_bytes"] + v["write_bytes"] for v in per.values())
+        alg = sum(v["weight_bytes"] for v in per.values())
+        out["classes"]["weight_gemm"] = {"bytes_per_launch": tot / len(per), "launches": 5 * len(per)}
     B, H, dh = args.batch, 32, 128
-    out["algorithmic"] = {"attention": B * H * profiled_mean_ctx(args) * dh * 8, "weight_gemm": None}
+    out["algorithmic"] = {"attention": B * H * profiled_mean_ctx(args) * dh * 8,
+                          "weight_gemm": (sum(v["weight_bytes"] for v in per.values()) / len(per)) if per else None}
     out["run"] = {"batch": B, "prompt": args.prompt, "steps": args.steps, "warmup": args.warmup}
     out["shape"] = {"batch": B, "heads": H, "head_dim": dh, "kv": "f32"}
     out["mean_ctx"] = profiled_mean_ctx(args)
@@ -338,6 +371,12 @@ def profiled_mean_ctx(args):
     P + warmup + steps .. P + warmup + 2 steps - 1; step s attends to position + 1 keys)."""
     pos1 = args.prompt + args.warmup + args.steps
     return pos1 + (args.steps + 1) / 2.0
+
+
+# (jas_lm_project name, K, M) of the LLaMA-7B decode weight GEMMs, in launch order; weight
+# bytes = 4 * M * K (gate_up: both matrices)
+PROJ_ORDER = [("w_qkv", 4096, 3 * 4096), ("w_o", 4096, 4096), ("w_gate_up", 4096, 11008), ("w_down", 11008, 4096),
+              ("w_head", 4096, 32000)]
 
 
 def traffic_kernels(args):
@@ -369,7 +408,23 @@ def traffic_kernels(args):
         jas.check(lib.jas_attn_decode(q.p, Kc.p, Vc.p, o.p, lens.p, B, H, D, max_len, H * max_len * D, max_len * D,
                                       C.c_float(D ** -0.5), ws.p, None))
     jas.check(lib.jas_synchronize(None))
-    print(json.dumps({"traffic_kernels": "attn_decode", "batch": B, "heads": H, "head_dim": D,
+    del Kc, Vc
+    # the decode weight GEMMs of one LLaMA-7B-width layer and the LM head, through
+    # jas_lm_project: the decode step's own skinny_kernel variants on the runner's packed
+    # weights, each launched five times in this order (pack_tokens_kernel and, for the split
+    # projections, sum_splits_kernel go with each launch)
+    lm = jas.Lm(llama_cfg(jas, B, 64))
+    lm.init_random(4, 0.02)
+    order = []
+    for name, K, M in PROJ_ORDER:
+        x, y = jas.DeviceArray((B, K)), jas.DeviceArray((B, M))
+        jas.check(lib.jas_fill_normal(x.p, B * K, 5, 3, 0.0, 1.0, None))
+        for _ in range(5):
+            lm.project(name, 0, x, y, B)
+        order.append(name)
+    jas.check(lib.jas_synchronize(None))
+    lm.close()
+    print(json.dumps({"traffic_kernels": ["attn_decode"] + order, "batch": B, "heads": H, "head_dim": D,
                       "mean_ctx": float(lens_h.mean()), "launches": 5}))
 
 

@@ -309,6 +309,15 @@ int jas_lm_position(jas_lm *lm);
  * above 1 = split over the cache plus the log-sum-exp merge; 0 = bad argument).  A query
  * for tests and tuning: no reference counterpart (jasmine has no KV cache). */
 int jas_lm_attn_splits(jas_lm *lm, int B);
+/* One of the runner's stored projections applied to B <= 16 token vectors with the decode
+ * step's own weight-streaming GEMM (same kernel variant and geometry): d_y[B][M] = W . x for
+ * d_x[B][K] (token-major, device).  Names: "w_qkv", "w_o", "w_fc", "w_proj", "w_down",
+ * "w_head" / "wte" (layer ignored) and "w_gate_up" (d_y[B][d_ff] = silu(W_gate x) * (W_up x)).
+ * No bias, no activation otherwise.  Runs on `stream` (NULL: the library stream) after
+ * draining the runner's stream, whose decode buffers it reuses (not concurrent with a decode).  No reference counterpart: weight_net_t::forward (mat_net_t.hpp:38-49) on the
+ * runner's packed weights, for callers that reuse a layer and for per-kernel measurement. */
+jas_status jas_lm_project(jas_lm *lm, const char *name, int layer, int B, const float *d_x, float *d_y,
+                          jas_stream_t stream);
 jas_stream_t jas_lm_stream(jas_lm *lm);
 /* Per-kernel-class GPU time (ms) accumulated with HIP events around every launch on the
  * runner's stream since the last reset; classes: 0 weight GEMM (decode), 1 attention decode,

@@ -85,6 +85,7 @@ _sigs = {
     "jas_lm_use_graph": [VP, I],
     "jas_lm_save": [VP, C.c_char_p], "jas_lm_load": [VP, C.c_char_p],
     "jas_lm_read_config": [C.c_char_p, C.POINTER(LmConfig)],
+    "jas_lm_project": [VP, C.c_char_p, I, I, VP, VP, VP],
 }
 for _n, _a in _sigs.items():
     getattr(lib, _n).argtypes = _a
@@ -250,6 +251,10 @@ class Lm:
     @property
     def position(self):
         return lib.jas_lm_position(self.h)
+
+    def project(self, name, layer, x_dev, y_dev, B, stream=None):
+        """y[B][M] = W . x with the decode GEMM on the stored weights (device arrays)."""
+        check(lib.jas_lm_project(self.h, name.encode(), int(layer), int(B), x_dev.p, y_dev.p, stream))
 
     def attn_splits(self, B):
         """Key splits the decode attention takes at batch B (1: one pass, no merge)."""

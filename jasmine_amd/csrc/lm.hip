@@ -118,6 +118,26 @@ __global__ void record_ids_kernel(const int32_t *ids, int32_t *hist, const int32
     if (b < B && step >= 0 && step < cap) hist[(long)step * B + b] = ids[b];
 }
 
+// token-major x [B][K] -> the packed B-operand layout of 16 token slots (slots >= B zero)
+__global__ void pack_tokens_kernel(const float *__restrict__ x, float *__restrict__ out, int B, int K)
+{
+    const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= 16L * K) return;
+    const int n = (int)(g / K), k = (int)(g % K);
+    out[packed_b_offset(n, k)] = n < B ? x[(long)n * K + k] : 0.f;
+}
+
+// y[n][m] = sum over the K splits, in split order, of part[(s * 16 + n) * M + m]
+__global__ void sum_splits_kernel(const float *__restrict__ part, int ks, int B, int M, float *__restrict__ y)
+{
+    const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= (long)B * M) return;
+    const int n = (int)(g / M), m = (int)(g % M);
+    float acc = part[(long)n * M + m];
+    for (int sp = 1; sp < ks; ++sp) acc += part[((long)sp * 16 + n) * M + m];
+    y[g] = acc;
+}
+
 __global__ void copy_ids_kernel(const int32_t *src, int32_t *dst, int B)
 {
     int b = blockIdx.x * blockDim.x + threadIdx.x;
@@ -734,6 +754,50 @@ jas_status jas_lm_generate(jas_lm *lm, int steps, int32_t *h_ids)
 }
 
 int jas_lm_position(jas_lm *lm) { return lm ? lm->position : -1; }
+
+jas_status jas_lm_project(jas_lm *lm, const char *name, int layer, int B, const float *d_x, float *d_y,
+                          jas_stream_t stream)
+{
+    JAS_CHECK(lm && name && d_x && d_y, JAS_ERR_INVALID, "jas_lm_project: null argument");
+    const jas_lm_config &c = lm->cfg;
+    JAS_CHECK(B >= 1 && B <= 16, JAS_ERR_INVALID, "jas_lm_project: 1 to 16 tokens");
+    const std::string n(name);
+    const bool head = n == "w_head" || n == "wte";
+    JAS_CHECK(head || (layer >= 0 && layer < c.n_layer), JAS_ERR_RANGE, "jas_lm_project: layer out of range");
+    const int d = c.d_model, F = c.d_ff, V = c.vocab;
+    const float *W = head ? lm->W(name) : lm->LW(n == "w_gate_up" ? "w_gate" : name, layer);
+    JAS_CHECK(W, JAS_ERR_INVALID, "jas_lm_project: no such projection for this model kind");
+    int M, K, ks = 0;
+    bool dual = false;
+    if (n == "w_qkv") M = 3 * d, K = d;
+    else if (n == "w_o") M = d, K = d, ks = lm->ks_o;
+    else if (n == "w_fc") M = F, K = d;
+    else if (n == "w_proj" || n == "w_down") M = d, K = F, ks = lm->ks_d;
+    else if (n == "w_gate_up") M = F, K = d, dual = true;
+    else if (head) M = V, K = d;
+    else return fail(JAS_ERR_INVALID, "jas_lm_project: unknown projection name");
+    // the library stream when `stream` is NULL, like every jas_* call; the runner's own
+    // stream is drained first, since its decode buffers are reused here
+    JAS_HIP(hipStreamSynchronize(lm->stream));
+    hipStream_t s = stream_or_default(stream);
+    float *xp = K == d ? lm->h : lm->ff;  // the runner's packed activation buffers
+    hipLaunchKernelGGL(pack_tokens_kernel, dim3(ceil_div(16L * K, 256)), dim3(256), 0, s, d_x, xp, B, K);
+    SkinnyEpiArgs e;
+    if (ks) {
+        e.mode = EPI_PARTIAL;
+        e.out = lm->part;
+        e.ksplit = ks;
+    } else {
+        e.mode = dual ? EPI_SWIGLU : EPI_STORE;
+        e.out = d_y;
+        e.ldo = M;
+    }
+    TRY(skinny_gemm(W, dual ? lm->LW("w_up", layer) : nullptr, xp, K, M, B, K, e, s, true, nullptr, lm->wbf16()));
+    if (ks)
+        hipLaunchKernelGGL(sum_splits_kernel, dim3(ceil_div((long)B * M, 256)), dim3(256), 0, s, lm->part, ks, B, M, d_y);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
 
 int jas_lm_attn_splits(jas_lm *lm, int B)
 {

@@ -325,3 +325,40 @@ def test_split_decode_gpt2_kind(jas):
     B = 8, 12 heads of 64 with a cache above 1024 keys (the unsplit form stops there)."""
     cfg = jas.LmConfig(0, 2, 768, 12, 256, 128, 1200, 8, 1e-5, 10000.0)
     run_parity_subset(jas, cfg, seed=33, B=8, P=700, steps=3, prompt_seed=33, check=(0, 5), want_splits=2)
+
+
+@pytest.mark.parametrize("kind,wb", [(1, 0), (0, 0), (1, 1)])
+def test_lm_project_matches_weights(jas, kind, wb):
+    """jas_lm_project runs the decode step's weight GEMM (same kernel variant) on one stored
+    projection: y = W x for 3 token vectors, against the weights read back (fp32 model)."""
+    import ctypes as C
+    cfg = jas.LmConfig(kind, 2, 256, 4, 320, 300, 32, 4, 1e-5 if kind == 0 else 1e-6, 10000.0, wb, 0)
+    lm = jas.Lm(cfg)
+    lm.init_random(17, 0.02)
+    rng = np.random.default_rng(3)
+    names = ["w_qkv", "w_o", "w_fc", "w_proj", "wte"] if kind == 0 else ["w_qkv", "w_o", "w_gate_up", "w_down", "w_head"]
+    for name in names:
+        layer = 1
+        def wmat(nm):
+            w = lm.weight(nm).reshape(lm.weight_shape(nm))
+            return w[layer] if w.shape[0] > 1 else w[0]
+        if name == "w_gate_up":
+            Wg, Wu = wmat("w_gate"), wmat("w_up")
+            M, K = Wg.shape
+        else:
+            W = wmat(name)
+            M, K = W.shape
+        x = rng.standard_normal((3, K)).astype(np.float32)
+        dx, dy = jas.to_device(x), jas.DeviceArray((3, M))
+        lm.project(name, layer, dx, dy, 3)
+        got = dy.numpy()
+        if name == "w_gate_up":
+            g = x.astype(np.float64) @ Wg.astype(np.float64).T
+            u = x.astype(np.float64) @ Wu.astype(np.float64).T
+            want = g / (1 + np.exp(-g)) * u
+        else:
+            want = x.astype(np.float64) @ W.astype(np.float64).T
+        close(got, want, atol=1e-4 * np.sqrt(K), rtol=1e-4)
+    from jasmine_amd import JasError
+    with pytest.raises(JasError):
+        lm.project("w_nope", 0, dx, dy, 3)
