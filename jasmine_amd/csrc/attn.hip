@@ -76,6 +76,16 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // 2^x on the hardware exp unit (v_exp_f32): results below 2^-126 flush to zero.  Used for
 // softmax terms 2^(s - max) <= 1, where such terms cannot change a sum that contains 1.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+// max over the four 16-lane rows of a wave (lanes l, l^16, l^32, l^48): gfx950's
+// permlane swaps exchange rows in registers (no LDS round trip, unlike a shuffle)
+__device__ __forceinline__ float max_across_rows(float v)
+{
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // a 16-byte chunk as a native vector (HIP's uint4 struct defeats register promotion)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -294,8 +304,7 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int r = (j == 0 ? 1 : 0); r < 4; ++r) tmax = fmaxf(tmax, s[j][r]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, WAVE));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, WAVE));
+        tmax = max_across_rows(tmax);
         const float m_new = fmaxf(m_run, tmax);
         // p = 2^(scale*log2e * (s - m)); a query with every key masked so far keeps m = -inf
         // and gets p = 0 from the -inf scores
