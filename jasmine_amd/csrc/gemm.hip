@@ -774,6 +774,26 @@ jas_status gemm_general(int M, int N, int K, const void *A, long as0, long as1, 
     return JAS_OK;
 }
 
+// first maximum (ties to the lowest index) over the four 16-lane rows of a wave: lanes l,
+// l ^ 16, l ^ 32, l ^ 48 end with the same pair (gfx950 permlane swaps, no LDS round trip)
+__device__ __forceinline__ void argmax_rows(float &bv, int &bi)
+{
+    auto step = [&](bool rows32) {
+        const unsigned vb = __float_as_uint(bv), ib = (unsigned)bi;
+        const auto pv = rows32 ? __builtin_amdgcn_permlane32_swap(vb, vb, false, false)
+                               : __builtin_amdgcn_permlane16_swap(vb, vb, false, false);
+        const auto pi = rows32 ? __builtin_amdgcn_permlane32_swap(ib, ib, false, false)
+                               : __builtin_amdgcn_permlane16_swap(ib, ib, false, false);
+        float av = __uint_as_float(pv[0]), ov = __uint_as_float(pv[1]);
+        int ai = (int)pi[0], oi = (int)pi[1];
+        if (ov > av || (ov == av && oi < ai)) { av = ov; ai = oi; }
+        bv = av;
+        bi = ai;
+    };
+    step(true);
+    step(false);
+}
+
 // ---------------------------------------------------------------- skinny (decode) GEMM
 // One workgroup per row group of 16 rows (NT tiles of 16 rows for NT > 1; DUAL: tile 0 from
 // W, tile 1 from W2 at the same 16 rows).  Its WPB waves interleave over the K chunks of 64
@@ -967,16 +987,46 @@ skinny_kernel(const void *__restrict__ W, const void *__restrict__ W2, const flo
 
     // epilogue: thread (t, ln) owns rows m..m+3 of tile t for token n = ln % 16
     const int n_items = NH * 64;
-    if (tid >= n_items) return;
     const int t = tid / 64, ln = tid % 64;
     const int n = ln & 15;
     const int m = m0 + t * 16 + 4 * (ln >> 4);
-    if (n >= N || m >= M) return;
-    floatx4 s0 = red[0][t][ln];
+    const bool live = tid < n_items && n < N && m < M;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    const int nv = live ? min(4, M - m) : 0;
+    if (live) {
+        floatx4 s0 = red[0][t][ln];
 #pragma unroll
-    for (int ww = 1; ww < WPB; ++ww) s0 += red[ww][t][ln];
-    float v[4] = {s0[0], s0[1], s0[2], s0[3]};
-    const int nv = min(4, M - m);
+        for (int ww = 1; ww < WPB; ++ww) s0 += red[ww][t][ln];
+        v[0] = s0[0], v[1] = s0[1], v[2] = s0[2], v[3] = s0[3];
+    }
+    if constexpr (!DUAL) {
+        if (epi.amax_v) {  // first maximum of the stored values over this workgroup's rows
+            __shared__ float sbv[NH * 16];
+            __shared__ int sbi[NH * 16];
+            float bv = -INFINITY;
+            int bi = 0x7fffffff;
+            for (int r = 0; r < nv; ++r) {
+                float x = epi.bias ? v[r] + epi.bias[m + r] : v[r];
+                x = apply_act(x, epi.act);
+                if (x > bv) { bv = x; bi = m + r; }
+            }
+            // the four lanes of a token in each wave (ln, ln ^ 16, ln ^ 32, ln ^ 48) combine in
+            // registers, then the tile waves' winners through LDS (ties to the lowest index)
+            argmax_rows(bv, bi);
+            if (tid < n_items && ln < 16) { sbv[t * 16 + ln] = bv; sbi[t * 16 + ln] = bi; }
+            __syncthreads();
+            if (tid < 16) {
+                for (int k = 1; k < NH; ++k) {
+                    const float ov = sbv[k * 16 + tid];
+                    const int oi = sbi[k * 16 + tid];
+                    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+                }
+                epi.amax_v[(long)tid * gridDim.x + blockIdx.x] = bv;
+                epi.amax_i[(long)tid * gridDim.x + blockIdx.x] = bi;
+            }
+        }
+    }
+    if (!live) return;
 
     if (epi.mode == EPI_PARTIAL) {  // raw split-K partial, [split][16][M]; the consumer reduces
         float *o = epi.out + ((long)blockIdx.y * 16 + n) * M + m;
@@ -1103,6 +1153,14 @@ SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split, bool wbf
 
 // K splits of a split-K residual projection: enough splits for about 256 workgroups with
 // the split geometry above, at most 8 and at least two 64-wide chunks per split
+int skinny_row_groups(int M, int K, bool dual, bool split, bool wbf16)
+{
+    const SkinnyTuning tu = skinny_default_tuning(M, K, dual, split, wbf16);
+    const int nt = dual && (tu.nt < 2 || tu.nt % 2) ? 2 : tu.nt;
+    const int rows = (dual ? nt / 2 : nt) * 16;
+    return (M + rows - 1) / rows;
+}
+
 int skinny_pick_ksplit(int M, int K, bool wbf16)
 {
     const int nt = skinny_default_tuning(M, K, false, true, wbf16).nt;

@@ -39,6 +39,10 @@ struct SkinnyEpiArgs {
     // optional [position][dh / 2] (cos, sin) of the rotary angles, the same double values
     // the epilogue would compute; saves the pow / cos / sin at the end of every workgroup
     const double2 *rope_tab = nullptr;
+    // EPI_STORE: also the first maximum over this workgroup's rows per token (the LM head's
+    // greedy pick), [token][workgroup]; argmax_finish reduces them
+    float *amax_v = nullptr;
+    int *amax_i = nullptr;
 };
 
 // Launch geometry of the weight-streaming GEMM: NT 16-row tiles per workgroup (non-SwiGLU)
@@ -47,6 +51,8 @@ struct SkinnyTuning {
     int nt = 1, wpb = 8, depth = 2;  // depth: chunk buffers in the load pipeline
 };
 SkinnyTuning skinny_default_tuning(int M, int K, bool dual, bool split = false, bool wbf16 = false);
+// workgroups along M of a default-tuned launch (the amax_v / amax_i partial count)
+int skinny_row_groups(int M, int K, bool dual, bool split = false, bool wbf16 = false);
 // K splits (<= 8, all non-empty) for an EPI_PARTIAL launch of an [M][K] weight
 int skinny_pick_ksplit(int M, int K, bool wbf16 = false);
 

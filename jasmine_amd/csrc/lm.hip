@@ -21,14 +21,6 @@
 namespace jas {
 
 
-__global__ void set_positions_kernel(int32_t *pos, int32_t *seqlens, int B, int p)
-{
-    int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b < B) {
-        pos[b] = p;
-        seqlens[b] = p + 1;
-    }
-}
 
 __global__ void prefill_positions_kernel(int32_t *pos, int B, int P)
 {
@@ -97,26 +89,73 @@ __global__ void embed_packed_kernel(const void *__restrict__ wte, const float *_
     out[g] = v;
 }
 
-// graph-replay form of set_positions_kernel: the position comes from (and advances) state[0]
-__global__ void advance_position_kernel(int32_t *state, int32_t *pos, int32_t *seqlens, int B)
+
+// The decode step's first kernel: the position (from the host, or from the device state
+// under graph replay) into pos / seqlens, and the embedding of every token at it.  PACKED:
+// GPT-2's tied, packed wte plus learned positions; else LLaMA's row-major table.
+template <bool PACKED, bool WB>
+__global__ void embed_step_kernel(const void *__restrict__ wte, const float *__restrict__ wpe,
+                                  const int32_t *__restrict__ ids, const int32_t *__restrict__ state, int host_pos,
+                                  int32_t *pos, int32_t *seqlens, float *__restrict__ out, int B, int d, int V)
 {
-    const int p = state[0];
-    const int b = threadIdx.x;
-    if (b < B) {
-        pos[b] = p;
-        seqlens[b] = p + 1;
+    const int p = state ? state[0] : host_pos;
+    const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g < B) {
+        pos[g] = p;
+        seqlens[g] = p + 1;
     }
-    __syncthreads();
-    if (b == 0) state[0] = p + 1;
+    if (g >= (long)B * d) return;
+    const int t = (int)(g / d), e = (int)(g % d);
+    float v;
+    if (PACKED) {
+        const long off = WB ? weight_pack_offset_b(ids[t], e, d, (V + 15) >> 4) : weight_pack_offset(ids[t], e, d, (V + 15) >> 4);
+        v = WB ? bf16_to_f32(((const uint16_t *)wte)[off]) : ((const float *)wte)[off];
+    } else {
+        v = ((const float *)wte)[(long)ids[t] * d + e];
+    }
+    if (wpe) v = v + wpe[(long)p * d + e];
+    out[g] = v;
 }
 
-// hist[(pos - state[1]) * B + b] = ids[b] for the step at position pos[0] (graph replay)
-__global__ void record_ids_kernel(const int32_t *ids, int32_t *hist, const int32_t *pos, const int32_t *state, int B,
-                                  int cap)
+// The decode step's last kernel, one workgroup per sequence: the first maximum over the LM
+// head's per-workgroup picks (ties to the lowest index) into ids; under graph replay also the
+// id into the history at step pos - state[1], and (sequence 0) the device position advanced.
+__global__ void __launch_bounds__(256) argmax_finish_kernel(const float *__restrict__ pv, const int *__restrict__ pi,
+                                                            int nch, int32_t *ids, int32_t *hist, const int32_t *pos,
+                                                            int32_t *state, int B, int cap)
 {
-    const int b = threadIdx.x, step = pos[0] - state[1];
-    if (b < B && step >= 0 && step < cap) hist[(long)step * B + b] = ids[b];
+    const int row = blockIdx.x;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int c = threadIdx.x; c < nch; c += 256) {
+        const float ov = pv[(long)row * nch + c];
+        const int oi = pi[(long)row * nch + c];
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {  // within the wave, then the four waves through LDS
+        const float ov = __shfl_xor(bv, o, WAVE);
+        const int oi = __shfl_xor(bi, o, WAVE);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    if (threadIdx.x % WAVE == 0) { sv[threadIdx.x / WAVE] = bv; si[threadIdx.x / WAVE] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; ++k)
+            if (sv[k] > bv || (sv[k] == bv && si[k] < bi)) { bv = sv[k]; bi = si[k]; }
+        const int id = bi == 0x7fffffff ? 0 : bi;
+        ids[row] = id;
+        if (state) {
+            const int p = pos[0], step = p - state[1];
+            if (step >= 0 && step < cap) hist[(long)step * B + row] = id;
+        }
+    }
+    // no other workgroup of this kernel reads state[0]: sequence 0's advances it
+    if (state && row == 0 && threadIdx.x == 0) state[0] = pos[0] + 1;
 }
+
 
 // token-major x [B][K] -> the packed B-operand layout of 16 token slots (slots >= B zero)
 __global__ void pack_tokens_kernel(const float *__restrict__ x, float *__restrict__ out, int B, int K)
@@ -267,11 +306,22 @@ jas_status decode_step(jas_lm *lm, bool device_pos)
     JAS_CHECK(device_pos || lm->position < c.max_ctx, JAS_ERR_RANGE,
               "jas_lm_decode: KV cache full (max_ctx reached)");
     hipStream_t s = lm->stream;
-    if (device_pos)
-        hipLaunchKernelGGL(advance_position_kernel, dim3(1), dim3(64), 0, s, lm->dstate, lm->pos, lm->seqlens, B);
-    else
-        hipLaunchKernelGGL(set_positions_kernel, dim3(1), dim3(256), 0, s, lm->pos, lm->seqlens, B, lm->position);
-    TRY(embed(lm, lm->ids, lm->pos, lm->x, B));
+    {  // positions and embeddings in one launch
+        TRY(prof_begin(lm, 2));
+        const dim3 grid(ceil_div((long)B * d, 256));
+        const int32_t *st = device_pos ? lm->dstate : nullptr;
+        if (c.kind == 0 && lm->wbf16())
+            hipLaunchKernelGGL((embed_step_kernel<true, true>), grid, dim3(256), 0, s, lm->W("wte"), lm->W("wpe"),
+                               lm->ids, st, lm->position, lm->pos, lm->seqlens, lm->x, B, d, V);
+        else if (c.kind == 0)
+            hipLaunchKernelGGL((embed_step_kernel<true, false>), grid, dim3(256), 0, s, lm->W("wte"), lm->W("wpe"),
+                               lm->ids, st, lm->position, lm->pos, lm->seqlens, lm->x, B, d, V);
+        else
+            hipLaunchKernelGGL((embed_step_kernel<false, false>), grid, dim3(256), 0, s, lm->W("wte"), nullptr,
+                               lm->ids, st, lm->position, lm->pos, lm->seqlens, lm->x, B, d, V);
+        JAS_LAUNCH_CHECK();
+        TRY(prof_end(lm));
+    }
     // The projections that feed the residual stream (O and down/proj) run K-split and leave
     // their partial sums in lm->part; the next norm kernel adds them (plus the bias) to x.
     int pend_ks = 0;
@@ -345,13 +395,21 @@ jas_status decode_step(jas_lm *lm, bool device_pos)
     TRY(resid_norm(lm->x, lm->part, pend_ks, pend_bias, lm->W("lnf_g"), lm->W("lnf_b"), lm->h, B, d, c.eps,
                    c.kind == 1, s, true));
     TRY(prof_end(lm));
+    // LM head; its epilogue also leaves each workgroup's greedy pick per sequence, and one
+    // small kernel finishes the argmax (and, under graph replay, records the id and advances
+    // the device position)
     SkinnyEpiArgs eh;
     eh.mode = EPI_STORE;
     eh.out = lm->logits;
     eh.ldo = V;
+    eh.amax_v = lm->amax_v;
+    eh.amax_i = lm->amax_i;
     TRY(proj(lm, c.kind == 0 ? lm->W("wte") : lm->W("w_head"), lm->h, B, V, d, eh));
     TRY(prof_begin(lm, 2));
-    TRY(argmax_impl(lm->logits, B, V, V, lm->ids, lm->argmax_ws, s));
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(B), dim3(256), 0, s, lm->amax_v, lm->amax_i,
+                       skinny_row_groups(V, d, false, false, lm->wbf16()), lm->ids, lm->hist, lm->pos,
+                       device_pos ? lm->dstate : nullptr, B, lm->hist_cap);
+    JAS_LAUNCH_CHECK();
     TRY(prof_end(lm));
     if (!device_pos) lm->position += 1;
     return JAS_OK;
@@ -453,7 +511,9 @@ jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out)
     if (st == JAS_OK) st = jas_malloc((void **)&lm->pos, 64 * sizeof(int32_t));
     if (st == JAS_OK) st = jas_malloc((void **)&lm->seqlens, 64 * sizeof(int32_t));
     if (st == JAS_OK) st = jas_malloc((void **)&lm->dstate, 2 * sizeof(int32_t));
-    if (st == JAS_OK) st = jas_malloc(&lm->argmax_ws, argmax_workspace_bytes(std::max(Bm, 64), V));
+    // the LM head's per-workgroup greedy picks: [16 tokens][row groups], at most V / 16 groups
+    if (st == JAS_OK) st = jas_malloc((void **)&lm->amax_v, sizeof(float) * 16 * (size_t)ceil_div(V, 16));
+    if (st == JAS_OK) st = jas_malloc((void **)&lm->amax_i, sizeof(int) * 16 * (size_t)ceil_div(V, 16));
     lm->attn_ws_bytes = jas_attn_decode_workspace(Bm, c.n_head, dh, c.max_ctx);
     for (int b = 1; b < Bm; ++b)  // workspace must cover every batch size actually used
         lm->attn_ws_bytes = std::max(lm->attn_ws_bytes, jas_attn_decode_workspace(b, c.n_head, dh, c.max_ctx));
@@ -483,7 +543,7 @@ jas_status jas_lm_destroy(jas_lm *lm)
     if (!lm) return JAS_OK;
     if (lm->stream) (void)hipStreamSynchronize(lm->stream);
     if (lm->graph) (void)hipGraphExecDestroy(lm->graph);
-    void *ptrs[] = {lm->argmax_ws, lm->dstate, lm->arena, lm->kc, lm->vc, lm->x, lm->h, lm->q, lm->att, lm->ff, lm->logits, lm->ids, lm->pos,
+    void *ptrs[] = {lm->amax_v, lm->amax_i, lm->dstate, lm->arena, lm->kc, lm->vc, lm->x, lm->h, lm->q, lm->att, lm->ff, lm->logits, lm->ids, lm->pos,
                     lm->seqlens, lm->hist, lm->attn_ws, lm->part, lm->pX, lm->pH, lm->pQKV, lm->pATT, lm->pG, lm->pU, lm->pFF,
                     lm->pIds, lm->pPos, lm->rope_tab};
     for (void *p : ptrs)
@@ -660,9 +720,13 @@ jas_status jas_lm_prefill(jas_lm *lm, int B, int P, const int32_t *h_ids, int32_
     eh.mode = EPI_STORE;
     eh.out = lm->logits;
     eh.ldo = V;
+    eh.amax_v = lm->amax_v;
+    eh.amax_i = lm->amax_i;
     TRY(skinny_gemm(c.kind == 0 ? lm->W("wte") : lm->W("w_head"), nullptr, lm->h, d, V, B, d, eh, s, true, nullptr,
                     lm->wbf16()));
-    TRY(argmax_impl(lm->logits, B, V, V, lm->ids, lm->argmax_ws, s));
+    hipLaunchKernelGGL(argmax_finish_kernel, dim3(B), dim3(256), 0, s, lm->amax_v, lm->amax_i,
+                       skinny_row_groups(V, d, false, false, lm->wbf16()), lm->ids, nullptr, nullptr, nullptr, B, 0);
+    JAS_LAUNCH_CHECK();
     lm->position = P;
     if (h_next) TRY(jas_memcpy_d2h(h_next, lm->ids, B * sizeof(int32_t), s));
     if (h_logits) TRY(jas_memcpy_d2h(h_logits, lm->logits, (size_t)B * V * sizeof(float), s));
@@ -698,10 +762,8 @@ jas_status capture_decode_graph(jas_lm *lm)
     }
     hipStream_t s = lm->stream;
     JAS_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    // the step's last kernel records the ids and advances the device position
     jas_status st = decode_step(lm, true);
-    if (st == JAS_OK)
-        hipLaunchKernelGGL(record_ids_kernel, dim3(1), dim3(64), 0, s, lm->ids, lm->hist, lm->pos, lm->dstate, lm->B,
-                           lm->hist_cap);
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(s, &g);  // always end the capture, also after a failure
     if (st != JAS_OK) {

@@ -49,7 +49,9 @@ struct jas_lm {
     // device-side decode state for graph replay: [0] next position, [1] first position of
     // the current jas_lm_generate call (its id history is indexed from there)
     int32_t *dstate = nullptr;
-    void *argmax_ws = nullptr;  // scratch of the two-pass argmax (allocated once: graph-safe)
+    // the LM head's per-workgroup greedy picks (allocated once: graph-safe)
+    float *amax_v = nullptr;
+    int *amax_i = nullptr;
     // one decode step captured as a HIP graph (for this batch size and id-history buffer)
     hipGraphExec_t graph = nullptr;
     bool use_graph = true;
