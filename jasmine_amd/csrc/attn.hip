@@ -6,8 +6,9 @@
 // the whole prefix every step.  Here:
 //  * prefill never materialises S: each workgroup owns 64 queries (16 per wave), streams
 //    64-key K/V tiles through LDS and keeps an online softmax.  The wave computes
-//    S^T = K Q^T with v_mfma_f32_16x16x4_f32 so that the probabilities land in exactly the
-//    B-operand layout of the O^T += V^T P^T product -- P never leaves registers.
+//    S^T = K Q^T on the matrix cores so that the probabilities land in exactly the operand
+//    layout of the second product (O += P V, or O^T += V^T P^T for bf16) -- P never leaves
+//    registers.
 //  * decode splits each (sequence, head)'s keys over workgroups (flash-decoding), each
 //    reading its K/V slice once from HBM, then merges the partial softmaxes by log-sum-exp.
 #include "jas_common.hpp"
@@ -73,6 +74,7 @@ constexpr int FA_WAVES = 8;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
+
 // 2^x on the hardware exp unit (v_exp_f32): results below 2^-126 flush to zero.  Used for
 // softmax terms 2^(s - max) <= 1, where such terms cannot change a sum that contains 1.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -111,10 +113,11 @@ __device__ __forceinline__ bool fa_work_item(int nqb, int BH, int nsplit, int &b
 // rows are double-staged: the global loads of tile t+1 are issued into registers before
 // tile t is computed from LDS, so HBM latency hides behind the matrix work.  Rows past
 // Sk are read clamped (finite data) and masked to probability 0.  fp32: S^T = K Q^T and
-// O^T += V^T P^T on v_mfma_f32_16x16x4_f32.  bf16: the same products on
+// O += P V on v_mfma_f32_16x16x4_f32.  bf16: S^T = K Q^T and O^T += V^T P^T on
 // v_mfma_f32_16x16x32_bf16 (fp32 accumulate, softmax in fp32, P rounded to bf16 for the
-// second product); the reduction index of each product is permuted identically in both
-// operands so that S lands in the P operand's registers with no shuffle.
+// second product), so every accumulator entry of a lane belongs to the lane's own query and
+// the rescale needs no cross-lane traffic; the reduction index of each product is permuted
+// identically in both operands so that S lands in the P operand's registers with no shuffle.
 template <int D, bool BF16, int BK, int NW = FA_WAVES>
 __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArgs p)
 {
@@ -155,7 +158,7 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
     const int k_lo = p.nsplit > 1 ? split * p.kchunk : 0;
     const int k_end = p.nsplit > 1 ? min(p.Sk, k_lo + p.kchunk) : p.causal ? min(p.Sk, q_last + shift + 1) : p.Sk;
     // keys this wave can see at all (causal): [0, wave_kend)
-    const int wave_kend = p.causal ? min(p.Sk, min(q0 + 15, p.Sq - 1) + shift + 1) : p.Sk;
+    const int wave_kend = min(k_end, p.causal ? min(p.Sk, min(q0 + 15, p.Sq - 1) + shift + 1) : p.Sk);
     const long kbase = (long)b * p.k_sb + (long)h * p.k_sh;
 
     // staging: chunk `it` of this thread is (key row, 16-byte column) of the 64-row tile
@@ -196,6 +199,9 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
     // the accumulator's query layout -- no per-score adds, no final shuffles
     floatx4 lacc = floatx4{0.f, 0.f, 0.f, 0.f};
     const float sl2 = p.scale_log2;
+    // bf16: the exponent base mb of this lane's query (exponent units, shared by the row's
+    // four lanes) and this lane's running max of its scores relative to it
+    float mb = 0.f, m_lane = -INFINITY;
 
     // Q fragments (B operand of S^T = K Q^T), raw (the scale is applied in the exponent)
     float4 qf[BF16 ? 1 : NC];
@@ -222,29 +228,47 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
     // (staged into the other buffer at the top of step t) and tile t+2 is in flight from HBM
     // into the other register set -- loads are issued two tiles ahead of their use.
     // Register set A holds the odd tiles, B the even ones (after tile 0).
-    if (k_end > k_lo) {
-        FA_GLOAD(k_lo, kra, vra)
-        FA_LSTORE(0, kra, vra)
-        if (k_lo + BK < k_end) { FA_GLOAD(k_lo + BK, kra, vra) }
-        if (k_lo + 2 * BK < k_end) { FA_GLOAD(k_lo + 2 * BK, krb, vrb) }
-    }
+    // Every step issues the same loads whether or not its tile exists (a tile past the work
+    // item's last one re-reads the last, an L2 hit): with a path-independent number of loads in
+    // flight the compiler's wait counts only cover the tile being staged, and the loads of the
+    // next two tiles stay in flight behind the matrix work.  Every work item has keys
+    // (k_end > k_lo).
+    const int k_last = k_lo + (k_end - k_lo - 1) / BK * BK;
+    FA_GLOAD(k_lo, kra, vra)
+    FA_LSTORE(0, kra, vra)
+    FA_GLOAD(min(k_lo + BK, k_last), kra, vra)
+    FA_GLOAD(min(k_lo + 2 * BK, k_last), krb, vrb)
     __syncthreads();
     auto tile = [&](const int kv0, const int buf) __attribute__((always_inline)) {
         const T *Kc = Ks[buf], *Vc = Vt[buf];
 
         // S^T tile: lane holds S^T[key = kv0 + 16j + 4g + r][query = qi] (raw scores)
         floatx4 s[NJ];
-        // bf16: every LDS fragment of the tile is requested up front -- K for S^T, and V for
-        // the second product, whose reads then complete behind the S products and the softmax
+        // bf16: the K fragments of the tile are requested first; the V fragments after the
+        // score products have been issued (reusing the K fragments' registers), and their
+        // reads complete behind the softmax
         bf16x8 kfr[BF16 ? NJ : 1][BF16 ? D / 32 : 1];
-        bf16x8 vfr[BF16 ? NC : 1][BF16 ? NJ / 2 : 1];
         if constexpr (BF16) {
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
 #pragma unroll
                 for (int c = 0; c < D / 32; ++c)
                     kfr[j][c] = *(const bf16x8 *)(Kc + (16 * j + r16) * KLD + 32 * c + 8 * g);
-            // B operand of O = P V for key block m, head-dim block c: lane (n = l%16, g) needs
+        }
+        // masking only on tiles that reach past Sk or cross this wave's causal diagonal: key
+        // kv0 + 16j + 4g + r is visible iff 16j + r <= lim, one compare per score
+        const bool need_mask = kv0 + BK > p.Sk || (p.causal && kv0 + BK - 1 > q0 + shift);
+        const int lim = (p.causal ? min(qi + shift, p.Sk - 1) : p.Sk - 1) - kv0 - 4 * g;
+        if constexpr (BF16) {
+            // raw scores; the NJ key blocks are independent accumulators, innermost so that
+            // consecutive matrix ops never wait on each other's result
+#pragma unroll
+            for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+                    s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kfr[j][c], qb16[c], c == 0 ? floatx4{0.f, 0.f, 0.f, 0.f} : s[j], 0, 0, 0);
+            bf16x8 vfr[NC][NJ / 2];
+            // A operand of O^T = V^T P^T for key block m, head-dim block c: lane (n = l%16, g) needs
             // V[key][16c + n] for keys 32m + 4g + 0..3 and 32m + 16 + 4g + 0..3.  The transpose
             // read hands lane n of each 16-lane group element n%4 of the 4-element chunks that
             // lanes n/4 + 4e address (e = 0..3), so lane i addresses row (key base + i/4),
@@ -260,18 +284,71 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
                     const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(v0 + 16 * KLDV));
                     vfr[c][m] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 }
-        }
-        // the NJ key blocks are independent accumulators: the j loop is innermost so that
-        // consecutive matrix ops never wait on each other's result
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) s[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-        if constexpr (BF16) {
-#pragma unroll
-            for (int c = 0; c < D / 32; ++c)
+            if (need_mask) {
 #pragma unroll
                 for (int j = 0; j < NJ; ++j)
-                    s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kfr[j][c], qb16[c], s[j], 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s[j][r] = 16 * j + r <= lim ? s[j][r] : -INFINITY;
+            }
+            // exponent units relative to the base: s <- sl2 s - mb (p = 2^s below)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s[j][r] = __builtin_fmaf(s[j][r], sl2, -mb);
+            // Lazy rescaling with a per-lane test: the base mb moves only when the row's running
+            // max leaves [mb - 64, mb + 8].  Meanwhile p stays below 2^8, numerator and row sum
+            // share the base, and O / l is unchanged.  Each lane tests only its own running max
+            // (taken after the fma: arithmetic results need no NaN canonicalisation before a
+            // max); the row max across the four lanes, and the move itself, are computed only
+            // when some lane trips, which for most inputs happens on no tile at all.  A query
+            // with no visible key keeps -inf maxima.
+            const float m_prev = m_lane;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) m_lane = fmaxf(fmaxf(m_lane, fmaxf(s[j][0], s[j][1])), fmaxf(s[j][2], s[j][3]));
+            if (__builtin_amdgcn_ballot_w64(m_lane > 8.f || (m_lane < -64.f && m_lane != -INFINITY))) {
+                const float row_prev = max_across_rows(m_prev), row = max_across_rows(m_lane);
+                if (row > 8.f || (row < -64.f && row != -INFINITY)) {
+                    // nothing accumulated yet (row_prev = -inf): factor 0, not 2^-row, which
+                    // overflows when the base moves far down
+                    const float corr = row_prev == -INFINITY ? 0.f : exp2_fast(-row);
+                    mb += row;
+                    m_lane -= row;
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) s[j] -= row;
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) oacc[c] *= corr;  // O^T: the lane's own query
+                    lacc *= corr;
+                }
+            }
+            // P^T operand for key block m (32 keys): slot t <-> key 32m + 16(t/4) + 4g + t%4,
+            // which are exactly s[2m][t] and s[2m+1][t-4] of this lane
+            bf16x8 pb[NJ / 2];
+#pragma unroll
+            for (int m = 0; m < NJ / 2; ++m)
+            {
+                float e[8];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    e[r] = exp2_fast(s[2 * m][r]);
+                    e[4 + r] = exp2_fast(s[2 * m + 1][r]);
+                }
+                pb[m] = bf16x8{(__bf16)e[0], (__bf16)e[1], (__bf16)e[2], (__bf16)e[3],
+                               (__bf16)e[4], (__bf16)e[5], (__bf16)e[6], (__bf16)e[7]};
+            }
+            // O^T += V^T P^T; row sums as P^T times a ones operand
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int m = 0; m < NJ / 2; ++m)
+                    oacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vfr[c][m], pb[m], oacc[c], 0, 0, 0);
+            const bf16x8 ones = bf16x8{(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f,
+                                       (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
+#pragma unroll
+            for (int m = 0; m < NJ / 2; ++m) lacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[m], lacc, 0, 0, 0);
         } else {
+            // raw scores; the NJ key blocks are independent accumulators (j innermost)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) s[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
                 float4 kf[NJ];
@@ -286,72 +363,44 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
 #pragma unroll
                 for (int j = 0; j < NJ; ++j) s[j] = mfma4(kf[j].w, qf[c].w, s[j]);
             }
-        }
-        // masking only on tiles that reach past Sk or cross this wave's causal diagonal
-        const bool need_mask = kv0 + BK > p.Sk || (p.causal && kv0 + BK - 1 > q0 + shift);
-        if (need_mask) {
+            if (need_mask) {
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) s[j][r] = 16 * j + r <= lim ? s[j][r] : -INFINITY;
+            }
+            float tmax = s[0][0];
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int kk = kv0 + 16 * j + 4 * g + r;
-                    const bool ok = kk < p.Sk && (!p.causal || kk <= qi + shift);
-                    s[j][r] = ok ? s[j][r] : -INFINITY;
-                }
-        }
-        float tmax = s[0][0];
+                for (int r = (j == 0 ? 1 : 0); r < 4; ++r) tmax = fmaxf(tmax, s[j][r]);
+            tmax = max_across_rows(tmax);
+            // lazy rescaling: the base m_run moves only when some query's max has grown by
+            // more than 2^8 in exponent units (or was -inf); p = 2^(sl2 (s - m_run)) stays below
+            // 256 meanwhile, and numerator and row sum share the stale base.  A query with
+            // every key masked so far keeps m = -inf and gets p = 0 from the -inf scores.
+            const float m_cand = fmaxf(m_run, tmax);
+            const float m_new = (m_cand - m_run) * sl2 > 8.f ? m_cand : m_run;  // NaN (-inf - -inf): keep
+            const float mb = m_new == -INFINITY ? 0.f : m_new * sl2;
+            const float corr = exp2_fast(m_run * sl2 - mb);  // 1 when kept; 0 from m_run = -inf
 #pragma unroll
-        for (int j = 0; j < NJ; ++j)
+            for (int j = 0; j < NJ; ++j)
 #pragma unroll
-            for (int r = (j == 0 ? 1 : 0); r < 4; ++r) tmax = fmaxf(tmax, s[j][r]);
-        tmax = max_across_rows(tmax);
-        const float m_new = fmaxf(m_run, tmax);
-        // p = 2^(scale*log2e * (s - m)); a query with every key masked so far keeps m = -inf
-        // and gets p = 0 from the -inf scores
-        const float mb = m_new == -INFINITY ? 0.f : m_new * sl2;
-        const float corr = exp2_fast(m_run * sl2 - mb);  // m_run = -inf on the first tile: 0
-#pragma unroll
-        for (int j = 0; j < NJ; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) s[j][r] = exp2_fast(__builtin_fmaf(s[j][r], sl2, -mb));
-        if constexpr (!BF16) {
+                for (int r = 0; r < 4; ++r) s[j][r] = exp2_fast(__builtin_fmaf(s[j][r], sl2, -mb));
             float psum = 0.f;
 #pragma unroll
             for (int j = 0; j < NJ; ++j) psum += (s[j][0] + s[j][1]) + (s[j][2] + s[j][3]);
             l_part = l_part * corr + psum;
-        }
-        m_run = m_new;
-        // rescale the accumulator only when some query's max moved (wave-uniform test)
-        if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
-            // oacc[c][r] is query 4g + r (O, not O^T), whose factor lives in lane 4g + r, the
-            // lane that owns that query's scores
-            floatx4 cr;
+            m_run = m_new;
+            if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
+                // oacc[c][r] is query 4g + r (O, not O^T), whose factor lives in lane 4g + r,
+                // the lane that owns that query's scores
+                floatx4 cr;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 4 * g + r, WAVE);
+                for (int r = 0; r < 4; ++r) cr[r] = __shfl(corr, 4 * g + r, WAVE);
 #pragma unroll
-            for (int c = 0; c < NC; ++c) oacc[c] *= cr;
-            if constexpr (BF16) lacc *= cr;
-        }
-
-        if constexpr (BF16) {
-            // P^T operand for key block m (32 keys): slot t <-> key 32m + 16(t/4) + 4g + t%4,
-            // which are exactly s[2m][t] and s[2m+1][t-4] of this lane
-            bf16x8 pb[NJ / 2];
-#pragma unroll
-            for (int m = 0; m < NJ / 2; ++m)
-                pb[m] = bf16x8{(__bf16)s[2 * m][0], (__bf16)s[2 * m][1], (__bf16)s[2 * m][2], (__bf16)s[2 * m][3],
-                               (__bf16)s[2 * m + 1][0], (__bf16)s[2 * m + 1][1], (__bf16)s[2 * m + 1][2],
-                               (__bf16)s[2 * m + 1][3]};
-#pragma unroll
-            for (int c = 0; c < NC; ++c)
-#pragma unroll
-                for (int m = 0; m < NJ / 2; ++m)
-                    oacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb[m], vfr[c][m], oacc[c], 0, 0, 0);
-            const bf16x8 ones = bf16x8{(__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f,
-                                       (__bf16)1.f, (__bf16)1.f, (__bf16)1.f, (__bf16)1.f};
-#pragma unroll
-            for (int m = 0; m < NJ / 2; ++m) lacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb[m], ones, lacc, 0, 0, 0);
-        } else {
+                for (int c = 0; c < NC; ++c) oacc[c] *= cr;
+            }
             // O[q][d = 16c + n] += sum_key P[q][key] V[key][d]: in product t of key block j the
             // lanes of group g contribute key 16j + 4g + t -- their own score s[j][t] as A and
             // V[16j + 4g + t][16c + n] (one float, consecutive across n) as B
@@ -370,54 +419,79 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
     // with buffer BUF before it is restaged
 #define FA_STEP(KV0, BUF, KR, VR)                                                            \
     {                                                                                        \
-        if ((KV0) + BK < k_end) {                                                            \
-            FA_LSTORE((BUF) ^ 1, KR, VR)                                                     \
-            if ((KV0) + 3 * BK < k_end) { FA_GLOAD((KV0) + 3 * BK, KR, VR) }                \
-        }                                                                                    \
-        if ((KV0) < wave_kend) tile(KV0, BUF); /* else every key is masked for this wave */  \
+        FA_LSTORE((BUF) ^ 1, KR, VR) /* unused when tile KV0 is the last */                \
+        FA_GLOAD(min((KV0) + 3 * BK, k_last), KR, VR)                                        \
+        if ((KV0) < wave_kend) tile(KV0, BUF); /* else no tile, or every key masked */       \
         __syncthreads();                                                                     \
     }
+    // both steps of an iteration always run (no break between them: a mid-loop exit gives the
+    // compiler a path with one register set in flight, and its wait counts then drain both)
     for (int kv0 = k_lo; kv0 < k_end; kv0 += 2 * BK) {
         FA_STEP(kv0, 0, kra, vra)
-        if (kv0 + BK >= k_end) break;
         FA_STEP(kv0 + BK, 1, krb, vrb)
     }
 #undef FA_STEP
     float l_run = l_part + __shfl_xor(l_part, 16, WAVE);
     l_run += __shfl_xor(l_run, 32, WAVE);
 
-    if (p.nsplit > 1) {  // unnormalised partial: O, then the row max (raw units) and row sum
+    if constexpr (BF16) {
+        // O^T accumulators: lane holds O[query = q0 + r16][d = 16c + 4g + r], its own query's
+        // row sum in lacc (every entry) and its base in m_run
+        if (qi >= p.Sq) return;
+        if (p.nsplit > 1) {  // unnormalised partial: O, then the row max (raw units) and row sum
+            float *row = p.part + (((long)split * p.B * p.H + bh) * p.Sq + qi) * (D + 2);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float lr = BF16 ? lacc[r] : __shfl(l_run, 4 * g + r, WAVE);
-            const float mr = __shfl(m_run, 4 * g + r, WAVE);
-            const int qo = q0 + 4 * g + r;
-            if (qo >= p.Sq) continue;
-            float *row = p.part + (((long)split * p.B * p.H + bh) * p.Sq + qo) * (D + 2);
+            for (int c = 0; c < NC; ++c)
 #pragma unroll
-            for (int c = 0; c < NC; ++c) row[16 * c + r16] = oacc[c][r];
-            if (r16 == 0) {
-                row[D] = mr;
-                row[D + 1] = lr;
+                for (int r = 0; r < 4; ++r) row[16 * c + 4 * g + r] = oacc[c][r];
+            if (g == 0) {  // the base in exponent units (-inf: no visible key)
+                row[D] = lacc[0] > 0.f ? mb : -INFINITY;
+                row[D + 1] = lacc[0];
             }
+            return;
         }
-        return;
-    }
-    // lane holds O[query = q0 + 4g + r][d = 16c + r16]; 1/l of query 4g + r from lane 4g + r
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const float lr = BF16 ? lacc[r] : __shfl(l_run, 4 * g + r, WAVE);
-        const int qo = q0 + 4 * g + r;
-        if (qo >= p.Sq) continue;
-        const float inv = lr > 0.f ? 1.0f / lr : 0.f;
-        const long orow = (long)b * p.o_sb + (long)h * p.o_sh + (long)qo * p.o_ss;
+        const float inv = lacc[0] > 0.f ? 1.0f / lacc[0] : 0.f;
+        const long orow = (long)b * p.o_sb + (long)h * p.o_sh + (long)qi * p.o_ss;
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            const float v = oacc[c][r] * inv;
-            if constexpr (BF16)
-                ((uint16_t *)p.O)[orow + 16 * c + r16] = __builtin_bit_cast(uint16_t, (__bf16)v);
-            else
-                ((float *)p.O)[orow + 16 * c + r16] = v;
+            uint2 o;
+            o.x = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(oacc[c][0] * inv)) |
+                  ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(oacc[c][1] * inv)) << 16);
+            o.y = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(oacc[c][2] * inv)) |
+                  ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(oacc[c][3] * inv)) << 16);
+            *(uint2 *)((uint16_t *)p.O + orow + 16 * c + 4 * g) = o;
+        }
+        return;
+    } else {
+        float l_run = l_part + __shfl_xor(l_part, 16, WAVE);
+        l_run += __shfl_xor(l_run, 32, WAVE);
+        if (p.nsplit > 1) {  // unnormalised partial: O, then the row max (raw units) and row sum
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float lr = __shfl(l_run, 4 * g + r, WAVE);
+                const float mr = __shfl(m_run, 4 * g + r, WAVE);
+                const int qo = q0 + 4 * g + r;
+                if (qo >= p.Sq) continue;
+                float *row = p.part + (((long)split * p.B * p.H + bh) * p.Sq + qo) * (D + 2);
+#pragma unroll
+                for (int c = 0; c < NC; ++c) row[16 * c + r16] = oacc[c][r];
+                if (r16 == 0) {
+                    row[D] = mr;
+                    row[D + 1] = lr;
+                }
+            }
+            return;
+        }
+        // lane holds O[query = q0 + 4g + r][d = 16c + r16]; 1/l of query 4g + r from lane 4g + r
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float lr = __shfl(l_run, 4 * g + r, WAVE);
+            const int qo = q0 + 4 * g + r;
+            if (qo >= p.Sq) continue;
+            const float inv = lr > 0.f ? 1.0f / lr : 0.f;
+            const long orow = (long)b * p.o_sb + (long)h * p.o_sh + (long)qo * p.o_ss;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) ((float *)p.O)[orow + 16 * c + r16] = oacc[c][r] * inv;
         }
     }
 #undef FA_GLOAD
@@ -425,7 +499,8 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
 }
 
 // Combines the key-split partials of a prefill launch: one thread per (row, head-dim
-// element); O = sum_i 2^((m_i - M) s) O_i / sum_i 2^((m_i - M) s) l_i with M = max_i m_i.
+// element); O = sum_i 2^((m_i - M) s) O_i / sum_i 2^((m_i - M) s) l_i with M = max_i m_i
+// (s = 1 for bf16 partials, whose m_i are already in exponent units).
 template <bool BF16>
 __global__ void __launch_bounds__(256) flash_merge_kernel(const PrefillArgs p, int D)
 {
@@ -442,7 +517,8 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(const PrefillArgs p, i
     float o = 0.f, l = 0.f;
     for (int i = 0; i < p.nsplit; ++i) {
         const float mi = pr[i * sstride + D];
-        const float w = mi == -INFINITY ? 0.f : exp2_fast((mi - mx) * p.scale_log2);
+        // bf16 partials carry their base in exponent units, fp32 ones their row max raw
+        const float w = mi == -INFINITY ? 0.f : exp2_fast(BF16 ? mi - mx : (mi - mx) * p.scale_log2);
         o += w * pr[i * sstride + e];
         l += w * pr[i * sstride + D + 1];
     }

@@ -476,6 +476,41 @@ def test_attn_prefill_long_causal(jas, B, H, Sq, Sk, D, dt):
             close(do.numpy(), want, atol=1e-5, rtol=1e-4)
 
 
+@pytest.mark.parametrize("D,dt,causal", [(64, 0, 1), (64, 3, 1), (128, 3, 0), (32, 3, 1), (128, 0, 0)])
+def test_attn_prefill_growing_scores(jas, D, dt, causal):
+    """Keys whose scale grows along the sequence, so the running row max keeps rising by more
+    than the lazy-rescale threshold (2^8 in exponent units) deep into the key range: the
+    accumulator is rescaled on late tiles, and probabilities above 1 (a stale base) are
+    exercised in between.  Raw scores reach about 100 here, so the fp32 rounding of a score
+    alone moves p by about 1e-5 relative: fp32 is held to 1e-4 abs (the configs' fp32 bound
+    is 1e-3)."""
+    B, H, S = 1, 2, 700
+    sc = 1 / math.sqrt(D)
+    Q = normal((B, H, S, D), 34, 0)
+    K = normal((B, H, S, D), 34, 1) * (1 + np.arange(S, dtype=np.float32) / 64)[None, None, :, None]
+    V = normal((B, H, S, D), 34, 2)
+
+    def bf(x):
+        u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+    def unbf(u):
+        return (u.astype(np.uint32) << 16).view(np.float32)
+
+    if dt:
+        Q, K, V = (unbf(bf(x)) for x in (Q, K, V))
+    want = np.zeros((B, H, S, D), np.float32)
+    orc.orc_attention(fp(Q), fp(K), fp(V), fp(want), B, H, S, S, D, sc, causal)
+    dq, dk, dv = (jas.to_device(bf(x) if dt else x) for x in (Q, K, V))
+    do = jas.DeviceArray((B, H, S, D), np.uint16 if dt else np.float32)
+    jas.check(jas.lib.jas_attn_prefill(dq.p, dk.p, dv.p, do.p, B, H, S, S, D, H * S * D, S * D, D, H * S * D,
+                                       S * D, D, H * S * D, S * D, D, sc, causal, dt, None))
+    if dt:
+        close(unbf(do.numpy()), want, atol=2e-2, rtol=2e-2)
+    else:
+        close(do.numpy(), want, atol=1e-4, rtol=1e-4)
+
+
 @pytest.mark.parametrize("B,H,D,lens", [(2, 3, 64, (1, 37)), (3, 2, 128, (1000, 513, 64)), (1, 4, 32, (2049,)),
                                         (8, 12, 64, (1024,) * 8)])
 def test_attn_decode(jas, B, H, D, lens):
