@@ -22,25 +22,36 @@ jas_status fail(jas_status code, const std::string &msg)
     return code;
 }
 
-// Library-internal scratch for multi-pass kernels (partials of whole-matrix reductions).
-// Grows on demand; calls on one stream are ordered, so reuse between calls is safe.
-static void *g_ws = nullptr;
-static size_t g_ws_bytes = 0;
+// Library-internal scratch for multi-pass kernels (partials of whole-matrix reductions,
+// prefill key-split partials, argmax partials): one buffer per stream, so work queued on
+// different streams never shares partials.  Calls on one stream run in order, so reuse
+// between them is safe; a buffer grows only after its own stream has drained (the old
+// buffer may still be read by queued kernels).  Issuing calls on one stream from two host
+// threads at once is not supported (neither is it by the reference, which has no threads).
+// A buffer lives until the process ends (streams destroyed by the caller leave theirs).
+struct Scratch {
+    void *p = nullptr;
+    size_t bytes = 0;
+};
+static std::mutex g_ws_mu;
+static std::unordered_map<hipStream_t, Scratch> g_ws;
 void *workspace(size_t bytes, hipStream_t s)
 {
-    if (bytes <= g_ws_bytes) return g_ws;
-    if (g_ws) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    Scratch &w = g_ws[s];
+    if (bytes <= w.bytes) return w.p;
+    if (w.p) {
         (void)hipStreamSynchronize(s);
-        (void)hipFree(g_ws);
+        (void)hipFree(w.p);
     }
     size_t nb = bytes < (1u << 20) ? (1u << 20) : bytes;
-    if (hipMalloc(&g_ws, nb) != hipSuccess) {
-        g_ws = nullptr;
-        g_ws_bytes = 0;
+    if (hipMalloc(&w.p, nb) != hipSuccess) {
+        w.p = nullptr;
+        w.bytes = 0;
         return nullptr;
     }
-    g_ws_bytes = nb;
-    return g_ws;
+    w.bytes = nb;
+    return w.p;
 }
 
 hipStream_t stream_or_default(jas_stream_t s)

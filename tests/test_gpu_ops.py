@@ -303,6 +303,33 @@ def test_softmax_global(jas):
     close(dy.numpy(), want, atol=1e-9, rtol=1e-4)
 
 
+def test_scratch_per_stream(jas):
+    """Whole-matrix softmax keeps its partials in library scratch: calls queued on two
+    streams without synchronising in between must not share it (one buffer per stream),
+    including when one stream's buffer grows while the other's work is in flight."""
+    import ctypes as C
+
+    hip = C.CDLL("libamdhip64.so")
+    sa, sb = C.c_void_p(), C.c_void_p()
+    assert hip.hipStreamCreateWithFlags(C.byref(sa), 1) == 0  # non-blocking, default priority
+    assert hip.hipStreamCreateWithFlags(C.byref(sb), 1) == 0
+    xa, xb = normal((512, 2048), 6, 0), normal((1024, 4096), 6, 1)
+    # float64 references: a sequential float sum over millions of terms drifts by ~1e-4
+    wa, wb = (np.exp(x.astype(np.float64) - x.max()) for x in (xa, xb))
+    wa, wb = wa / wa.sum(), wb / wb.sum()
+    dxa, dxb = jas.to_device(xa), jas.to_device(xb)
+    outs = [(jas.DeviceArray(xa.shape), jas.DeviceArray(xb.shape)) for _ in range(4)]
+    for ya, yb in outs:
+        jas.check(jas.lib.jas_softmax_global(dxa.p, ya.p, xa.size, sa))
+        jas.check(jas.lib.jas_softmax_global(dxb.p, yb.p, xb.size, sb))
+    assert hip.hipDeviceSynchronize() == 0
+    for ya, yb in outs:
+        close(ya.numpy(), wa, atol=0, rtol=1e-5)
+        close(yb.numpy(), wb, atol=0, rtol=1e-5)
+    hip.hipStreamDestroy(sa)
+    hip.hipStreamDestroy(sb)
+
+
 # ---------------------------------------------------------------- GEMM
 def _gemm_case(jas, M, N, K, ta=False, tb=False, col_c=False, bias_mode=0, act=0, acc=False, batch=1, seed=0):
     A = normal((batch, K, M) if ta else (batch, M, K), 10 + seed, 0)
