@@ -362,3 +362,33 @@ def test_lm_project_matches_weights(jas, kind, wb):
     from jasmine_amd import JasError
     with pytest.raises(JasError):
         lm.project("w_nope", 0, dx, dy, 3)
+
+
+@pytest.mark.parametrize("shape", ["config4_gpt2_small_b8_p512", "config5_llama7b_b16_p2048"])
+def test_full_shape_decode_equals_recompute(jas, shape):
+    """The benchmark workloads at their full shapes (the bench's seeds, batch and prompt
+    length), checked through the property the reference's decode loop rests on
+    (transformer_test.hpp:231-238): after a prefill, four HIP-graph decode steps and one
+    eager step, the step's logits equal those of a fresh prefill of the prompt plus every
+    generated token (fp32 bound 1e-3 abs + 1e-4 rel), and the greedy pick agrees."""
+    if shape.startswith("config4"):
+        kind, L, d, H, F, V, B, P, seed, eps = 0, 12, 768, 12, 3072, 50257, 8, 512, 3, 1e-5
+    else:
+        kind, L, d, H, F, V, B, P, seed, eps = 1, 32, 4096, 32, 11008, 32000, 16, 2048, 4, 1e-6
+    lm = jas.Lm(jas.LmConfig(kind, L, d, H, F, V, P + 16, B, eps, 10000.0))
+    try:
+        lm.init_random(seed, 0.02)
+        prompt = randint((B, P), V, seed)
+        nxt0, _ = lm.prefill(prompt)
+        gen = lm.generate(4, B)  # inputs: the prefill's picks, then each step's
+        nxt, lg = lm.decode(gen[-1], want_logits=True)
+        full = np.concatenate([prompt, nxt0[:, None], gen.T], 1)
+        assert full.shape == (B, P + 5)
+        nxt_full, lg_full = lm.prefill(full, want_logits=True)
+    finally:
+        lm.close()
+    close(lg, lg_full, atol=1e-3, rtol=1e-4)
+    top2 = np.sort(lg_full, axis=1)[:, -2:]
+    clear = top2[:, 1] - top2[:, 0] > 2e-3  # picks decided by more than the tolerance
+    assert clear.any()
+    assert np.array_equal(nxt[clear], nxt_full[clear])
