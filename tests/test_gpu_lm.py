@@ -370,7 +370,11 @@ def test_full_shape_decode_equals_recompute(jas, shape):
     length), checked through the property the reference's decode loop rests on
     (transformer_test.hpp:231-238): after a prefill, four HIP-graph decode steps and one
     eager step, the step's logits equal those of a fresh prefill of the prompt plus every
-    generated token (fp32 bound 1e-3 abs + 1e-4 rel), and the greedy pick agrees."""
+    generated token (fp32 bound 1e-3 abs + 1e-4 rel), and the greedy pick agrees.  (With
+    bf16 storage the property holds only loosely -- decode attends over the bf16-rounded
+    cache, a prefill over unrounded keys and values; 32 layers at 2048 positions put 0.13 abs
+    between them -- so that variant is held to the oracle, which rounds the cache as the
+    runner does, in test_bf16_storage.)"""
     if shape.startswith("config4"):
         kind, L, d, H, F, V, B, P, seed, eps = 0, 12, 768, 12, 3072, 50257, 8, 512, 3, 1e-5
     else:
