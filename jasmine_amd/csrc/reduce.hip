@@ -50,15 +50,20 @@ rowop_reg_kernel(const float *__restrict__ x, float *__restrict__ y, int len, lo
         for (int k = 0; k < PER; ++k)
             if (idx(k) < len && v[k] > m) m = v[k];
         m = block_max<NT>(m, red);
+        // exp(x - m) = 2^(x log2(e) - m log2(e)): one fma and the hardware exp per element
+        // (terms below 2^-126 flush to zero; the row max contributes 1), then one reciprocal
+        // of the row sum for the whole row -- the VALU otherwise paid a full-precision expf and
+        // an IEEE division per element
+        const float l2e = 1.4426950408889634f, ml = m * l2e;
         float s = 0.f;
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
-            v[k] = idx(k) < len ? expf(v[k] - m) : 0.f;
+            v[k] = idx(k) < len ? __builtin_amdgcn_exp2f(__builtin_fmaf(v[k], l2e, -ml)) : 0.f;
             s += v[k];
         }
-        s = block_sum<NT>(s, red);
+        const float inv = 1.0f / block_sum<NT>(s, red);
 #pragma unroll
-        for (int k = 0; k < PER; ++k) v[k] = v[k] / s;
+        for (int k = 0; k < PER; ++k) v[k] *= inv;
     } else if (MODE == RM_LN) {
         float s = 0.f;
 #pragma unroll
@@ -70,21 +75,21 @@ rowop_reg_kernel(const float *__restrict__ x, float *__restrict__ y, int len, lo
             float d = idx(k) < len ? v[k] - mean : 0.f;
             s2 += d * d;
         }
-        float den = sqrtf(block_sum<NT>(s2, red) / (float)len + eps);
+        const float inv = 1.0f / sqrtf(block_sum<NT>(s2, red) / (float)len + eps);  // one per row
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             int e = idx(k) < len ? idx(k) : 0;
-            v[k] = (v[k] - mean) / den * (g ? g[e] : 1.f) + (bta ? bta[e] : 0.f);
+            v[k] = (v[k] - mean) * inv * (g ? g[e] : 1.f) + (bta ? bta[e] : 0.f);
         }
     } else {
         float s2 = 0.f;
 #pragma unroll
         for (int k = 0; k < PER; ++k) s2 += v[k] * v[k];
-        float den = sqrtf(block_sum<NT>(s2, red) / (float)len + eps);
+        const float inv = 1.0f / sqrtf(block_sum<NT>(s2, red) / (float)len + eps);  // one per row
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             int e = idx(k) < len ? idx(k) : 0;
-            v[k] = v[k] / den * (g ? g[e] : 1.f);
+            v[k] = v[k] * inv * (g ? g[e] : 1.f);
         }
     }
 
@@ -120,23 +125,24 @@ rowop_loop_kernel(const float *__restrict__ x, float *__restrict__ y, int len, l
         for (int e = t; e < len; e += NT) m = xr[e] > m ? xr[e] : m;
         m = block_max<NT>(m, red);
         float s = 0.f;
-        for (int e = t; e < len; e += NT) s += expf(xr[e] - m);
-        s = block_sum<NT>(s, red);
-        for (int e = t; e < len; e += NT) yr[e] = expf(xr[e] - m) / s;
+        const float l2e = 1.4426950408889634f, ml = m * l2e;  // exp as in rowop_reg_kernel
+        for (int e = t; e < len; e += NT) s += __builtin_amdgcn_exp2f(__builtin_fmaf(xr[e], l2e, -ml));
+        const float inv = 1.0f / block_sum<NT>(s, red);
+        for (int e = t; e < len; e += NT) yr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(xr[e], l2e, -ml)) * inv;
     } else if (MODE == RM_LN) {
         float s = 0.f;
         for (int e = t; e < len; e += NT) s += xr[e];
         float mean = block_sum<NT>(s, red) / (float)len;
         float s2 = 0.f;
         for (int e = t; e < len; e += NT) { float d = xr[e] - mean; s2 += d * d; }
-        float den = sqrtf(block_sum<NT>(s2, red) / (float)len + eps);
+        const float inv = 1.0f / sqrtf(block_sum<NT>(s2, red) / (float)len + eps);
         for (int e = t; e < len; e += NT)
-            yr[e] = (xr[e] - mean) / den * (g ? g[e] : 1.f) + (bta ? bta[e] : 0.f);
+            yr[e] = (xr[e] - mean) * inv * (g ? g[e] : 1.f) + (bta ? bta[e] : 0.f);
     } else {
         float s2 = 0.f;
         for (int e = t; e < len; e += NT) s2 += xr[e] * xr[e];
-        float den = sqrtf(block_sum<NT>(s2, red) / (float)len + eps);
-        for (int e = t; e < len; e += NT) yr[e] = xr[e] / den * (g ? g[e] : 1.f);
+        const float inv = 1.0f / sqrtf(block_sum<NT>(s2, red) / (float)len + eps);
+        for (int e = t; e < len; e += NT) yr[e] = xr[e] * inv * (g ? g[e] : 1.f);
     }
 }
 
@@ -189,22 +195,24 @@ rowop_col_kernel(const float *__restrict__ x, float *__restrict__ y, int n_vec, 
         JAS_COL_LOOP(m = fmaxf(m, at(k, e));)
         m = combine(m, true);
         float s = 0.f;
-        JAS_COL_LOOP(s += expf(at(k, e) - m);)
+        const float l2e = 1.4426950408889634f, ml = m * l2e;  // exp as in rowop_reg_kernel
+        JAS_COL_LOOP(s += __builtin_amdgcn_exp2f(__builtin_fmaf(at(k, e), l2e, -ml));)
         s = combine(s, false);
-        JAS_COL_LOOP(yr[(long)e * estride] = expf(at(k, e) - m) / s;)
+        const float inv = 1.0f / s;
+        JAS_COL_LOOP(yr[(long)e * estride] = __builtin_amdgcn_exp2f(__builtin_fmaf(at(k, e), l2e, -ml)) * inv;)
     } else if (MODE == RM_LN) {
         float s = 0.f;
         JAS_COL_LOOP(s += at(k, e);)
         const float mean = combine(s, false) / (float)len;
         float s2 = 0.f;
         JAS_COL_LOOP(const float d = at(k, e) - mean; s2 += d * d;)
-        const float den = sqrtf(combine(s2, false) / (float)len + eps);
-        JAS_COL_LOOP(yr[(long)e * estride] = (at(k, e) - mean) / den * (g ? g[e] : 1.f) + (bta ? bta[e] : 0.f);)
+        const float inv = 1.0f / sqrtf(combine(s2, false) / (float)len + eps);
+        JAS_COL_LOOP(yr[(long)e * estride] = (at(k, e) - mean) * inv * (g ? g[e] : 1.f) + (bta ? bta[e] : 0.f);)
     } else {
         float s2 = 0.f;
         JAS_COL_LOOP(s2 += at(k, e) * at(k, e);)
-        const float den = sqrtf(combine(s2, false) / (float)len + eps);
-        JAS_COL_LOOP(yr[(long)e * estride] = at(k, e) / den * (g ? g[e] : 1.f);)
+        const float inv = 1.0f / sqrtf(combine(s2, false) / (float)len + eps);
+        JAS_COL_LOOP(yr[(long)e * estride] = at(k, e) * inv * (g ? g[e] : 1.f);)
     }
 #undef JAS_COL_LOOP
 }
@@ -432,16 +440,16 @@ resid_norm_kernel(float *__restrict__ x, const float *__restrict__ part, int ks,
         const float dv = e < d ? v[k] - mean : 0.f;
         s2 += dv * dv;
     }
-    const float den = sqrtf(block_sum<NT>(s2, red) / (float)d + eps);
+    const float inv = 1.0f / sqrtf(block_sum<NT>(s2, red) / (float)d + eps);  // one reciprocal per token
 #pragma unroll
     for (int k = 0; k < PER / 4; ++k) {
         const int e = (k * NT + t) * 4;
         if (e >= d) continue;
         float4 o;
-        o.x = (v[4 * k] - mean) / den * gg[k].x;
-        o.y = (v[4 * k + 1] - mean) / den * gg[k].y;
-        o.z = (v[4 * k + 2] - mean) / den * gg[k].z;
-        o.w = (v[4 * k + 3] - mean) / den * gg[k].w;
+        o.x = (v[4 * k] - mean) * inv * gg[k].x;
+        o.y = (v[4 * k + 1] - mean) * inv * gg[k].y;
+        o.z = (v[4 * k + 2] - mean) * inv * gg[k].z;
+        o.w = (v[4 * k + 3] - mean) * inv * gg[k].w;
         if (!RMS && bta) {
             o.x += bb4[k].x; o.y += bb4[k].y; o.z += bb4[k].z; o.w += bb4[k].w;
         }
