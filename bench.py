@@ -428,6 +428,26 @@ def traffic_kernels(args):
                       "mean_ctx": float(lens_h.mean()), "launches": 5}))
 
 
+def traffic_bf16_projections(args):
+    """The decode weight GEMMs of the bf16-storage variant alone (for rocprofv3 counter runs):
+    a LLaMA-7B-shape model with bf16 weights, each projection of layer 0 and the LM head
+    through jas_lm_project, five launches each, in PROJ_ORDER."""
+    import jasmine_amd as jas
+    lib = jas.lib
+    jas.check(lib.jas_init(0))
+    B = args.batch
+    lm = jas.Lm(llama_cfg(jas, B, 64, bf16=True))
+    lm.init_random(4, 0.02)
+    for name, K, M in PROJ_ORDER:
+        x, y = jas.DeviceArray((B, K)), jas.DeviceArray((B, M))
+        jas.check(lib.jas_fill_normal(x.p, B * K, 5, 3, 0.0, 1.0, None))
+        for _ in range(5):
+            lm.project(name, 0, x, y, B)
+    jas.check(lib.jas_synchronize(None))
+    lm.close()
+    print(json.dumps({"traffic_bf16_projections": [n for n, _, _ in PROJ_ORDER], "batch": B, "launches": 5}))
+
+
 def copy_calibration():
     """A plain device-to-device copy of COPY_BYTES (the copy-kernel reference for FETCH_SIZE /
     WRITE_SIZE), five times."""
@@ -527,6 +547,8 @@ def main():
     ap.add_argument("--copy-calib", action="store_true", help="only run the copy used to calibrate PMC bytes")
     ap.add_argument("--traffic-kernels", action="store_true",
                     help="only run the dominant decode kernel at the profiled pass's shape (for rocprofv3 --pmc)")
+    ap.add_argument("--traffic-bf16", action="store_true",
+                    help="only run the bf16-weight decode projections (for rocprofv3 counter runs)")
     ap.add_argument("--summarize-pmc", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV", "COPY_WRITE_CSV"),
                     help="write the traffic summary from rocprofv3 --pmc counter_collection.csv files")
     args = ap.parse_args()
@@ -535,6 +557,9 @@ def main():
         return
     if args.traffic_kernels:
         traffic_kernels(args)
+        return
+    if args.traffic_bf16:
+        traffic_bf16_projections(args)
         return
     if args.kernels_only:
         import jasmine_amd as jas
