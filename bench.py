@@ -222,6 +222,10 @@ def run_kernel_legs(jas, reps=10):
         return {"kernel": name, "avg_launch_us": round(ms * 1e3, 2), "bound": "mfma", "flops": flops,
                 "achieved": round(ach, 2), "unit": "TFLOP/s", "peak": peak, "frac": round(ach / peak, 4)}
 
+    # the achievable-bandwidth reference for the HBM-bound lines: the runtime's own
+    # device-to-device copy of one 8192^2 fp32 matrix (one read and one write per byte)
+    ms = time_launches(lambda: chk(lib.jas_memcpy_d2d(D.p, A.p, mb, None)), reps)
+    out["hbm_copy"] = line("device-to-device copy (HIP runtime), 268 MB: achievable-bandwidth reference", ms, 2 * mb)
     ms = time_launches(lambda: chk(lib.jas_ew_eval(pa, len(prog), la, len(leaves), D.p, 0, R, Cc, None)), reps)
     out["ew_cfg2"] = line("ew_eval_kernel: D = A*B + 0.5*C - tanh(A), 8192^2 fp32 (3 reads + 1 write)", ms, 4 * mb)
     ms = time_launches(lambda: chk(lib.jas_softmax(D.p, Y.p, R, Cc, Cc, Cc, 1, None)), reps)
