@@ -15,6 +15,7 @@
 
 #include <cfloat>
 #include <mutex>
+#include <unordered_map>
 
 namespace jas {
 
@@ -66,6 +67,8 @@ struct PrefillArgs {
     // its row max and row sum to part[split][b*H + h][q][D + 2]; a merge kernel combines them
     int nsplit = 1, kchunk = 0;
     float *part = nullptr;
+    // > 0: the CU count of a launch whose workgroups sit two to a CU (see fa_work_item)
+    int fold = 0;
 };
 
 // waves per workgroup (16 queries each), measured with the heaviest-first work order: 4 or
@@ -98,12 +101,18 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // ones starting late: about 1.4x longer for the causal config-3 shape).  Consecutive ids go
 // round robin to the 8 XCDs, so with B*H a multiple of 8 the query blocks of one head,
 // which share its K/V, stay on one XCD's L2.
-__device__ __forceinline__ bool fa_work_item(int nqb, int BH, int nsplit, int &bh, int &qb, int &split)
+// fold = C (the CU count, when workgroups sit two to a CU): ids i and i + C start together
+// on one CU, so ranks [C, 2C) are taken in reverse groups of 8 (the XCD of each rank kept):
+// the heaviest first-round items share their CU with the lightest of the second 256 rather
+// than with the next heaviest (a workgroup timeline of the config-3 launch showed CUs paired
+// 16 + 12 key tiles against others at 12 + 6).
+__device__ __forceinline__ bool fa_work_item(int nqb, int BH, int nsplit, int fold, int &bh, int &qb, int &split)
 {
     const int id = (int)blockIdx.x;
     if (id >= nqb * BH * nsplit) return false;
     split = id / (nqb * BH);
-    const int rem = id % (nqb * BH);
+    int rem = id % (nqb * BH);
+    if (fold > 0 && rem >= fold && rem < 2 * fold) rem = fold + (fold / 8 - 1 - (rem - fold) / 8) * 8 + (rem & 7);
     qb = nqb - 1 - rem / BH;
     bh = rem % BH;
     return true;
@@ -145,7 +154,7 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
     int bh, qb, split;
     const int nqb = (p.Sq + FA_BQ - 1) / FA_BQ;
-    if (!fa_work_item(nqb, p.B * p.H, p.nsplit, bh, qb, split)) return;
+    if (!fa_work_item(nqb, p.B * p.H, p.nsplit, p.fold, bh, qb, split)) return;
     const int b = bh / p.H, h = bh % p.H;
     const int q0 = qb * FA_BQ + w * 16;
     const int qi = q0 + r16;  // this lane's query (column of S^T)
@@ -826,6 +835,31 @@ static jas_status decode_scratch_ptr(void **out)
 
 using namespace jas;
 
+// fold argument of a causal launch (fa_work_item): the CU count when the kernel's workgroups
+// sit exactly two to a CU and the launch has at least two per CU, else 0.  Looked up once per
+// kernel and device.
+static int fa_fold(const void *kernel, int threads, int total)
+{
+    static std::mutex mu;
+    static std::unordered_map<const void *, int> cache;  // kernel -> workgroups per CU
+    int dev = 0, ncu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    int per = 0;
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        auto it = cache.find(kernel);
+        if (it == cache.end()) {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess) per = 0;
+            cache.emplace(kernel, per);
+        } else {
+            per = it->second;
+        }
+    }
+    return per == 2 && ncu % 8 == 0 && total >= 2 * ncu ? ncu : 0;
+}
+
 extern "C" {
 
 jas_status jas_attn_prefill(const void *Q, const void *K, const void *V, void *O, int B, int H, int Sq, int Sk, int D,
@@ -869,6 +903,7 @@ jas_status jas_attn_prefill(const void *Q, const void *K, const void *V, void *O
 #define JAS_FA_LAUNCH(DD, BF, NWV)                                                                     \
     {                                                                                                  \
         const int total = ceil_div(Sq, 16 * (NWV)) * B * H * p.nsplit;                                 \
+        p.fold = causal && p.nsplit == 1 ? fa_fold((const void *)flash_prefill_kernel<DD, BF, 64, NWV>, 64 * (NWV), total) : 0; \
         hipLaunchKernelGGL((flash_prefill_kernel<DD, BF, 64, NWV>), dim3((total + 7) / 8 * 8), dim3(64 * (NWV)), 0, s, p); \
     }
 #define JAS_FA(DD)                                                                                     \
