@@ -721,12 +721,16 @@ __global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p
     p.O[decode_out_index(p, bh, D, tid)] = L > 0.f ? A / L : 0.f;
 }
 
-// Split count: about max_len / (2*B*H) keys per split (at least 192) -- many splits when few
-// (sequence, head) pairs must fill the chip, three at the LLaMA-7B batch-16 shape -- then
+// Split count: splits of about 2*B*H keys (at least 192) -- many when few (sequence, head)
+// pairs must fill the chip -- but never more than two workgroups per CU need: one split
+// when the pairs alone give that (LLaMA-7B at batch 16: 512 pairs, no merge launch).  Then
 // max_len is cut into that many equal splits, so no workgroup is left with a short tail
-// (1024 + 1024 + 249 keys at 2297 streamed at 6.41 TB/s, 3 x 768 at 6.53).  A sequence's keys
-// fall into the same splits for a given max_len (the runner always passes its max_ctx);
-// splits past a shorter sequence's length are empty and carry zero weight in the merge.
+// (1024 + 1024 + 249 keys at 2297 streamed at 6.41 TB/s, 3 x 768 at 6.53).  Measured on
+// MI355X: one split against three at 16 x 32 pairs over 2300 keys, 176.7 against 181.7 us
+// plus the 4.5 us merge; 4 x 32 pairs, four splits against nine: 47.1 against 49.6 us; batch
+// 1 keeps its 12 (16.6 us, the best of 1..24).  A sequence's keys fall into the same splits
+// for a given max_len (the runner always passes its max_ctx); splits past a shorter
+// sequence's length are empty and carry zero weight in the merge.
 // bf16 caches take twice the keys per step (8 elements per lane), so their split count is
 // never larger than the fp32 one: the fp32 workspace size covers both.
 // "wide" form: one 16-wave workgroup per (sequence, head) over the whole context -- no split
@@ -735,6 +739,19 @@ __global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p
 // 8 x 12 pairs: 0.544 against 0.588 ms per step), but not a full 1024-key cache at the same
 // count (18 against 15 us: only 96 CUs stream).  The runner asks for it; jas_attn_decode
 // keeps the split form.
+// CUs of the current device (256 on MI355X), looked up once per device
+static int device_cu_count()
+{
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    return cached[dev];
+}
+
 constexpr int DECODE_WIDE_PAIRS = 128;
 static bool decode_wide_ok(int B, int H, int D, int max_len, bool kv_bf16)
 {
@@ -750,9 +767,12 @@ static int decode_nsplit(int B, int H, int D, int max_len, int *chunk, bool kv_b
         return 1;
     }
     const int keys_per_step = 4 * (WAVE / (D / (kv_bf16 ? 8 : 4))) * 4;  // NG * U
+    // splits of about 2*B*H keys (at least 192), but no more than two workgroups per CU need
     int ch = std::max(2 * B * H, 192);
     ch = (ch + keys_per_step - 1) / keys_per_step * keys_per_step;
+    const long pairs = (long)B * H, slots = 2L * device_cu_count();
     int ns = std::max(1, (max_len + ch - 1) / ch);
+    ns = (int)std::min<long>(ns, std::max(1L, (slots + pairs - 1) / pairs));
     // then equal splits of max_len (e.g. 3 x 768 keys instead of 1024 + 1024 + 249)
     ch = (max_len + ns - 1) / ns;
     ch = (ch + keys_per_step - 1) / keys_per_step * keys_per_step;

@@ -256,18 +256,23 @@ def test_weight_set_get_roundtrip(jas):
 
 # ---------------------------------------------------------------------------------------
 # Multi-split decode attention inside the runner.  The headline decode (LLaMA-7B shape,
-# B = 16, H = 32, d_h 128, cache of about 2100 keys) splits each (sequence, head) over the
-# cache and merges the splits by log-sum-exp into the packed O-projection operand; batch 1
-# takes about 11 splits.  These cases force that path (asserted through jas_lm_attn_splits)
-# with prompts long enough that several splits hold keys, and check the logits of every
-# step against the oracle.  The oracle runs the sequences named in `check` (sequences are
+# B = 16, H = 32, d_h 128, cache of about 2300 keys) has 512 (sequence, head) pairs, two per
+# CU, and takes one pass per pair that writes the packed O-projection operand itself; fewer
+# pairs split each pair's cache and merge the splits by log-sum-exp into that operand (batch
+# 4: four splits; batch 1: about 11).  These cases force each form (asserted through
+# jas_lm_attn_splits) with prompts long enough that several splits hold keys, and check the
+# logits of every step against the oracle.  The oracle runs the sequences named in `check`
+# (sequences are
 # independent, so a subset pins the batch); its cost is the prompt length times the weights.
 
-def run_parity_subset(jas, cfg, seed, B, P, steps, prompt_seed, check, want_splits):
+def run_parity_subset(jas, cfg, seed, B, P, steps, prompt_seed, check, want_splits, exact=False):
     lm = jas.Lm(cfg)
     lm.init_random(seed, 0.02)
     got_splits = lm.attn_splits(B)
-    assert got_splits >= want_splits, f"expected >= {want_splits} attention splits, runner takes {got_splits}"
+    if exact:
+        assert got_splits == want_splits, f"expected {want_splits} attention splits, runner takes {got_splits}"
+    else:
+        assert got_splits >= want_splits, f"expected >= {want_splits} attention splits, runner takes {got_splits}"
     ocfg, ow, keep = oracle_for(jas, lm, cfg)
     prompt = randint((B, P), cfg.vocab, prompt_seed)
     check = list(check)
@@ -295,12 +300,22 @@ def run_parity_subset(jas, cfg, seed, B, P, steps, prompt_seed, check, want_spli
 @pytest.mark.parametrize("kv_bf16", [0, 1])
 def test_split_decode_b16_h32(jas, kv_bf16):
     """B = 16, H = 32, d_h 128 (the headline's attention shape, d_model 4096), fp32 and bf16
-    KV cache: a 1100-key cache gives two splits of the cache (the fp32 one: 2 x 576 keys),
-    and the 600-token prompt puts keys in both; the merge writes the packed operand of the
-    O projection.  Oracle on sequences 0 and 15 (fp32 cache) or 7 (bf16 cache)."""
+    KV cache: 512 pairs take one pass each over the 1100-key cache, the attention kernel
+    writing the packed operand of the O projection directly (no merge).  Oracle on
+    sequences 0 and 15 (fp32 cache) or 7 (bf16 cache)."""
     cfg = jas.LmConfig(1, 2, 4096, 32, 64, 96, 1100, 16, 1e-6, 10000.0, 0, kv_bf16)
     run_parity_subset(jas, cfg, seed=31, B=16, P=600, steps=3, prompt_seed=31, check=(7,) if kv_bf16 else (0, 15),
-                      want_splits=2)
+                      want_splits=1, exact=True)
+
+
+@pytest.mark.parametrize("kv_bf16", [0, 1])
+def test_split_decode_b4_h32(jas, kv_bf16):
+    """B = 4 at the headline's head shape (32 heads of 128), fp32 and bf16 KV cache: 128
+    pairs split a 1100-key cache four ways (fp32: 4 x 288 keys; bf16: 4 x 320), the
+    600-token prompt puts keys in three of them, and the merge writes the packed operand of
+    the O projection.  Oracle on sequences 0 and 3."""
+    cfg = jas.LmConfig(1, 2, 4096, 32, 64, 96, 1100, 4, 1e-6, 10000.0, 0, kv_bf16)
+    run_parity_subset(jas, cfg, seed=34, B=4, P=600, steps=3, prompt_seed=34, check=(0, 3), want_splits=3)
 
 
 @pytest.mark.parametrize("kv_bf16", [0, 1])
@@ -314,10 +329,10 @@ def test_split_decode_batch1_many_splits(jas, kv_bf16):
 
 def test_split_decode_real_width_b16(jas):
     """B = 16 at the full LLaMA-7B width (d 4096, 32 heads, SwiGLU 11008, vocab 32000),
-    2 layers, with the cache long enough for two attention splits; oracle on sequence 15
-    with a 560-token prompt (keys in both splits)."""
+    2 layers, 1100-key cache (one attention pass per pair, as in the headline); oracle on
+    sequence 15 with a 560-token prompt."""
     cfg = jas.LmConfig(1, 2, 4096, 32, 11008, 32000, 1100, 16, 1e-6, 10000.0)
-    run_parity_subset(jas, cfg, seed=4, B=16, P=560, steps=2, prompt_seed=4, check=(15,), want_splits=2)
+    run_parity_subset(jas, cfg, seed=4, B=16, P=560, steps=2, prompt_seed=4, check=(15,), want_splits=1, exact=True)
 
 
 def test_split_decode_gpt2_kind(jas):

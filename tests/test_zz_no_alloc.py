@@ -3,7 +3,7 @@
 Both run the same kernels; only where the split partials live differs (a static device array
 against the caller's workspace), so the outputs must be bit-identical.  Two calls in a row,
 the second with a smaller shape, check that the shared array carries nothing from one call
-into the next; a shape whose partials exceed the array is rejected before any launch."""
+into the next; the array holds the partials of every shape."""
 import math
 
 import numpy as np
@@ -34,19 +34,23 @@ def _decode_both(jas, B, H, D, lens, seed):
 
 
 def test_noalloc_decode_matches_workspace_entry(jas):
-    # first call: 16 x 32 heads of 128 over up to 2100 keys (3 splits); second: a smaller
+    # first call: 4 x 32 heads of 128 over up to 2100 keys (4 splits); second: a smaller
     # shape (4 x 8 heads of 64, ragged lengths, more splits per pair) in the same array
-    for B, H, D, lens, seed in ((16, 32, 128, [2100 - 37 * i for i in range(16)], 71),
+    for B, H, D, lens, seed in ((4, 32, 128, [2100 - 370 * i for i in range(4)], 71),
                                 (4, 8, 64, [900, 1, 333, 517], 72)):
         want, got = _decode_both(jas, B, H, D, lens, seed)
         assert np.isfinite(want).all()
         assert np.array_equal(got, want), f"B={B} H={H} D={D}: max diff {np.abs(got - want).max():.3g}"
 
 
-def test_noalloc_decode_rejects_oversize(jas):
-    from jasmine_amd import JasError
-    B, H, D, ml = 16, 128, 128, 200000  # partials far beyond the static array
-    assert jas.lib.jas_attn_decode_workspace(B, H, D, ml) > jas.lib.jas_attn_decode_scratch_max()
-    with pytest.raises(JasError, match="scratch"):
-        # null tensors: the size check comes first, nothing is launched
-        jas.check(jas.lib.jas_attn_decode_noalloc(None, None, None, None, None, B, H, D, ml, 0, 0, 1.0, None))
+def test_noalloc_scratch_covers_every_shape(jas):
+    """The split count never asks for more than two workgroups per CU beyond the pairs
+    themselves, so the partials of any shape stay below about 0.5 MB on this part and fit the
+    static array (the entry point still checks the size and rejects a shape that would not)."""
+    cap = jas.lib.jas_attn_decode_scratch_max()
+    worst = 0
+    for D in (32, 64, 128):
+        for pairs in list(range(1, 130)) + [200, 255, 256, 257, 300, 384, 511, 512, 513, 1024, 4096]:
+            for ml in (1, 100, 1000, 2300, 20000, 200000):
+                worst = max(worst, jas.lib.jas_attn_decode_workspace(1, pairs, D, ml))
+    assert 0 < worst <= cap, (worst, cap)
