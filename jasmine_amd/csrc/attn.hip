@@ -728,7 +728,8 @@ __global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p
 // (1024 + 1024 + 249 keys at 2297 streamed at 6.41 TB/s, 3 x 768 at 6.53).  Measured on
 // MI355X: one split against three at 16 x 32 pairs over 2300 keys, 176.7 against 181.7 us
 // plus the 4.5 us merge; 4 x 32 pairs, four splits against nine: 47.1 against 49.6 us; batch
-// 1 keeps its 12 (16.6 us, the best of 1..24).  A sequence's keys fall into the same splits
+// 1 keeps its 12 (16.6 us, the best of 1..24); config 3 (8 x 12 pairs of head dim 64 over 1024
+// keys) eight splits of 128 against six of 192: 10.7 against 12.1 us with the merge.  A sequence's keys fall into the same splits
 // for a given max_len (the runner always passes its max_ctx); splits past a shorter
 // sequence's length are empty and carry zero weight in the merge.
 // bf16 caches take twice the keys per step (8 elements per lane), so their split count is
@@ -767,10 +768,13 @@ static int decode_nsplit(int B, int H, int D, int max_len, int *chunk, bool kv_b
         return 1;
     }
     const int keys_per_step = 4 * (WAVE / (D / (kv_bf16 ? 8 : 4))) * 4;  // NG * U
-    // splits of about 2*B*H keys (at least 192), but no more than two workgroups per CU need
-    int ch = std::max(2 * B * H, 192);
+    // splits of about 2*B*H keys (at least 192), but no more than two workgroups per CU need;
+    // head dims up to 64 (half the bytes per key) take splits of B*H keys (at least 128), up
+    // to four workgroups per CU
+    const bool narrow = D <= 64;
+    int ch = narrow ? std::max(B * H, 128) : std::max(2 * B * H, 192);
     ch = (ch + keys_per_step - 1) / keys_per_step * keys_per_step;
-    const long pairs = (long)B * H, slots = 2L * device_cu_count();
+    const long pairs = (long)B * H, slots = (narrow ? 4L : 2L) * device_cu_count();
     int ns = std::max(1, (max_len + ch - 1) / ch);
     ns = (int)std::min<long>(ns, std::max(1L, (slots + pairs - 1) / pairs));
     // then equal splits of max_len (e.g. 3 x 768 keys instead of 1024 + 1024 + 249)
