@@ -229,8 +229,8 @@ jas_status jas_attn_decode(const float *d_q, const float *d_K, const float *d_V,
  * partials go to a static device array of jas_attn_decode_scratch_max() bytes (8 MiB) per
  * GPU, held until the process ends; shapes whose partials
  * (jas_attn_decode_workspace(B, H, D, max_len)) exceed it are rejected with JAS_ERR_INVALID
- * (the split count stays within two workgroups per CU, so on a 256-CU MI355X every shape's
- * partials stay below about 0.5 MiB and none is rejected).
+ * (the split count stays within two to four workgroups per CU, so on a 256-CU MI355X every shape's
+ * partials stay below 1 MiB and none is rejected).
  * Every call on one GPU shares that array: calls that overlap on one GPU (two streams, or
  * two host threads) race.  Results are identical to jas_attn_decode's. */
 #define JAS_DECODE_SCRATCH_BYTES ((size_t)8 << 20)

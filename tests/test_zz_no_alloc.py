@@ -44,8 +44,8 @@ def test_noalloc_decode_matches_workspace_entry(jas):
 
 
 def test_noalloc_scratch_covers_every_shape(jas):
-    """The split count never asks for more than two workgroups per CU beyond the pairs
-    themselves, so the partials of any shape stay below about 0.5 MB on this part and fit the
+    """The split count never asks for more than two to four workgroups per CU beyond the pairs
+    themselves, so the partials of any shape stay below 1 MiB on this part and fit the
     static array (the entry point still checks the size and rejects a shape that would not)."""
     cap = jas.lib.jas_attn_decode_scratch_max()
     worst = 0
