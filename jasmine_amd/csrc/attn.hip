@@ -440,8 +440,6 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
         FA_STEP(kv0 + BK, 1, krb, vrb)
     }
 #undef FA_STEP
-    float l_run = l_part + __shfl_xor(l_part, 16, WAVE);
-    l_run += __shfl_xor(l_run, 32, WAVE);
 
     if constexpr (BF16) {
         // O^T accumulators: lane holds O[query = q0 + r16][d = 16c + 4g + r], its own query's
