@@ -14,6 +14,7 @@
 #include "jas_common.hpp"
 
 #include <cfloat>
+#include <atomic>
 #include <mutex>
 #include <unordered_map>
 
@@ -741,14 +742,16 @@ __global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p
 // CUs of the current device (256 on MI355X), looked up once per device
 static int device_cu_count()
 {
-    static int cached[64] = {0};
+    static std::atomic<int> cached[64];  // 0: not looked up yet
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cached[dev]) {
+    int v = cached[dev].load(std::memory_order_relaxed);
+    if (!v) {
         int n = 0;
-        cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+        v = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+        cached[dev].store(v, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return v;
 }
 
 constexpr int DECODE_WIDE_PAIRS = 128;
