@@ -537,6 +537,8 @@ def main():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--prompt", type=int, default=2048)
     ap.add_argument("--no-gpt2", action="store_true")
+    ap.add_argument("--gpt2-only", action="store_true",
+                    help="only the GPT-2-small (config 4) leg: 8 x 512 prefill, 4 + 32 decode steps")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-encdec", action="store_true", help="skip the C++ API encoder-decoder leg")
     ap.add_argument("--encdec-only", action="store_true",
@@ -569,6 +571,15 @@ def main():
         import jasmine_amd as jas
         jas.check(jas.lib.jas_init(0))
         print(json.dumps({"kernels": run_kernel_legs(jas)}), flush=True)
+        return
+    if args.gpt2_only:
+        import jasmine_amd as jas
+        jas.check(jas.lib.jas_init(0))
+        g_tok, g_ms, g_bytes = run_gpt2(jas, (12, 768, 12, 3072, 50257, 1024), 8, 512, 3, 32, 4,
+                                        graph=not args.no_graph)
+        print(json.dumps({"gpt2_small": {"decode_tok_s": round(g_tok, 1), "ms_per_step": round(g_ms, 3),
+                                         "step_hbm_frac": round(g_bytes / (g_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                         "graph": not args.no_graph, "prefill": run_gpt2.last_prefill}}), flush=True)
         return
     if args.encdec_only:
         import jasmine_amd as jas
