@@ -193,6 +193,19 @@ jas_status jas_gemm(int M, int N, int K,
                     int batch, long a_bstride, long b_bstride, long c_bstride, long bias_bstride,
                     jas_stream_t stream);
 
+/* C(m, n) = act(sum_k A(m, k) B(k, n) + bias) + R(m, n), R(m, n) = R[m*rs0 + n*rs1]: a
+ * residual block's last product with the skip connection in its epilogue -- jasmine's
+ * residual_net_t::forward (mat_net_t.hpp:326-329) computes f(x) + x with f ending in
+ * weight_net_t::forward (mat_net_t.hpp:38-49), optionally followed by relu_net_t /
+ * sigmoid_net_t (the encoder-decoder FFN), or in mat_mha_t's output projection; every step
+ * is formed in the same order and precision.  One problem (no batch); R must not overlap C. */
+jas_status jas_gemm_residual(int M, int N, int K,
+                             const float *d_A, long as0, long as1,
+                             const float *d_B, long bs0, long bs1,
+                             float *d_C, long cs0, long cs1,
+                             const float *d_bias, int bias_mode, int act,
+                             const float *d_R, long rs0, long rs1, jas_stream_t stream);
+
 /* Same contract in fp64 (mat_dot_t on mat_t<double>), on the fp64 matrix cores
  * (v_mfma_f64_16x16x4_f64); no activation or accumulate, bias_mode 0/1/2 as above. */
 jas_status jas_gemm_f64(int M, int N, int K,

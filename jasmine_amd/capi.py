@@ -62,6 +62,7 @@ _sigs = {
     "jas_layernorm": [VP, VP, I, I, L, L, L, C.c_float, VP, VP, VP],
     "jas_rmsnorm": [VP, VP, I, I, L, L, L, C.c_float, VP, VP],
     "jas_gemm": [I, I, I, VP, L, L, VP, L, L, VP, L, L, VP, I, I, I, I, L, L, L, L, VP],
+    "jas_gemm_residual": [I, I, I, VP, L, L, VP, L, L, VP, L, L, VP, I, I, VP, L, L, VP],
     "jas_gemm_f64": [I, I, I, VP, L, L, VP, L, L, VP, L, L, VP, I, VP],
     "jas_attn_prefill": [VP, VP, VP, VP, I, I, I, I, I, L, L, L, L, L, L, L, L, L, C.c_float, I, I, VP],
     "jas_attn_decode": [VP, VP, VP, VP, VP, I, I, I, I, L, L, C.c_float, VP, VP],

@@ -312,6 +312,9 @@ struct DmaArgs {
     int c_vec;  // 1: row-major C with float4 stores over n; 2: column-major C, float4 over m
     // fused prefill epilogues (packed weights, token-major output, c_vec == 2)
     DmaFused fz;
+    // residual source added after the bias (residual_net_t's f(x) + x): R(m, n) = resid[m*rs0 + n*rs1]
+    const float *resid = nullptr;
+    long rs0 = 0, rs1 = 0;
 };
 
 // M0 is a reserved register to the compiler; nothing else in these kernels uses it (no
@@ -540,6 +543,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_dma_kernel(const DmaArgs p)
     auto finish = [&](float x, int m, int n, float *cp) {
         if (bias) x = x + (p.bias_mode == 1 ? bias[m] : bias[n]);
         x = apply_act(x, p.act);
+        if (p.resid) x = x + p.resid[(long)m * p.rs0 + (long)n * p.rs1];
         return p.accumulate ? *cp + x : x;
     };
     const int mw = m0 + wm * WTM, nw = n0 + wn * WTN;
@@ -696,7 +700,7 @@ static int dma_mode(const float *X, long so, long sk, int O, long bst)
 static bool gemm_dma(int M, int N, int K, const void *A, long as0, long as1, const float *B, long bs0, long bs1,
                      float *C, long cs0, long cs1, const float *bias, int bias_mode, int act, int accumulate, int batch,
                      long abs_, long bbs, long cbs, long biasbs, hipStream_t s, bool a_packed, bool a_bf16,
-                     const DmaFused *fz = nullptr)
+                     const DmaFused *fz = nullptr, const float *resid = nullptr, long rs0 = 0, long rs1 = 0)
 {
     if (a_bf16 || K <= 0) return false;
     int am = a_packed ? DM_PK : dma_mode((const float *)A, as0, as1, M, abs_);
@@ -709,6 +713,8 @@ static bool gemm_dma(int M, int N, int K, const void *A, long as0, long as1, con
     p.abs_ = abs_; p.bbs = bbs; p.cbs = cbs; p.biasbs = biasbs;
     p.M = M; p.N = N; p.K = K;
     p.bias_mode = bias_mode; p.act = act; p.accumulate = accumulate;
+    p.resid = resid; p.rs0 = rs0; p.rs1 = rs1;
+    if (resid && (batch != 1 || fz)) return false;
     const bool ca = ((uintptr_t)C & 15) == 0 && cbs % 4 == 0;
     p.c_vec = 0;
     if (ca && cs1 == 1 && cs0 % 4 == 0 && N % 4 == 0) p.c_vec = 1;
@@ -1408,4 +1414,42 @@ extern "C" jas_status jas_gemm(int M, int N, int K, const float *A, long as0, lo
     }
     return gemm_general(M, N, K, A, as0, as1, B, bs0, bs1, C, cs0, cs1, bias, bias_mode, act, accumulate, batch, abs_,
                         bbs, cbs, biasbs, s, false);
+}
+
+// C(m, n) += R(m, n) after a product that did not take the residual in its epilogue
+__global__ void add_residual_kernel(float *C, long cs0, long cs1, const float *R, long rs0, long rs1, int M, int N)
+{
+    const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= (long)M * N) return;
+    const int m = (int)(g / N), n = (int)(g % N);
+    float *c = C + (long)m * cs0 + (long)n * cs1;
+    *c = *c + R[(long)m * rs0 + (long)n * rs1];
+}
+
+extern "C" jas_status jas_gemm_residual(int M, int N, int K, const float *A, long as0, long as1, const float *B,
+                                        long bs0, long bs1, float *C, long cs0, long cs1, const float *bias,
+                                        int bias_mode, int act, const float *R, long rs0, long rs1,
+                                        jas_stream_t stream)
+{
+    JAS_CHECK(M >= 0 && N >= 0 && K >= 0, JAS_ERR_INVALID, "jas_gemm_residual: negative size");
+    JAS_CHECK(A && B && C && R, JAS_ERR_INVALID, "jas_gemm_residual: null operand");
+    JAS_CHECK(bias_mode >= 0 && bias_mode <= 2 && (bias_mode == 0 || bias), JAS_ERR_INVALID,
+              "jas_gemm_residual: bad bias");
+    JAS_CHECK(act >= JAS_ACT_NONE && act <= JAS_ACT_SIGMOID, JAS_ERR_INVALID, "jas_gemm_residual: bad activation");
+    if (M == 0 || N == 0) return JAS_OK;
+    hipStream_t s = stream_or_default(stream);
+    if (gemm_dma(M, N, K, A, as0, as1, B, bs0, bs1, C, cs0, cs1, bias, bias_mode, act, 0, 1, 0, 0, 0, 0, s, false,
+                 false, nullptr, R, rs0, rs1)) {
+        JAS_LAUNCH_CHECK();
+        return JAS_OK;
+    }
+    // other operand layouts: the product, then the residual added in the same order
+    const jas_status st = jas_gemm(M, N, K, A, as0, as1, B, bs0, bs1, C, cs0, cs1, bias, bias_mode, act, 0, 1, 0, 0,
+                                   0, 0, stream);
+    if (st != JAS_OK) return st;
+    const long n = (long)M * N;
+    hipLaunchKernelGGL(add_residual_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, C, cs0, cs1, R, rs0,
+                       rs1, M, N);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
 }

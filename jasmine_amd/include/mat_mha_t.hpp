@@ -289,7 +289,8 @@ private:
                             JAS_ACT_NONE, 0, H, (long)dh * dh, (long)dh * x.s0, dh, dh, nullptr));
     }
 
-    mat_t<val_type> fused_forward(const input_type &input, const input_type *encoder_input)
+    mat_t<val_type> fused_forward(const input_type &input, const input_type *encoder_input,
+                                  const mat_t<val_type> *residual = nullptr)
     {
         const int d = m_d_model, H = m_num_heads, dh = m_d_head, Tq = input.col_num();
         packed_weights();
@@ -332,6 +333,13 @@ private:
         // y = W_o . concat(heads) + b_o, the concatenation read from the token-major rows
         auto &wo = m_output_proj;
         mat_t<val_type> y(d, Tq, typename mat_t<val_type>::device_uninit_tag{});
+        if (residual) {  // residual_net_t's + x in the projection's epilogue
+            const long r0 = residual->row_first() ? Tq : 1, r1 = residual->row_first() ? 1 : d;
+            jas::check(jas_gemm_residual(d, Tq, d, wo.weight().device_data(), d, 1, o, 1, d, y.device_data_mut(), Tq, 1,
+                                         wo.bias().device_data(), 1, JAS_ACT_NONE, residual->device_data(), r0, r1,
+                                         nullptr));
+            return y;
+        }
         jas::check(jas_gemm(d, Tq, d, wo.weight().device_data(), d, 1, o, 1, d, y.device_data_mut(), Tq, 1,
                             wo.bias().device_data(), 1, JAS_ACT_NONE, 0, 1, 0, 0, 0, 0, nullptr));
         return y;
@@ -367,6 +375,26 @@ public:
         head_outputs.reserve(m_num_heads);
         for (int i = 0; i < m_num_heads; ++i) head_outputs.push_back(m_heads[i].forward(splits[i]));
         return m_output_proj.forward(vconcat(head_outputs));
+    }
+
+    // forward(input) + residual with the residual added in the output projection's epilogue
+    // (residual_net_t, mat_net_t.hpp:326-329); false: not fused
+    bool forward_residual_into(const input_type &input, const mat_t<val_type> &residual, mat_t<val_type> &y)
+    {
+        if (!fusable(input.col_num()) || residual.is_scalar() || residual.row_num() != m_d_model ||
+            residual.col_num() != input.col_num())
+            return false;
+        y = fused_forward(input, nullptr, &residual);
+        return true;
+    }
+    bool forward_residual_into(const input_type &input, const input_type &encoder_input,
+                               const mat_t<val_type> &residual, mat_t<val_type> &y)
+    {
+        if (!fusable(input.col_num()) || encoder_input.col_num() < 1 || residual.is_scalar() ||
+            residual.row_num() != m_d_model || residual.col_num() != input.col_num())
+            return false;
+        y = fused_forward(input, &encoder_input, &residual);
+        return true;
     }
 
     mat_t<val_type> forward(const input_type &input, const input_type &encoder_input)
@@ -445,6 +473,13 @@ public:
     {
         if (m_encoder_output == nullptr) throw std::runtime_error("Encoder output not set for cross attention");
         return base_type::forward(input, *m_encoder_output);
+    }
+
+    // cross attention: the residual rides in the output projection over the encoder output
+    bool forward_residual_into(const input_type &input, const mat_t<val_type> &residual, mat_t<val_type> &y)
+    {
+        if (m_encoder_output == nullptr) throw std::runtime_error("Encoder output not set for cross attention");
+        return base_type::forward_residual_into(input, *m_encoder_output, residual, y);
     }
 
     mat_t<val_type> backward(const input_type &) { jas::detail::no_training("mat_mhca_t::backward"); }

@@ -38,6 +38,31 @@ mat_t<T> linear(const mat_t<T> &W, const X &x, const mat_t<T> &b)
     return y;
 }
 
+// act(W . X + b) + R with the skip connection added in the product's epilogue, for
+// residual_net_t over a linear layer (mat_net_t.hpp:326-329): each value is formed in the
+// order jasmine forms it (the biased product, then the activation, then + R).  Returns false
+// when the operands do not fit (the caller then takes jasmine's separate passes).
+template <typename T, typename X>
+bool linear_residual(const mat_t<T> &W, const X &x, const mat_t<T> &b, int act, const mat_t<T> &R, mat_t<T> &y)
+{
+    if constexpr (!std::is_same_v<T, float>) {
+        return false;
+    } else {
+        const int M = W.row_num(), N = x.col_num(), K = W.col_num();
+        if (K != x.row_num()) throw std::invalid_argument("mat_dot_t: inner dimensions do not match for dot product");
+        const bool ok = !W.is_scalar() && W.row_first() && !b.is_scalar() && b.row_num() == M && b.col_num() == 1 &&
+                        !(M == 1 && N == 1) && !R.is_scalar() && R.row_num() == M && R.col_num() == N;
+        if (!ok) return false;
+        auto xo = gemm_operand<T>(x);
+        mat_t<T> out(M, N, typename mat_t<T>::device_uninit_tag{});
+        const long r0 = R.row_first() ? N : 1, r1 = R.row_first() ? 1 : M;
+        check(jas_gemm_residual(M, N, K, W.device_data(), K, 1, xo.p, xo.s0, xo.s1, out.device_data_mut(), N, 1,
+                                b.device_data(), 1, act, R.device_data(), r0, r1, nullptr));
+        y = std::move(out);
+        return true;
+    }
+}
+
 // column LayerNorm with population std and eps = 0 (layer_norm_net_t::forward,
 // mat_net_t.hpp:209-225), gamma/beta per row
 template <typename T, typename X>
@@ -88,6 +113,17 @@ public:
     }
 
     mat_t<val_type> forward(const input_type &input) { return jas::linear(m_weight, input, m_bias); }
+
+    // act(forward(input)) + residual as one product (used by residual_net_t); false: not fused
+    bool forward_act_residual_into(const input_type &input, int act, const mat_t<val_type> &residual,
+                                   mat_t<val_type> &y)
+    {
+        return jas::linear_residual(m_weight, input, m_bias, act, residual, y);
+    }
+    bool forward_residual_into(const input_type &input, const mat_t<val_type> &residual, mat_t<val_type> &y)
+    {
+        return forward_act_residual_into(input, JAS_ACT_NONE, residual, y);
+    }
 
     template <typename init_type>
     void init_weight()
@@ -153,6 +189,8 @@ class relu_net_t
 public:
     using val_type = typename input_type::ele_type;
     relu_net_t() = default;
+    // the product epilogue's activation that computes exactly this forward
+    static constexpr int jas_fused_act = JAS_ACT_RELU;
     // (x > 0) * x, so negative inputs give -0 and -inf gives NaN as in mat_net_t.hpp:152
     mat_t<val_type> forward(const input_type &input) { return ((input > 0) * input).clone(); }
     template <typename other_type>
@@ -255,8 +293,16 @@ public:
     base_net_type &base_net() { return m_net; }
     base_net_type const &base_net() const { return m_net; }
 
-    // f(x) + x (mat_net_t.hpp:326-329)
-    mat_t<val_type> forward(const mat_t<val_type> &input) { return m_net.forward(input) + input; }
+    // f(x) + x (mat_net_t.hpp:326-329); where f ends in a product, the + x rides in that
+    // product's epilogue (same values, one launch fewer)
+    mat_t<val_type> forward(const mat_t<val_type> &input)
+    {
+        if constexpr (requires(mat_t<val_type> &y) { m_net.forward_residual_into(input, input, y); }) {
+            mat_t<val_type> y;
+            if (m_net.forward_residual_into(input, input, y)) return y;
+        }
+        return m_net.forward(input) + input;
+    }
 
     template <typename other_type>
     auto backward(const other_type &)
@@ -321,6 +367,28 @@ public:
     auto forward(const input_type &input)
     {
         return std::apply([&input](auto &&...nets) { return net_forward(input, nets...); }, m_nets);
+    }
+
+    // forward(input) + residual with the residual added in the last product's epilogue, when
+    // the chain is one linear layer, optionally followed by relu (the encoder-decoder FFN);
+    // false: not fused
+    template <typename input_type>
+    bool forward_residual_into(const input_type &input, const mat_t<val_type> &residual, mat_t<val_type> &y)
+    {
+        using first_t = std::tuple_element_t<0, std::tuple<net_types...>>;
+        if constexpr (!requires(first_t &f, mat_t<val_type> &o) { f.forward_act_residual_into(input, 0, residual, o); }) {
+            return false;
+        } else if constexpr (sizeof...(net_types) == 1) {
+            return std::get<0>(m_nets).forward_act_residual_into(input, JAS_ACT_NONE, residual, y);
+        } else if constexpr (sizeof...(net_types) == 2) {
+            using second_t = std::tuple_element_t<1, std::tuple<net_types...>>;
+            if constexpr (requires { second_t::jas_fused_act; })
+                return std::get<0>(m_nets).forward_act_residual_into(input, second_t::jas_fused_act, residual, y);
+            else
+                return false;
+        } else {
+            return false;
+        }
     }
 
     template <typename input_type>

@@ -400,6 +400,30 @@ def test_gemm_dma_geometries(jas, ta, tb, col_c, M, N, K):
     _gemm_case(jas, M, N, K, ta=bool(ta), tb=bool(tb), col_c=bool(col_c), bias_mode=1, acc=True)
 
 
+@pytest.mark.parametrize("M,N,K,act,rcol,bstride", [(512, 512, 512, 0, 0, 0), (300, 260, 200, 1, 0, 0),
+                                                    (257, 129, 129, 1, 1, 0), (96, 70, 64, 0, 0, 3)])
+def test_gemm_residual(jas, M, N, K, act, rcol, bstride):
+    """jas_gemm_residual: act(A B + bias) + R, against jas_gemm of the same operands followed by
+    the residual added in fp32 (bit for bit: the same product, then the same two roundings).
+    R row- or column-major; B with a padded row stride (3 extra floats) is not 16-byte
+    addressable per row, which takes the product-then-add path."""
+    rng = np.random.default_rng(61)
+    A = rng.standard_normal((M, K), dtype=np.float32)
+    ldb = N + bstride
+    B = rng.standard_normal((K, ldb), dtype=np.float32)
+    bias = rng.standard_normal(M, dtype=np.float32)
+    R = rng.standard_normal((M, N), dtype=np.float32)
+    Rs = np.asfortranarray(R) if rcol else R
+    dA, dB, db = jas.to_device(A), jas.to_device(B), jas.to_device(bias)
+    dR = jas.to_device(np.ascontiguousarray(Rs.T) if rcol else R)
+    r0, r1 = (1, M) if rcol else (N, 1)
+    want, got = jas.DeviceArray((M, N)), jas.DeviceArray((M, N))
+    jas.check(jas.lib.jas_gemm(M, N, K, dA.p, K, 1, dB.p, ldb, 1, want.p, N, 1, db.p, 1, act, 0, 1, 0, 0, 0, 0, None))
+    jas.check(jas.lib.jas_gemm_residual(M, N, K, dA.p, K, 1, dB.p, ldb, 1, got.p, N, 1, db.p, 1, act, dR.p, r0, r1,
+                                        None))
+    assert np.array_equal(got.numpy(), want.numpy() + R)
+
+
 def test_gemm_dma_k_tail_padded_rows(jas):
     """K not a multiple of 4 with 16-byte aligned, padded rows (K-contiguous operands take the
     direct-to-LDS path): the tail slab reads element by element and zero-fills past K."""
