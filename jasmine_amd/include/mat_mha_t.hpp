@@ -223,7 +223,8 @@ private:
     jas::detail::mha_scratch m_fx;
 
     // All heads at once for float matrices with d_h in {32, 64, 128}: the per-head Q/K/V
-    // projections are three batched GEMMs (one problem per head) writing token-major rows,
+    // projections are one batched GEMM (one problem per head, its three blocks stacked;
+    // cross attention: Q alone, and K / V of the encoder output) writing token-major rows,
     // attention is the flash kernel over every head (no score matrix in memory), and the
     // output projection reads the token-major result transposed.  Cross attention keeps
     // the encoder-side keys / values while the encoder output and the weights are unchanged.
@@ -265,8 +266,8 @@ private:
             for (int h = 0; h < H; ++h) {
                 const std::array<weight_net_t<input_type, updator_type> *, 3> ns{
                     &m_heads[h].q_net(), &m_heads[h].k_net(), &m_heads[h].v_net()};
-                for (int sct = 0; sct < 3; ++sct) {
-                    const size_t i = (size_t)sct * H + h;
+                for (int sct = 0; sct < 3; ++sct) {  // per head: q, k, v stacked (3 dh rows)
+                    const size_t i = (size_t)h * 3 + sct;
                     jas::check(jas_memcpy_d2d(w + i * dh * dh, ns[sct]->weight().device_data(),
                                               sizeof(float) * dh * dh, nullptr));
                     jas::check(jas_memcpy_d2d(b + i * dh, ns[sct]->bias().device_data(), sizeof(float) * dh, nullptr));
@@ -284,9 +285,20 @@ private:
     {
         const int H = m_num_heads, dh = m_d_head;
         const float *w = (const float *)m_fx.w.get();
-        const float *b = w + (size_t)3 * H * dh * dh + (size_t)sct * H * dh;
-        jas::check(jas_gemm(dh, T, dh, w + (size_t)sct * H * dh * dh, dh, 1, x.p, x.s0, x.s1, out, 1, ld, b, 1,
-                            JAS_ACT_NONE, 0, H, (long)dh * dh, (long)dh * x.s0, dh, dh, nullptr));
+        const float *b = w + (size_t)3 * H * dh * dh + (size_t)sct * dh;
+        jas::check(jas_gemm(dh, T, dh, w + (size_t)sct * dh * dh, dh, 1, x.p, x.s0, x.s1, out, 1, ld, b, 1,
+                            JAS_ACT_NONE, 0, H, 3L * dh * dh, (long)dh * x.s0, dh, 3L * dh, nullptr));
+    }
+
+    // q, k and v of every head in one batched product (one problem per head, its three
+    // d_h x d_h blocks stacked): out(n, h, s, m) at out[n*3d + h*3dh + s*dh + m]
+    void project_qkv(const jas::gemm_operand_t<float> &x, int T, float *out)
+    {
+        const int H = m_num_heads, dh = m_d_head;
+        const float *w = (const float *)m_fx.w.get();
+        const float *b = w + (size_t)3 * H * dh * dh;
+        jas::check(jas_gemm(3 * dh, T, dh, w, dh, 1, x.p, x.s0, x.s1, out, 1, 3L * m_d_model, b, 1, JAS_ACT_NONE, 0,
+                            H, 3L * dh * dh, (long)dh * x.s0, 3L * dh, 3L * dh, nullptr));
     }
 
     mat_t<val_type> fused_forward(const input_type &input, const input_type *encoder_input,
@@ -296,14 +308,14 @@ private:
         packed_weights();
         auto xq = jas::gemm_operand<float>(input);
         const float *Q, *K, *V;
-        long qs, ks;
+        long qs, ks, qh = dh, kh = dh;  // token and head strides
         int Tk;
         if (!encoder_input) {
             Tk = Tq;
             m_fx.qkv.allocate(sizeof(float) * (size_t)Tq * 3 * d);
             float *qkv = (float *)m_fx.qkv.get();
-            for (int sct = 0; sct < 3; ++sct) project(sct, xq, Tq, qkv + (size_t)sct * d, 3L * d);
-            Q = qkv, K = qkv + d, V = qkv + 2 * d, qs = ks = 3L * d;
+            project_qkv(xq, Tq, qkv);
+            Q = qkv, K = qkv + dh, V = qkv + 2 * dh, qs = ks = 3L * d, qh = kh = 3L * dh;
         } else {
             Tk = encoder_input->col_num();
             m_fx.qkv.allocate(sizeof(float) * (size_t)Tq * d);
@@ -327,7 +339,7 @@ private:
         m_fx.o.allocate(sizeof(float) * (size_t)Tq * d);
         float *o = (float *)m_fx.o.get();
         const bool causal = !encoder_input && m_mask;
-        jas::check(jas_attn_prefill(Q, K, V, o, 1, H, Tq, Tk, dh, (long)Tq * qs, dh, qs, (long)Tk * ks, dh, ks,
+        jas::check(jas_attn_prefill(Q, K, V, o, 1, H, Tq, Tk, dh, (long)Tq * qs, qh, qs, (long)Tk * ks, kh, ks,
                                     (long)Tq * d, dh, d, (float)(1.0 / std::sqrt((double)dh)), causal ? 1 : 0,
                                     JAS_F32, nullptr));
         // y = W_o . concat(heads) + b_o, the concatenation read from the token-major rows
