@@ -657,11 +657,13 @@ __global__ void __launch_bounds__(NW * 64) gemm_dma_kernel(const DmaArgs p)
 
 // Geometry: 256 x 256 tiles (8 waves, 3 stages) when they give every CU a workgroup, else
 // 128 x 128 (4 waves, 4 stages) when those give every CU at least four, else 64 x 64 (4
-// waves, 4 stages of 32-wide slabs).  64 x 64 tiles win wherever the 128-wide ones would
+// waves, 4 stages of 32-wide slabs) when those give every CU one, else 32 x 32 (one 16 x 16
+// block per wave: four times the workgroups; jasmine's Transformer-base encoder-decoder, 512
+// x 512 products, encode 0.49 -> 0.34 ms; neutral at 1024^3).  64 x 64 tiles win wherever the 128-wide ones would
 // leave a partly filled last round (GPT-2-small prefill QKV 2304 x 4096 x 768: 90 against
 // 75 TFLOP/s; FC 3072 x 4096 x 768: 92 against 84).  MI355X fp32: 4096^3 at 130-137
 // TFLOP/s, 2048^3 at 113, 1024^3 at 82-89.
-// JAS_GEMM_GEOMETRY=256|128|64 forces one geometry (a tuning knob; default: the rule above).
+// JAS_GEMM_GEOMETRY=256|128|64|32 forces one geometry (a tuning knob; default: the rule above).
 static int forced_geometry()
 {
     static const int g = [] {
@@ -682,6 +684,13 @@ static void launch_dma(const DmaArgs &p, int batch, hipStream_t s)
     } else if (fg == 128 || (fg == 0 && tiles(128) >= 1024)) {
         const dim3 grid(ceil_div(p.N, 128), ceil_div(p.M, 128), batch);
         hipLaunchKernelGGL((gemm_dma_kernel<AM, BM, 128, 128, 4, 2, 4, 1>), grid, dim3(256), 0, s, p);
+    } else if (AM != DM_PK && p.fz.mode == FZ_NONE && (fg == 32 || (fg == 0 && tiles(64) < 256))) {
+        // plain operands only: packed weights and the fused prefill epilogues (SwiGLU pairs
+        // two 16-row blocks in one wave) assume wave tiles of at least 32 rows
+        if constexpr (AM != DM_PK) {
+            const dim3 grid(ceil_div(p.N, 32), ceil_div(p.M, 32), batch);
+            hipLaunchKernelGGL((gemm_dma_kernel<AM, BM, 32, 32, 4, 2, 4, 2>), grid, dim3(256), 0, s, p);
+        }
     } else {
         const dim3 grid(ceil_div(p.N, 64), ceil_div(p.M, 64), batch);
         hipLaunchKernelGGL((gemm_dma_kernel<AM, BM, 64, 64, 4, 2, 4, 2>), grid, dim3(256), 0, s, p);
