@@ -909,13 +909,15 @@ jas_status jas_attn_prefill(const void *Q, const void *K, const void *V, void *O
     // grid: one workgroup per (query block, batch x head), padded to a multiple of the 8 XCDs.
     // When 8-wave workgroups (128 queries) would not give every CU one, 4-wave workgroups
     // (64 queries) double the count -- where a thread's K/V staging stays at four 16-byte
-    // loads per tile (not fp32 with D = 128).  A non-causal launch that still leaves CUs
-    // idle also splits its keys over up to 4 work items (at least two 64-key tiles each),
-    // merged by a second kernel.
+    // loads per tile (not fp32 with D = 128).  A launch that still leaves CUs idle also
+    // splits its keys over up to 4 work items (at least two 64-key tiles each), merged by a
+    // second kernel; with a causal mask the splits past a query block's diagonal find every
+    // key masked and leave a zero-weight partial (decoder self-attention of jasmine's
+    // Transformer-base, 8 heads x 512 tokens: forward 0.63 -> 0.57 ms).
     const bool few = (long)ceil_div(Sq, 16 * FA_WAVES) * B * H < 256;
     const int nw = few && (dtype == JAS_BF16 || D <= 64) ? 4 : FA_WAVES;
     const long items = (long)ceil_div(Sq, 16 * nw) * B * H;
-    if (!causal && items < 256 && Sk >= 4 * 64) {
+    if (items < 256 && Sk >= 4 * 64) {
         int ns = (int)std::min<long>(4, (512 + items - 1) / items);
         ns = std::min(ns, Sk / 128);
         if (ns > 1) {
