@@ -1,7 +1,7 @@
 // Rotary position embedding of jasmine's API (mat_RoPE_t.hpp:7-230 of the reference).
-// mat_RoPE_t keeps the host-side cos/sin cache and forward_unite() views for code that
-// inspects rotation blocks; RoPE_net_t::forward runs the rotation as one device kernel with
-// the same angle formula (jas_rope_jasmine).
+// mat_RoPE_t evaluates rotation blocks on the host for code that inspects them
+// (forward_unite); RoPE_net_t::forward runs the rotation as one device kernel with the same
+// angle formula (jas_rope_jasmine).
 #ifndef __MAT_ROPE_HPP__
 #define __MAT_ROPE_HPP__
 #include <cmath>
@@ -10,61 +10,19 @@
 #include "mat_express_t.hpp"
 #include "mat_view_t.hpp"
 
-// growable cache matrix (mat_RoPE_t.hpp:7-73)
-template <typename val_type>
-class mat_cache_t
-{
-    mat_t<val_type> m_cache;
-    int m_cache_rows = 0, m_cache_cols = 0;
-    static constexpr int EXPAND_SIZE = 1024;
+#include <array>
+#include <map>
 
-    void expand_cache(int rows, int cols)
-    {
-        if (rows > m_cache.row_num() || cols > m_cache.col_num()) {
-            const int nr = rows > m_cache.row_num() ? std::max(rows, m_cache.row_num() + EXPAND_SIZE) : m_cache.row_num();
-            const int nc = cols > m_cache.col_num() ? std::max(cols, m_cache.col_num() + EXPAND_SIZE) : m_cache.col_num();
-            mat_t<val_type> grown(nr, nc);
-            for (int i = 0; i < m_cache.row_num(); ++i)
-                for (int j = 0; j < m_cache.col_num(); ++j) grown(i, j) = m_cache(i, j);
-            m_cache = std::move(grown);
-        }
-    }
-
-public:
-    mat_cache_t() : m_cache(EXPAND_SIZE, EXPAND_SIZE) {}
-
-    val_type &operator()(int row, int col)
-    {
-        if (row >= m_cache_rows || col >= m_cache_cols) {
-            expand_cache(row + 1, col + 1);
-            m_cache_rows = std::max(m_cache_rows, row + 1);
-            m_cache_cols = std::max(m_cache_cols, col + 1);
-        }
-        return m_cache(row, col);
-    }
-
-    const val_type &operator()(int row, int col) const
-    {
-        if (row >= m_cache_rows || col >= m_cache_cols) throw std::out_of_range("Cache access out of range");
-        return m_cache(row, col);
-    }
-
-    mat_view_t<mat_t<val_type>> range(int row, int col, int rows, int cols)
-    {
-        if (row + rows > m_cache_rows || col + cols > m_cache_cols) {
-            expand_cache(row + rows, col + cols);
-            m_cache_rows = std::max(m_cache_rows, row + rows);
-            m_cache_cols = std::max(m_cache_cols, col + cols);
-        }
-        return m_cache.view(row, col, rows, cols);
-    }
-};
-
+// Host-side rotation blocks of jasmine's RoPE (mat_RoPE_t.hpp:76-150 of the reference).
+// Only inspection code uses them: RoPE_net_t::forward computes every angle on the device.
+// Each distinct block request (row_beg, rows, col_beg, cols) is evaluated once from the
+// closed form into a matrix of exactly that size and kept for the object's lifetime, so the
+// views returned stay valid; a changed d drops every block.
 template <typename val_type>
 class mat_RoPE_t
 {
-    mat_cache_t<val_type> m_cache;
-    int m_enable_rows = 0, m_enable_cols = 0;
+    using key_t = std::array<int, 4>;
+    std::map<key_t, mat_t<val_type>> m_blocks;  // node-based: stored matrices never move
     int m_d;
 
 public:
@@ -73,32 +31,36 @@ public:
     void set_d(int const &d)
     {
         m_d = d;
-        m_enable_rows = m_enable_cols = 0;
+        m_blocks.clear();
     }
 
     val_type get_d() const { return m_d; }
 
-    // cache entry (i, j): angle = j / 10000^((i/2) / d) in val_type; cos where i and j have
-    // the same parity, -sin at (even, odd), sin at (odd, even) (mat_RoPE_t.hpp:99-134)
-    void init(int const &row_beg, int const &rows, int const &col_beg, int const &cols)
+    // Entry (r, c) of jasmine's rotation table (mat_RoPE_t.hpp:113-131): with
+    // a = c / 10000^((r/2) / d) evaluated in val_type, cos(a) where r and c have the same
+    // parity, -sin(a) at (even r, odd c) and sin(a) at (odd r, even c).
+    val_type entry(int r, int c) const
     {
-        for (int i = 0; i < row_beg + rows; ++i)
-            for (int j = 0; j < col_beg + cols; ++j) {
-                if (i < m_enable_rows && j < m_enable_cols) continue;
-                val_type angle = j / std::pow(10000.0, (i / 2) / static_cast<val_type>(m_d));
-                if ((i % 2) == (j % 2)) m_cache(i, j) = std::cos(angle);
-                else if (i % 2 == 0) m_cache(i, j) = -std::sin(angle);
-                else m_cache(i, j) = std::sin(angle);
-            }
-        m_enable_rows = row_beg + rows;
-        m_enable_cols = col_beg + cols;
+        const val_type a = c / std::pow(10000.0, (r / 2) / static_cast<val_type>(m_d));
+        if ((r & 1) == (c & 1)) return std::cos(a);
+        return (r & 1) ? std::sin(a) : -std::sin(a);
     }
 
+    // view of rows [row_beg, row_beg + row_num) x columns [col_beg, col_beg + col_num)
     mat_view_t<mat_t<val_type>> range(int row_beg, int row_num, int col_beg, int col_num)
     {
-        if (row_beg + row_num >= m_enable_rows || col_beg + col_num >= m_enable_cols)
-            init(row_beg, row_num, col_beg, col_num);
-        return m_cache.range(row_beg, col_beg, row_num, col_num);
+        if (row_beg < 0 || col_beg < 0 || row_num <= 0 || col_num <= 0)
+            throw std::out_of_range("mat_RoPE_t::range: empty or negative block");
+        auto found = m_blocks.find(key_t{row_beg, row_num, col_beg, col_num});
+        if (found == m_blocks.end()) {
+            // mat_t(1, 1) would be a scalar: blocks are built at 2x2 or larger, then viewed
+            const int R = std::max(row_num, 2), C = std::max(col_num, 2);
+            mat_t<val_type> blk(R, C);
+            for (int r = 0; r < R; ++r)
+                for (int c = 0; c < C; ++c) blk(r, c) = entry(row_beg + r, col_beg + c);
+            found = m_blocks.emplace(key_t{row_beg, row_num, col_beg, col_num}, std::move(blk)).first;
+        }
+        return found->second.view(0, 0, row_num, col_num);
     }
 
     // the 2x2 rotation block of pair i at position m

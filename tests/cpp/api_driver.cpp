@@ -258,6 +258,23 @@ int api_rope(const float *X, int d, int T, float *Y)
     });
 }
 
+// mat_RoPE_t::forward_unite(i, m) (the 2x2 block test_RoPE prints, mat_RoPE_t.hpp:232-243),
+// then range() over rows x cols from (row_beg, col_beg), each written row-major
+int api_rope_blocks(int d, int i, int m, float *blk4, int row_beg, int rows, int col_beg, int cols, float *blk)
+{
+    return guarded([&] {
+        mat_RoPE_t<float> rope(d);
+        for (int rep = 0; rep < 2; ++rep) {  // the second request is served from the stored block
+            auto u = rope.forward_unite(i, m);
+            for (int r = 0; r < 2; ++r)
+                for (int c = 0; c < 2; ++c) blk4[r * 2 + c] = u(r, c);
+        }
+        auto v = rope.range(row_beg, rows, col_beg, cols);
+        for (int r = 0; r < rows; ++r)
+            for (int c = 0; c < cols; ++c) blk[r * cols + c] = v(r, c);
+    });
+}
+
 int api_transformer(const float *en, int Te, const float *de, int Td, int d, int H, int n_enc, int n_dec,
                     const float *W, float *Y)
 {

@@ -10,6 +10,7 @@ Tolerance (fp32): |api - ref| <= 1e-3 + 1e-4 |ref|; elementwise +-*/ trees and p
 per-column reductions are also checked bit-exact, as their arithmetic order is jasmine's.
 """
 import ctypes
+import math
 import os
 
 import numpy as np
@@ -401,3 +402,29 @@ def test_api_bf16_gemm_linear_softmax_reductions(api, g):
     assert bitexact(hs, rb(rs)) and bitexact(vs, rb(cs)) and bitexact(hm, xb.max(1))
     close(hs, g["hsum"].reshape(hs.shape), atol=BF_ATOL, rtol=BF_RTOL)
     assert sc[1] == xb.max()
+
+
+def rope_entry(r, c, d):
+    """jasmine's rotation table entry (mat_RoPE_t.hpp:113-131), float32 angle as val_type."""
+    a = np.float32(c) / np.float32(np.power(10000.0, np.float32(r // 2) / np.float32(d)))
+    a = float(np.float32(a))
+    if r % 2 == c % 2:
+        return math.cos(a)
+    return math.sin(a) if r % 2 else -math.sin(a)
+
+
+def test_api_rope_blocks(api):
+    """mat_RoPE_t host blocks: forward_unite(1, 1) at d 4 is the closed form
+    [cos .2, -sin .3; sin .2, cos .3] (angle c / 10000^((r/2)/d), 10000^(-1/4) = 0.1), and
+    ragged range() requests (odd start, 3 x 5, 1 x 1) match the entry formula element by
+    element.
+    Host-only: no device work runs."""
+    d = 4
+    blk4 = np.zeros(4, np.float32)
+    for (r0, R, c0, C) in ((1, 3, 3, 5), (2, 1, 7, 1), (0, 4, 0, 9)):
+        blk = np.zeros(R * C, np.float32)
+        ok(api, api.api_rope_blocks(d, 1, 1, fp(blk4), r0, R, c0, C, fp(blk)))
+        a2, a3 = 2 / 10000 ** 0.25, 3 / 10000 ** 0.25
+        assert np.allclose(blk4, [math.cos(a2), -math.sin(a3), math.sin(a2), math.cos(a3)], atol=1e-6)
+        want = [[rope_entry(r0 + i, c0 + j, d) for j in range(C)] for i in range(R)]
+        assert np.allclose(blk.reshape(R, C), want, atol=1e-6)
