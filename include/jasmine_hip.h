@@ -47,6 +47,13 @@ jas_status jas_init(int device);
 const char *jas_last_error(void);
 const char *jas_version(void);
 jas_stream_t jas_default_stream(void);
+/* Frees the library's scratch buffer for `stream` (NULL: the library stream), which
+ * multi-pass kernels (whole-matrix reductions, global softmax, prefill key splits) grow
+ * per stream and otherwise keep until the process ends.  Waits for the stream's queued work
+ * first.  Call it before destroying a short-lived stream that ran such kernels (never after:
+ * a destroyed handle is not a stream); the next such kernel on that stream allocates again.
+ * No reference counterpart (jasmine has no streams). */
+jas_status jas_stream_release_scratch(jas_stream_t stream);
 jas_status jas_malloc(void **d_ptr, size_t bytes);          /* mat_t.hpp:67 new[] */
 jas_status jas_free(void *d_ptr);                            /* mat_t.hpp:39 delete[] */
 /* Stream-ordered block cache behind the C++ headers' mat_t storage (jasmine allocates and
@@ -324,12 +331,21 @@ int jas_lm_position(jas_lm *lm);
  * above 1 = split over the cache plus the log-sum-exp merge; 0 = bad argument).  A query
  * for tests and tuning: no reference counterpart (jasmine has no KV cache). */
 int jas_lm_attn_splits(jas_lm *lm, int B);
+/* The decode GEMM geometry the runner's step launches for one projection ("w_qkv", "w_o",
+ * "w_fc", "w_proj", "w_gate_up", "w_down", "w_head" / "wte"): geo[0] 16-row weight tiles per
+ * workgroup (gate/up pairs count two), geo[1] waves per workgroup, geo[2] K chunks in
+ * flight per wave, geo[3] K splits (1 = unsplit).  A query for tests and tuning, so a test
+ * can show which kernel variant it covered; no reference counterpart. */
+jas_status jas_lm_proj_geometry(jas_lm *lm, const char *name, int *geo);
 /* One of the runner's stored projections applied to B <= 16 token vectors with the decode
  * step's own weight-streaming GEMM (same kernel variant and geometry): d_y[B][M] = W . x for
  * d_x[B][K] (token-major, device).  Names: "w_qkv", "w_o", "w_fc", "w_proj", "w_down",
  * "w_head" / "wte" (layer ignored) and "w_gate_up" (d_y[B][d_ff] = silu(W_gate x) * (W_up x)).
  * No bias, no activation otherwise.  Runs on `stream` (NULL: the library stream) after
- * draining the runner's stream, whose decode buffers it reuses (not concurrent with a decode).  No reference counterpart: weight_net_t::forward (mat_net_t.hpp:38-49) on the
+ * draining the runner's stream, whose decode buffers it reuses; before returning it makes the
+ * runner's stream wait (on the device) for the projection's last launch, so runner calls may
+ * follow without a host synchronisation.  Not thread-safe against a concurrent runner call
+ * from another host thread.  No reference counterpart: weight_net_t::forward (mat_net_t.hpp:38-49) on the
  * runner's packed weights, for callers that reuse a layer and for per-kernel measurement. */
 jas_status jas_lm_project(jas_lm *lm, const char *name, int layer, int B, const float *d_x, float *d_y,
                           jas_stream_t stream);

@@ -87,6 +87,8 @@ _sigs = {
     "jas_lm_save": [VP, C.c_char_p], "jas_lm_load": [VP, C.c_char_p],
     "jas_lm_read_config": [C.c_char_p, C.POINTER(LmConfig)],
     "jas_lm_project": [VP, C.c_char_p, I, I, VP, VP, VP],
+    "jas_lm_proj_geometry": [VP, C.c_char_p, IP],
+    "jas_stream_release_scratch": [VP],
 }
 for _n, _a in _sigs.items():
     getattr(lib, _n).argtypes = _a
@@ -256,6 +258,12 @@ class Lm:
     def project(self, name, layer, x_dev, y_dev, B, stream=None):
         """y[B][M] = W . x with the decode GEMM on the stored weights (device arrays)."""
         check(lib.jas_lm_project(self.h, name.encode(), int(layer), int(B), x_dev.p, y_dev.p, stream))
+
+    def proj_geometry(self, name):
+        """(tiles per workgroup, waves, chunks in flight, K splits) of one decode projection."""
+        geo = (C.c_int * 4)()
+        check(lib.jas_lm_proj_geometry(self.h, name.encode(), geo))
+        return tuple(geo)
 
     def attn_splits(self, B):
         """Key splits the decode attention takes at batch B (1: one pass, no merge)."""

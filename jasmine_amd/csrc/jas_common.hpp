@@ -15,6 +15,8 @@ void set_error(const std::string &msg);
 jas_status fail(jas_status code, const std::string &msg);
 hipStream_t stream_or_default(jas_stream_t s);
 void *workspace(size_t bytes, hipStream_t s);
+// frees the stream's scratch after its queued work (or the device) has drained
+jas_status release_workspace(hipStream_t s);
 // x[n] += sum_s part[(s*16 + n)*d ...] + bias; y = norm(x) (RMSNorm, or LayerNorm with b)
 jas_status resid_norm(float *x, const float *part, int ks, const float *bias, const float *g, const float *b, float *y,
                       int N, int d, float eps, bool rms, hipStream_t s, bool y_packed = false);

@@ -549,6 +549,7 @@ jas_status jas_lm_destroy(jas_lm *lm)
     for (void *p : ptrs)
         if (p) (void)hipFree(p);
     for (auto e : lm->ev) (void)hipEventDestroy(e);
+    if (lm->proj_done) (void)hipEventDestroy(lm->proj_done);
     if (lm->stream) (void)hipStreamDestroy(lm->stream);
     delete lm;
     return JAS_OK;
@@ -858,6 +859,35 @@ jas_status jas_lm_project(jas_lm *lm, const char *name, int layer, int B, const 
     if (ks)
         hipLaunchKernelGGL(sum_splits_kernel, dim3(ceil_div((long)B * M, 256)), dim3(256), 0, s, lm->part, ks, B, M, d_y);
     JAS_LAUNCH_CHECK();
+    // the projection used the runner's decode buffers (h / ff / part) on `s`: later runner
+    // work waits for it on the device, so a decode queued right after cannot overwrite them
+    if (!lm->proj_done) JAS_HIP(hipEventCreateWithFlags(&lm->proj_done, hipEventDisableTiming));
+    JAS_HIP(hipEventRecord(lm->proj_done, s));
+    JAS_HIP(hipStreamWaitEvent(lm->stream, lm->proj_done, 0));
+    return JAS_OK;
+}
+
+jas_status jas_lm_proj_geometry(jas_lm *lm, const char *name, int *geo)
+{
+    JAS_CHECK(lm && name && geo, JAS_ERR_INVALID, "jas_lm_proj_geometry: null argument");
+    const jas_lm_config &c = lm->cfg;
+    const std::string n(name);
+    const int d = c.d_model, F = c.d_ff, V = c.vocab;
+    int M, K, ks = 1;
+    bool dual = false, split = false;
+    if (n == "w_qkv") M = 3 * d, K = d;
+    else if (n == "w_o") M = d, K = d, split = true, ks = lm->ks_o;
+    else if (n == "w_fc" && c.kind == 0) M = F, K = d;
+    else if ((n == "w_proj" && c.kind == 0) || (n == "w_down" && c.kind == 1)) M = d, K = F, split = true, ks = lm->ks_d;
+    else if (n == "w_gate_up" && c.kind == 1) M = F, K = d, dual = true;
+    else if ((n == "w_head" && c.kind == 1) || (n == "wte" && c.kind == 0)) M = V, K = d;
+    else return fail(JAS_ERR_INVALID, "jas_lm_proj_geometry: no such decode projection for this model kind");
+    // the same rule skinny_gemm applies when the runner passes no explicit tuning
+    const SkinnyTuning t = skinny_default_tuning(M, K, dual, split, lm->wbf16());
+    geo[0] = dual && (t.nt < 2 || t.nt % 2) ? 2 : t.nt;
+    geo[1] = t.wpb;
+    geo[2] = t.depth;
+    geo[3] = ks;
     return JAS_OK;
 }
 

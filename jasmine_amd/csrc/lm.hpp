@@ -73,6 +73,8 @@ struct jas_lm {
     std::vector<hipEvent_t> ev;
     std::vector<int> ev_cls;
     size_t ev_used = 0;
+    // jas_lm_project's last launch on the caller's stream: the runner's stream waits on it
+    hipEvent_t proj_done = nullptr;
 
     const float *W(const char *n) const
     {

@@ -28,7 +28,7 @@ jas_status fail(jas_status code, const std::string &msg)
 // between them is safe; a buffer grows only after its own stream has drained (the old
 // buffer may still be read by queued kernels).  Issuing calls on one stream from two host
 // threads at once is not supported (neither is it by the reference, which has no threads).
-// A buffer lives until the process ends (streams destroyed by the caller leave theirs).
+// A buffer lives until jas_stream_release_scratch(stream) or the process ends.
 struct Scratch {
     void *p = nullptr;
     size_t bytes = 0;
@@ -52,6 +52,17 @@ void *workspace(size_t bytes, hipStream_t s)
     }
     w.bytes = nb;
     return w.p;
+}
+
+jas_status release_workspace(hipStream_t s)
+{
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    auto it = g_ws.find(s);
+    if (it == g_ws.end()) return JAS_OK;
+    JAS_HIP(hipStreamSynchronize(s));  // queued kernels may still read the buffer
+    if (it->second.p) JAS_HIP(hipFree(it->second.p));
+    g_ws.erase(it);
+    return JAS_OK;
 }
 
 hipStream_t stream_or_default(jas_stream_t s)
@@ -87,6 +98,11 @@ jas_status jas_init(int device)
 }
 
 jas_stream_t jas_default_stream(void) { return (jas_stream_t)stream_or_default(nullptr); }
+
+jas_status jas_stream_release_scratch(jas_stream_t stream)
+{
+    return release_workspace(stream_or_default(stream));
+}
 
 jas_status jas_malloc(void **p, size_t bytes)
 {

@@ -30,7 +30,7 @@ def oracle_for(jas, lm, cfg):
     return ocfg, ow, w
 
 
-def run_parity(jas, cfg, seed, B, P, steps, prompt_seed):
+def run_parity(jas, cfg, seed, B, P, steps, prompt_seed, decode_atol=ATOL):
     lm = jas.Lm(cfg)
     lm.init_random(seed, 0.02)
     ocfg, ow, keep = oracle_for(jas, lm, cfg)
@@ -48,10 +48,11 @@ def run_parity(jas, cfg, seed, B, P, steps, prompt_seed):
         gpu_ids.append(nxt)
     gpu_logits = np.stack(gpu_logits)
     gpu_ids = np.stack(gpu_ids, 1)
-    close(gpu_logits, cpu_logits)
+    close(gpu_logits[:1], cpu_logits[:1])
+    close(gpu_logits[1:], cpu_logits[1:], atol=decode_atol)
     srt = np.sort(cpu_logits, -1)
     margin = (srt[..., -1] - srt[..., -2]).T  # [B, steps]
-    decisive = margin > ATOL + RTOL * np.abs(srt[..., -1]).T
+    decisive = margin > decode_atol + RTOL * np.abs(srt[..., -1]).T
     assert np.all(gpu_ids[decisive] == cpu_ids[decisive])
     return lm, prompt, cpu_ids, int((~decisive).sum())
 
@@ -169,6 +170,93 @@ def test_llama7b_full_depth(jas):
     # one 16-token prompt (seed 4), 3 greedy steps -- 26 GB of weights read back for the oracle
     cfg = jas.LmConfig(1, 32, 4096, 32, 11008, 32000, 32, 1, 1e-6, 10000.0)
     run_parity(jas, cfg, seed=4, B=1, P=16, steps=3, prompt_seed=4)
+
+
+# decode GEMM geometry (tiles per workgroup, waves, chunks in flight, K splits) per projection
+# at the benchmark widths; the bf16-weight lines of bench.py run exactly these variants
+BENCH_GEOMETRY = {
+    ("llama7b", 1): {"w_qkv": (3, 4, 4, 1), "w_o": (2, 8, 2, 2), "w_gate_up": (6, 4, 2, 1),
+                     "w_down": (4, 4, 4, 4), "w_head": (4, 4, 2, 1)},
+    ("llama7b", 0): {"w_qkv": (3, 4, 2, 1), "w_o": (2, 4, 3, 2), "w_gate_up": (6, 4, 2, 1),
+                     "w_down": (2, 4, 2, 2), "w_head": (4, 4, 3, 1)},
+    ("gpt2", 1): {"w_qkv": (1, 8, 3, 1), "w_o": (2, 8, 2, 6), "w_fc": (1, 8, 3, 1),
+                  "w_proj": (2, 8, 2, 8), "wte": (4, 4, 3, 1)},
+}
+
+
+def check_geometry(lm, key):
+    got = {n: lm.proj_geometry(n) for n in BENCH_GEOMETRY[key]}
+    assert got == BENCH_GEOMETRY[key], got
+
+
+@pytest.mark.parametrize("kb", [1, 0])
+def test_llama7b_width_bf16_weights_b16(jas, kb):
+    """bf16 weights (and a bf16 or fp32 KV cache) at config 5's width and batch: d 4096, 32
+    heads of 128, SwiGLU 11008, vocab 32000, 16 sequences, 2 of the 32 layers.  The decode
+    GEMM variants are the ones the bf16 benchmark line runs (asserted through the runner's
+    geometry query); the oracle runs the rounded weights read back from the device and
+    rounds the cache as the runner does, so the fp32 tolerance holds for the prefill logits
+    and, with an fp32 cache, for every step.  With a bf16 cache a decode step's keys and
+    values are rounded from fp32 values that differ between the two sides in their last
+    bits; an element near a bf16 rounding boundary then lands one bf16 step (2^-8 relative)
+    apart, and at d 4096 enough of them do to move logits by ~2e-3 (measured max 1.98e-3):
+    those steps are held to 5e-3."""
+    cfg = jas.LmConfig(1, 2, 4096, 32, 11008, 32000, 64, 16, 1e-6, 10000.0, 1, kb)
+    lm = jas.Lm(cfg)
+    check_geometry(lm, ("llama7b", 1))
+    lm.close()
+    run_parity(jas, cfg, seed=4, B=16, P=10, steps=3, prompt_seed=4, decode_atol=5e-3 if kb else ATOL)
+
+
+def test_llama7b_width_fp32_geometry(jas):
+    """The fp32 runner's decode GEMM variants at config 5's width (the headline line)."""
+    lm = jas.Lm(jas.LmConfig(1, 2, 4096, 32, 11008, 32000, 64, 16, 1e-6, 10000.0))
+    check_geometry(lm, ("llama7b", 0))
+    lm.close()
+
+
+def test_gpt2_width_bf16_weights(jas):
+    """bf16 weights and cache at config 4's width (d 768, 12 heads, FFN 3072, vocab 50257 as the
+    tied bf16 LM head), batch 8, 2 of the 12 layers."""
+    cfg = jas.LmConfig(0, 2, 768, 12, 3072, 50257, 64, 8, 1e-5, 10000.0, 1, 1)
+    lm = jas.Lm(cfg)
+    check_geometry(lm, ("gpt2", 1))
+    lm.close()
+    run_parity(jas, cfg, seed=3, B=8, P=10, steps=3, prompt_seed=3)
+
+
+@pytest.mark.parametrize("wb", [1, 0])
+def test_lm_project_llama7b_width(jas, wb):
+    """Every decode projection at config 5's width, 16 tokens, bf16 and fp32 weights: the
+    runner's own GEMM variant (jas_lm_project) against fp64 products of the weights read back
+    from the device (the rounded bf16 values for wb = 1)."""
+    cfg = jas.LmConfig(1, 2, 4096, 32, 11008, 32000, 16, 16, 1e-6, 10000.0, wb, 0)
+    lm = jas.Lm(cfg)
+    lm.init_random(5, 0.02)
+    rng = np.random.default_rng(5)
+    layer = 1
+    for name in ["w_qkv", "w_o", "w_gate_up", "w_down", "w_head"]:
+        def wmat(nm):
+            w = lm.weight(nm).reshape(lm.weight_shape(nm))
+            return (w[layer] if w.shape[0] > 1 else w[0]).astype(np.float64)
+        if name == "w_gate_up":
+            Wg, Wu = wmat("w_gate"), wmat("w_up")
+            M, K = Wg.shape
+        else:
+            W = wmat(name)
+            M, K = W.shape
+        x = rng.standard_normal((16, K)).astype(np.float32)
+        dx, dy = jas.to_device(x), jas.DeviceArray((16, M))
+        lm.project(name, layer, dx, dy, 16)
+        got = dy.numpy()
+        xd = x.astype(np.float64)
+        if name == "w_gate_up":
+            g, u = xd @ Wg.T, xd @ Wu.T
+            want = g / (1 + np.exp(-g)) * u
+        else:
+            want = xd @ W.T
+        close(got, want, atol=1e-4 * np.sqrt(K), rtol=1e-4)
+    lm.close()
 
 
 @pytest.mark.parametrize("kind", [0, 1])
@@ -377,6 +465,38 @@ def test_lm_project_matches_weights(jas, kind, wb):
     from jasmine_amd import JasError
     with pytest.raises(JasError):
         lm.project("w_nope", 0, dx, dy, 3)
+
+
+def test_lm_project_then_decode_without_sync(jas):
+    """jas_lm_project queues its kernels on the caller's stream (here the library stream) and
+    reuses the runner's decode buffers; a decode issued right after it, with no host
+    synchronisation in between, must still see its own activations: the runner's stream
+    waits for the projection on the device.  The decode's logits must equal those of an
+    identical model that ran no projection, and the projection its fp64 product."""
+    cfg = jas.LmConfig(1, 2, 1024, 8, 2816, 500, 40, 4, 1e-6, 10000.0)
+    prompt = randint((4, 9), 500, 23)
+    rng = np.random.default_rng(23)
+
+    def fresh():
+        lm = jas.Lm(cfg)
+        lm.init_random(23, 0.02)
+        first, _ = lm.prefill(prompt)
+        return lm, first
+
+    a, first = fresh()
+    b, _ = fresh()
+    x = rng.standard_normal((16, 2816)).astype(np.float32)
+    dx, dy = jas.to_device(x), jas.DeviceArray((16, 1024))
+    dx2, dy2 = jas.to_device(np.ascontiguousarray(x[:, :1024])), jas.DeviceArray((16, 2816))
+    for _ in range(3):
+        a.project("w_down", 1, dx, dy, 16)  # K-split partials in the runner's split buffer
+        a.project("w_gate_up", 0, dx2, dy2, 16)  # the runner's packed activation buffer
+        na, la = a.decode(first, want_logits=True)
+        nb, lb = b.decode(first, want_logits=True)
+        assert np.array_equal(la, lb) and np.array_equal(na, nb)
+        first = na
+    W = a.weight("w_down").reshape(a.weight_shape("w_down"))[1]
+    close(dy.numpy(), x.astype(np.float64) @ W.astype(np.float64).T, atol=1e-4 * np.sqrt(2816), rtol=1e-4)
 
 
 @pytest.mark.parametrize("shape", ["config4_gpt2_small_b8_p512", "config5_llama7b_b16_p2048"])

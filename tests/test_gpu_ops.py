@@ -326,6 +326,17 @@ def test_scratch_per_stream(jas):
     for ya, yb in outs:
         close(ya.numpy(), wa, atol=0, rtol=1e-5)
         close(yb.numpy(), wb, atol=0, rtol=1e-5)
+    # releasing a stream's scratch waits for its queued work; the next multi-pass call on it
+    # allocates again, and a stream that never held scratch releases nothing
+    for ya, _ in outs:
+        jas.check(jas.lib.jas_softmax_global(dxa.p, ya.p, xa.size, sa))
+    jas.check(jas.lib.jas_stream_release_scratch(sa))
+    jas.check(jas.lib.jas_softmax_global(dxa.p, outs[0][0].p, xa.size, sa))
+    jas.check(jas.lib.jas_stream_release_scratch(sa))
+    jas.check(jas.lib.jas_stream_release_scratch(sa))
+    for ya, _ in outs:
+        close(ya.numpy(), wa, atol=0, rtol=1e-5)
+    jas.check(jas.lib.jas_stream_release_scratch(sb))
     hip.hipStreamDestroy(sa)
     hip.hipStreamDestroy(sb)
 
@@ -400,28 +411,36 @@ def test_gemm_dma_geometries(jas, ta, tb, col_c, M, N, K):
     _gemm_case(jas, M, N, K, ta=bool(ta), tb=bool(tb), col_c=bool(col_c), bias_mode=1, acc=True)
 
 
-@pytest.mark.parametrize("M,N,K,act,rcol,bstride", [(512, 512, 512, 0, 0, 0), (300, 260, 200, 1, 0, 0),
-                                                    (257, 129, 129, 1, 1, 0), (96, 70, 64, 0, 0, 3)])
-def test_gemm_residual(jas, M, N, K, act, rcol, bstride):
+@pytest.mark.parametrize("M,N,K,act,rcol,bstride,ccol", [
+    (512, 512, 512, 0, 0, 0, 0), (300, 260, 200, 1, 0, 0, 0), (257, 129, 129, 1, 1, 0, 0), (96, 70, 64, 0, 0, 3, 0),
+    # 64 x 64 tiles (256 of them): float4 row-major store, and the column-major C store
+    (1024, 1024, 256, 1, 0, 0, 0), (1024, 1024, 256, 0, 1, 0, 1),
+    # 256 x 256 tiles (256 of them; the 128-wide geometry needs >= 1024 of its tiles with
+    # fewer than 256 of 256, which no single product meets): both C layouts
+    (4096, 4096, 128, 0, 0, 0, 0), (4096, 4096, 128, 1, 1, 0, 1), (300, 516, 96, 1, 0, 0, 1)])
+def test_gemm_residual(jas, M, N, K, act, rcol, bstride, ccol):
     """jas_gemm_residual: act(A B + bias) + R, against jas_gemm of the same operands followed by
     the residual added in fp32 (bit for bit: the same product, then the same two roundings).
-    R row- or column-major; B with a padded row stride (3 extra floats) is not 16-byte
-    addressable per row, which takes the product-then-add path."""
+    R row- or column-major, C row- or column-major; B with a padded row stride (3 extra
+    floats) is not 16-byte addressable per row, which takes the product-then-add path."""
     rng = np.random.default_rng(61)
     A = rng.standard_normal((M, K), dtype=np.float32)
     ldb = N + bstride
     B = rng.standard_normal((K, ldb), dtype=np.float32)
     bias = rng.standard_normal(M, dtype=np.float32)
     R = rng.standard_normal((M, N), dtype=np.float32)
-    Rs = np.asfortranarray(R) if rcol else R
     dA, dB, db = jas.to_device(A), jas.to_device(B), jas.to_device(bias)
-    dR = jas.to_device(np.ascontiguousarray(Rs.T) if rcol else R)
+    dR = jas.to_device(np.ascontiguousarray(R.T) if rcol else R)
     r0, r1 = (1, M) if rcol else (N, 1)
+    c0, c1 = (1, M) if ccol else (N, 1)
     want, got = jas.DeviceArray((M, N)), jas.DeviceArray((M, N))
-    jas.check(jas.lib.jas_gemm(M, N, K, dA.p, K, 1, dB.p, ldb, 1, want.p, N, 1, db.p, 1, act, 0, 1, 0, 0, 0, 0, None))
-    jas.check(jas.lib.jas_gemm_residual(M, N, K, dA.p, K, 1, dB.p, ldb, 1, got.p, N, 1, db.p, 1, act, dR.p, r0, r1,
+    jas.check(jas.lib.jas_gemm(M, N, K, dA.p, K, 1, dB.p, ldb, 1, want.p, c0, c1, db.p, 1, act, 0, 1, 0, 0, 0, 0, None))
+    jas.check(jas.lib.jas_gemm_residual(M, N, K, dA.p, K, 1, dB.p, ldb, 1, got.p, c0, c1, db.p, 1, act, dR.p, r0, r1,
                                         None))
-    assert np.array_equal(got.numpy(), want.numpy() + R)
+    w, g_ = want.numpy(), got.numpy()
+    if ccol:  # the buffers hold C column-major
+        w, g_ = w.reshape(N, M).T, g_.reshape(N, M).T
+    assert np.array_equal(g_, w + R)
 
 
 def test_gemm_dma_k_tail_padded_rows(jas):
