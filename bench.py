@@ -270,7 +270,7 @@ def run_kernel_legs(jas, reps=10):
     ws = jas.DeviceArray(max(lib.jas_attn_decode_workspace(Bb, H, Dh, S) // 4, 1))
     ms = time_launches(lambda: chk(lib.jas_attn_decode(q.p, K.p, V.p, o.p, lens.p, Bb, H, Dh, S, st[0], st[1],
                                                        C.c_float(0.125), ws.p, None)), reps * 5)
-    out["attn_decode_f32"] = line("attn_decode_kernel<64> + merge, 1 query over 1024 cached keys, B8 H12",
+    out["attn_decode_f32"] = line("attn_decode_kernel<64> (key splits merged by each pair's last split), 1 query over 1024 cached keys, B8 H12",
                                   ms, 2 * ne * 4)
     del Q, K, V, O
 
@@ -290,7 +290,7 @@ def run_kernel_legs(jas, reps=10):
 
 # ---------------------------------------------------------------- rocprofv3 summaries
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "llama7b_decode_b16_traffic.json")
-KCLASS = {"attention": ("attn_decode_kernel<128,", "attn_decode_merge_kernel<128>")}
+KCLASS = {"attention": ("attn_decode_kernel<128,",)}
 
 
 def _pmc_per_kernel(csv_path, counter):

@@ -234,10 +234,13 @@ jas_status jas_attn_prefill(const void *d_Q, const void *d_K, const void *d_V, v
                             long o_sb, long o_sh, long o_ss,
                             float scale, int causal, int dtype, jas_stream_t stream);
 /* One-query-per-(b,h) decode step over a KV cache (flash-decoding: split over the keys,
- * log-sum-exp merge).  q[B,H,D], cache K/V[(b,h)] rows of D at k_sb/k_sh strides,
- * seqlens[B] = number of valid keys per sequence (device int32).  Equivalent to the last
- * column of a full recompute (transformer_test.hpp:231-238 recomputes the prefix).
- * d_work must hold jas_attn_decode_workspace(B, H, D, max_len) bytes. */
+ * log-sum-exp merge by the last split of each (b,h) to finish, in the same launch).
+ * q[B,H,D], cache K/V[(b,h)] rows of D at k_sb/k_sh strides, seqlens[B] = number of valid
+ * keys per sequence (device int32).  Equivalent to the last column of a full recompute
+ * (transformer_test.hpp:231-238 recomputes the prefix).  d_work must hold
+ * jas_attn_decode_workspace(B, H, D, max_len) bytes of split partials (no initialisation;
+ * calls that share it must not overlap).  The splits' arrival counters are the library's,
+ * one zeroed array per stream (jas_stream_release_scratch frees it). */
 size_t jas_attn_decode_workspace(int B, int H, int D, int max_len);
 jas_status jas_attn_decode(const float *d_q, const float *d_K, const float *d_V, float *d_O,
                            const int32_t *d_seqlens, int B, int H, int D, int max_len,
@@ -247,8 +250,9 @@ jas_status jas_attn_decode(const float *d_q, const float *d_K, const float *d_V,
  * the reference (jasmine allocates per matrix).  It is for callers that cannot allocate --
  * code under HIP graph capture, serving loops, harnesses that forbid hipMalloc.  The split
  * partials go to a static device array of jas_attn_decode_scratch_max() bytes (8 MiB) per
- * GPU, held until the process ends; shapes whose partials
- * (jas_attn_decode_workspace(B, H, D, max_len)) exceed it are rejected with JAS_ERR_INVALID
+ * GPU, with a second static array of 65536 split-arrival counters, held until the process
+ * ends; shapes whose partials (jas_attn_decode_workspace(B, H, D, max_len)) exceed the
+ * scratch, or that split over more than 65536 (b, h) pairs, are rejected with JAS_ERR_INVALID
  * (the split count stays within two to four workgroups per CU, so on a 256-CU MI355X every shape's
  * partials stay below 1 MiB and none is rejected).
  * Every call on one GPU shares that array: calls that overlap on one GPU (two streams, or
@@ -327,8 +331,8 @@ jas_status jas_lm_generate(jas_lm *lm, int steps, int32_t *h_ids);
 jas_status jas_lm_use_graph(jas_lm *lm, int enable);
 /* Current sequence length (tokens in the KV cache). */
 int jas_lm_position(jas_lm *lm);
-/* Key splits of the runner's decode attention at batch B (1 = one pass, no merge launch;
- * above 1 = split over the cache plus the log-sum-exp merge; 0 = bad argument).  A query
+/* Key splits of the runner's decode attention at batch B (1 = one pass, no merge;
+ * above 1 = split over the cache plus the log-sum-exp merge by the last split to finish; 0 = bad argument).  A query
  * for tests and tuning: no reference counterpart (jasmine has no KV cache). */
 int jas_lm_attn_splits(jas_lm *lm, int B);
 /* The decode GEMM geometry the runner's step launches for one projection ("w_qkv", "w_o",

@@ -40,7 +40,8 @@ def sources():
 
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [hipcc()] + HIPCC_FLAGS + ["-x", "hip", "-c", src, "-o", obj]
+    extra = os.environ.get("JAS_EXTRA_CXXFLAGS", "").split()  # e.g. -D tuning switches
+    cmd = [hipcc()] + HIPCC_FLAGS + extra + ["-x", "hip", "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l)

@@ -545,18 +545,84 @@ struct DecodeArgs {
     const void *K, *V;  // fp32 or (KB) bf16 elements
     float *O;
     const int32_t *seqlens;
-    float *part;  // [B*H][nsplit][D + 2]
+    float *part;    // [B*H][nsplit][D + 2]
+    unsigned *ctr;  // [B*H] split-arrival counters, zero between calls
     long k_sb, k_sh;
     int B, H, nsplit, chunk;
     float scale_log2;
     int o_packed_d;  // > 0: write O in the packed B-operand layout over o_packed_d features
 };
 
+// Cross-workgroup hand-off of split partials.  The L2 caches of the XCDs are not coherent
+// with each other, and a device-scope release or acquire fence writes back or invalidates a
+// whole L2 -- per workgroup, far more than the partials.  So the partials are written and
+// read with device-scope relaxed atomic stores and loads (coherent across XCDs on their own),
+// a wave waits for its stores to complete before the workgroup barrier, and the arrival
+// counter is a relaxed atomic add: no fence anywhere.
+__device__ __forceinline__ void part_store(float *a, float v)
+{
+    __hip_atomic_store(a, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float part_load(const float *a)
+{
+    return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Arrival counter of one (sequence, head) pair: the splits that have published their
+// partials.  Counter arrays are zero when allocated and the last arrival puts its counter
+// back to zero, for the next call and for graph replays.  Returns true for the last arrival.
+__device__ __forceinline__ bool decode_arrive(unsigned *ctr, int nsplit)
+{
+    const unsigned old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old + 1 != (unsigned)nsplit) return false;
+    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
 __device__ __forceinline__ long decode_out_index(const DecodeArgs &p, int bh, int D, int e)
 {
     if (p.o_packed_d <= 0) return (long)bh * D + e;
     const int b = bh / p.H, k = (bh % p.H) * D + e;  // token b, feature k
     return ((long)(k >> 4) * 64 + b + 16 * ((k & 15) >> 2)) * 4 + (k & 3);
+}
+
+// Merges the nsplit partials (max, sum, weighted values) of pair bh into its output element
+// tid.  Eight splits' triples are requested at a time; with at most eight splits the whole
+// merge is one memory round trip.  The sums keep split order.
+template <int D>
+__device__ __forceinline__ void decode_merge_splits(const DecodeArgs &p, int bh, int tid)
+{
+    const float *pp = p.part + (long)bh * p.nsplit * (D + 2);
+    constexpr int G = 8;
+    const int ns = p.nsplit;
+    float mv[G], lv[G], av[G];
+    auto load = [&](int s0) {
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+            const bool in = s0 + u < ns;
+            const float *q = pp + (s0 + u) * (D + 2);
+            mv[u] = in ? part_load(q) : -FLT_MAX;
+            lv[u] = in ? part_load(q + 1) : 0.f;
+            av[u] = in ? part_load(q + 2 + tid) : 0.f;
+        }
+    };
+    load(0);
+    float M = -FLT_MAX;
+#pragma unroll
+    for (int u = 0; u < G; ++u) M = fmaxf(M, mv[u]);
+    for (int s0 = G; s0 < ns; ++s0) M = fmaxf(M, part_load(pp + s0 * (D + 2)));
+    float L = 0.f, A = 0.f;
+    for (int s0 = 0; s0 < ns; s0 += G) {
+        if (s0 > 0) load(s0);
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+            if (s0 + u >= ns) break;
+            const float f = mv[u] == -FLT_MAX ? 0.f : exp2f(mv[u] - M);
+            L += lv[u] * f;
+            A += av[u] * f;
+        }
+    }
+    p.O[decode_out_index(p, bh, D, tid)] = L > 0.f ? A / L : 0.f;
 }
 
 // TPK lanes per key (D/4 floats each); each group of TPK lanes walks its own keys.
@@ -675,49 +741,20 @@ __global__ void __launch_bounds__(WPB * 64) attn_decode_kernel(const DecodeArgs 
             p.O[decode_out_index(p, bh, D, tid)] = L > 0.f ? A / L : 0.f;
         } else {
             float *pp = p.part + ((long)bh * p.nsplit + split) * (D + 2);
-            pp[2 + tid] = A;
-            if (tid == 0) { pp[0] = M; pp[1] = L; }
+            part_store(pp + 2 + tid, A);
+            if (tid == 0) { part_store(pp, M); part_store(pp + 1, L); }
         }
     }
-}
-
-template <int D>
-__global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p)
-{
-    const int bh = blockIdx.x, tid = threadIdx.x;
-    const float *pp = p.part + (long)bh * p.nsplit * (D + 2);
-    // eight splits' (max, sum, value) are requested at a time; with at most eight splits the
-    // whole merge is one memory round trip.  The sums keep split order.
-    constexpr int G = 8;
-    const int ns = p.nsplit;
-    float mv[G], lv[G], av[G];
-    auto load = [&](int s0) {
-#pragma unroll
-        for (int u = 0; u < G; ++u) {
-            const bool in = s0 + u < ns;
-            const float *q = pp + (s0 + u) * (D + 2);
-            mv[u] = in ? q[0] : -FLT_MAX;
-            lv[u] = in ? q[1] : 0.f;
-            av[u] = in ? q[2 + tid] : 0.f;
-        }
-    };
-    load(0);
-    float M = -FLT_MAX;
-#pragma unroll
-    for (int u = 0; u < G; ++u) M = fmaxf(M, mv[u]);
-    for (int s0 = G; s0 < ns; ++s0) M = fmaxf(M, pp[s0 * (D + 2)]);
-    float L = 0.f, A = 0.f;
-    for (int s0 = 0; s0 < ns; s0 += G) {
-        if (s0 > 0) load(s0);
-#pragma unroll
-        for (int u = 0; u < G; ++u) {
-            if (s0 + u >= ns) break;
-            const float f = mv[u] == -FLT_MAX ? 0.f : exp2f(mv[u] - M);
-            L += lv[u] * f;
-            A += av[u] * f;
-        }
-    }
-    p.O[decode_out_index(p, bh, D, tid)] = L > 0.f ? A / L : 0.f;
+    if (p.nsplit == 1) return;
+    // the last split of this (sequence, head) to finish merges all of them: every wave's
+    // partial stores complete before the barrier, then one arrival is counted
+    __shared__ int s_last;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) s_last = decode_arrive(p.ctr + bh, p.nsplit);
+    __syncthreads();
+    if (!s_last) return;
+    if (tid < D) decode_merge_splits<D>(p, bh, tid);
 }
 
 // Split count: splits of about 2*B*H keys (at least 192) -- many when few (sequence, head)
@@ -728,7 +765,10 @@ __global__ void __launch_bounds__(D) attn_decode_merge_kernel(const DecodeArgs p
 // MI355X: one split against three at 16 x 32 pairs over 2300 keys, 176.7 against 181.7 us
 // plus the 4.5 us merge; 4 x 32 pairs, four splits against nine: 47.1 against 49.6 us; batch
 // 1 keeps its 12 (16.6 us, the best of 1..24); config 3 (8 x 12 pairs of head dim 64 over 1024
-// keys) eight splits of 128 against six of 192: 10.7 against 12.1 us with the merge.  A sequence's keys fall into the same splits
+// keys) eight splits of 128 against six of 192: 10.7 against 12.1 us with the merge.  With
+// the merge done by each pair's last split (no second launch) config 3 stays at 10.4-10.8 us
+// for splits of 64 to 256 keys: the hand-off's store, counter and load round trips cost what
+// the merge launch did.  A sequence's keys fall into the same splits
 // for a given max_len (the runner always passes its max_ctx); splits past a shorter
 // sequence's length are empty and carry zero weight in the merge.
 // bf16 caches take twice the keys per step (8 elements per lane), so their split count is
@@ -801,8 +841,8 @@ int attn_decode_splits(int B, int H, int D, int max_len, bool kv_bf16, bool wide
 }
 
 jas_status attn_decode_impl(const float *q, const void *K, const void *V, float *O, const int32_t *seqlens, int B,
-                            int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, hipStream_t s,
-                            int o_packed_d, bool kv_bf16, bool wide)
+                            int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, unsigned *ctr,
+                            hipStream_t s, int o_packed_d, bool kv_bf16, bool wide)
 {
     JAS_CHECK(q && K && V && O && seqlens, JAS_ERR_INVALID, "jas_attn_decode: null tensor");
     JAS_CHECK(B > 0 && H > 0 && max_len > 0, JAS_ERR_INVALID, "jas_attn_decode: empty shape");
@@ -811,9 +851,9 @@ jas_status attn_decode_impl(const float *q, const void *K, const void *V, float 
     int chunk;
     const bool use_wide = wide && decode_wide_ok(B, H, D, max_len, kv_bf16);
     int ns = decode_nsplit(B, H, D, max_len, &chunk, kv_bf16, use_wide);
-    JAS_CHECK(ns == 1 || work, JAS_ERR_INVALID, "jas_attn_decode: workspace required");
+    JAS_CHECK(ns == 1 || (work && ctr), JAS_ERR_INVALID, "jas_attn_decode: workspace and counters required");
     JAS_CHECK(o_packed_d <= 0 || (B <= 16 && o_packed_d == H * D), JAS_ERR_INVALID, "attn_decode: bad packed output");
-    DecodeArgs p{q, K, V, O, seqlens, (float *)work, k_sb, k_sh, B, H, ns, chunk, scale * 1.4426950408889634f,
+    DecodeArgs p{q, K, V, O, seqlens, (float *)work, ctr, k_sb, k_sh, B, H, ns, chunk, scale * 1.4426950408889634f,
                  o_packed_d};
     dim3 grid(ns, B * H);
 #define JAS_DEC(DD)                                                                                  \
@@ -821,7 +861,6 @@ jas_status attn_decode_impl(const float *q, const void *K, const void *V, float 
         if (use_wide) launch_decode_wide<DD>(grid, s, p);                                              \
         else if (kv_bf16) hipLaunchKernelGGL((attn_decode_kernel<DD, true, 4>), grid, dim3(256), 0, s, p); \
         else hipLaunchKernelGGL((attn_decode_kernel<DD, false, 4>), grid, dim3(256), 0, s, p);       \
-        if (ns > 1) hipLaunchKernelGGL((attn_decode_merge_kernel<DD>), dim3(B * H), dim3(DD), 0, s, p); \
     }
     JAS_DEC(32) JAS_DEC(64) JAS_DEC(128)
 #undef JAS_DEC
@@ -836,23 +875,29 @@ jas_status attn_decode_impl(const float *q, const void *K, const void *V, float 
 // only a stand-in for the symbol); its device address is looked up once per device with that
 // device current and kept here.
 static __device__ __align__(256) float scratch[JAS_DECODE_SCRATCH_BYTES / sizeof(float)];
+// its split-arrival counters: zero at load, and every call leaves them zero
+constexpr int NOALLOC_MAX_PAIRS = 65536;
+static __device__ __align__(256) unsigned scratch_arrivals[NOALLOC_MAX_PAIRS];
 constexpr int MAX_DEVICES = 64;
-static void *scratch_dev_ptr[MAX_DEVICES];
+static void *scratch_dev_ptr[MAX_DEVICES], *arrivals_dev_ptr[MAX_DEVICES];
 static std::mutex scratch_mu;
 
-static jas_status decode_scratch_ptr(void **out)
+static jas_status decode_scratch_ptr(void **out, unsigned **ctr)
 {
     int dev = 0;
     JAS_HIP(hipGetDevice(&dev));
     JAS_CHECK(dev >= 0 && dev < MAX_DEVICES, JAS_ERR_INVALID, "jas_attn_decode_noalloc: device index out of range");
     std::lock_guard<std::mutex> g(scratch_mu);
     if (!scratch_dev_ptr[dev]) {
-        void *ptr = nullptr;
+        void *ptr = nullptr, *cptr = nullptr;
         JAS_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
-        JAS_CHECK(ptr, JAS_ERR_HIP, "jas_attn_decode_noalloc: no device address for the scratch array");
+        JAS_HIP(hipGetSymbolAddress(&cptr, HIP_SYMBOL(scratch_arrivals)));
+        JAS_CHECK(ptr && cptr, JAS_ERR_HIP, "jas_attn_decode_noalloc: no device address for the scratch arrays");
         scratch_dev_ptr[dev] = ptr;
+        arrivals_dev_ptr[dev] = cptr;
     }
     *out = scratch_dev_ptr[dev];
+    *ctr = (unsigned *)arrivals_dev_ptr[dev];
     return JAS_OK;
 }
 
@@ -965,7 +1010,13 @@ jas_status jas_attn_decode(const float *q, const float *K, const float *V, float
                            int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work,
                            jas_stream_t stream)
 {
-    return attn_decode_impl(q, K, V, O, seqlens, B, H, D, max_len, k_sb, k_sh, scale, work, stream_or_default(stream), 0);
+    hipStream_t s = stream_or_default(stream);
+    unsigned *ctr = nullptr;
+    if (jas_attn_decode_workspace(B, H, D, max_len)) {
+        ctr = arrival_counters((size_t)B * H, s);
+        JAS_CHECK(ctr, JAS_ERR_OOM, "jas_attn_decode: no memory for the split-arrival counters");
+    }
+    return attn_decode_impl(q, K, V, O, seqlens, B, H, D, max_len, k_sb, k_sh, scale, work, ctr, s, 0);
 }
 
 size_t jas_attn_decode_scratch_max(void) { return JAS_DECODE_SCRATCH_BYTES; }
@@ -979,11 +1030,15 @@ jas_status jas_attn_decode_noalloc(const float *q, const float *K, const float *
               "jas_attn_decode_noalloc: split partials exceed the static scratch (B*H*splits*(D+2)*4 > "
               "jas_attn_decode_scratch_max()); use jas_attn_decode with a workspace");
     void *work = nullptr;
+    unsigned *ctr = nullptr;
     if (need) {
-        const jas_status st = decode_scratch_ptr(&work);
+        JAS_CHECK((long)B * H <= NOALLOC_MAX_PAIRS, JAS_ERR_INVALID,
+                  "jas_attn_decode_noalloc: more than 65536 (sequence, head) pairs with a key split");
+        const jas_status st = decode_scratch_ptr(&work, &ctr);
         if (st != JAS_OK) return st;
     }
-    return attn_decode_impl(q, K, V, O, seqlens, B, H, D, max_len, k_sb, k_sh, scale, work, stream_or_default(stream), 0);
+    return attn_decode_impl(q, K, V, O, seqlens, B, H, D, max_len, k_sb, k_sh, scale, work, ctr,
+                            stream_or_default(stream), 0);
 }
 
 } // extern "C"

@@ -15,7 +15,10 @@ void set_error(const std::string &msg);
 jas_status fail(jas_status code, const std::string &msg);
 hipStream_t stream_or_default(jas_stream_t s);
 void *workspace(size_t bytes, hipStream_t s);
-// frees the stream's scratch after its queued work (or the device) has drained
+// n zeroed split-arrival counters for kernels on stream s (one array per stream, left zero
+// by every kernel that uses it); nullptr when out of memory
+unsigned *arrival_counters(size_t n, hipStream_t s);
+// frees the stream's scratch and counters after its queued work has drained
 jas_status release_workspace(hipStream_t s);
 // x[n] += sum_s part[(s*16 + n)*d ...] + bias; y = norm(x) (RMSNorm, or LayerNorm with b)
 jas_status resid_norm(float *x, const float *part, int ks, const float *bias, const float *g, const float *b, float *y,
@@ -24,9 +27,9 @@ jas_status resid_norm(float *x, const float *part, int ks, const float *bias, co
 // next packed GEMM; 0 = the jas_attn_decode layout O[b][h][D]
 // kv_bf16: K/V hold bf16 elements (same element strides)
 jas_status attn_decode_impl(const float *q, const void *K, const void *V, float *O, const int32_t *seqlens, int B,
-                            int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, hipStream_t s,
-                            int o_packed_d, bool kv_bf16 = false, bool wide = false);
-// key splits attn_decode_impl launches for this shape (1: no merge launch; 0: bad shape)
+                            int H, int D, int max_len, long k_sb, long k_sh, float scale, void *work, unsigned *ctr,
+                            hipStream_t s, int o_packed_d, bool kv_bf16 = false, bool wide = false);
+// key splits attn_decode_impl launches for this shape (1: one pass, no merge; 0: bad shape)
 int attn_decode_splits(int B, int H, int D, int max_len, bool kv_bf16, bool wide);
 
 

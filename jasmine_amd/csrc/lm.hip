@@ -349,7 +349,7 @@ jas_status decode_step(jas_lm *lm, bool device_pos)
         TRY(proj(lm, lm->LW("w_qkv", l), lm->h, B, 3 * d, d, eq));
         TRY(prof_begin(lm, 1));
         TRY(attn_decode_impl(lm->q, lm->kv_layer_ptr(lm->kc, l), lm->kv_layer_ptr(lm->vc, l), lm->att, lm->seqlens, B, H,
-                             dh, c.max_ctx, lm->kv_sb, lm->kv_sh, 1.0f / sqrtf((float)dh), lm->attn_ws, s, d,
+                             dh, c.max_ctx, lm->kv_sb, lm->kv_sh, 1.0f / sqrtf((float)dh), lm->attn_ws, lm->attn_ctr, s, d,
                              c.kv_bf16 != 0, /*wide*/ true));
         TRY(prof_end(lm));
         SkinnyEpiArgs eo;
@@ -518,6 +518,10 @@ jas_status jas_lm_create(const jas_lm_config *cfg, jas_lm **out)
     for (int b = 1; b < Bm; ++b)  // workspace must cover every batch size actually used
         lm->attn_ws_bytes = std::max(lm->attn_ws_bytes, jas_attn_decode_workspace(b, c.n_head, dh, c.max_ctx));
     if (st == JAS_OK && lm->attn_ws_bytes) st = jas_malloc(&lm->attn_ws, lm->attn_ws_bytes);
+    // split-arrival counters of the attention's in-kernel merge: zero here, and every decode
+    // step leaves them zero (outside any captured graph)
+    if (st == JAS_OK && lm->attn_ws_bytes) st = jas_malloc((void **)&lm->attn_ctr, sizeof(unsigned) * Bm * c.n_head);
+    if (st == JAS_OK && lm->attn_ctr) st = jas_memset(lm->attn_ctr, 0, sizeof(unsigned) * Bm * c.n_head, lm->stream);
     if (st == JAS_OK && c.kind == 1) {
         const long n = (long)c.max_ctx * (dh / 2);
         st = jas_malloc((void **)&lm->rope_tab, sizeof(double2) * n);
@@ -544,7 +548,7 @@ jas_status jas_lm_destroy(jas_lm *lm)
     if (lm->stream) (void)hipStreamSynchronize(lm->stream);
     if (lm->graph) (void)hipGraphExecDestroy(lm->graph);
     void *ptrs[] = {lm->amax_v, lm->amax_i, lm->dstate, lm->arena, lm->kc, lm->vc, lm->x, lm->h, lm->q, lm->att, lm->ff, lm->logits, lm->ids, lm->pos,
-                    lm->seqlens, lm->hist, lm->attn_ws, lm->part, lm->pX, lm->pH, lm->pQKV, lm->pATT, lm->pG, lm->pU, lm->pFF,
+                    lm->seqlens, lm->hist, lm->attn_ws, lm->attn_ctr, lm->part, lm->pX, lm->pH, lm->pQKV, lm->pATT, lm->pG, lm->pU, lm->pFF,
                     lm->pIds, lm->pPos, lm->rope_tab};
     for (void *p : ptrs)
         if (p) (void)hipFree(p);

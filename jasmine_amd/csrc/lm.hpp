@@ -58,6 +58,7 @@ struct jas_lm {
     int graph_B = 0, graph_cap = 0;
     const int32_t *graph_hist = nullptr;
     void *attn_ws = nullptr;
+    unsigned *attn_ctr = nullptr;  // [max_batch * n_head] split-arrival counters (zero between steps)
     double2 *rope_tab = nullptr;  // LLaMA: [max_ctx][dh / 2] (cos, sin) for the QKV epilogue
     float *part = nullptr;  // K-split partials of the residual projections [split][16][d]
     int ks_o = 1, ks_d = 1;

@@ -54,14 +54,48 @@ void *workspace(size_t bytes, hipStream_t s)
     return w.p;
 }
 
+// Split-arrival counters (decode attention's in-kernel merge), one zeroed array per stream.
+// Kernels leave every counter at zero, so an array is zeroed only when it is allocated; it
+// grows (after its stream has drained) like the scratch above.
+static std::unordered_map<hipStream_t, Scratch> g_ctr;
+unsigned *arrival_counters(size_t n, hipStream_t s)
+{
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    Scratch &w = g_ctr[s];
+    const size_t bytes = n * sizeof(unsigned);
+    if (bytes <= w.bytes) return (unsigned *)w.p;
+    if (w.p) {
+        (void)hipStreamSynchronize(s);
+        (void)hipFree(w.p);
+    }
+    const size_t nb = bytes < 4096 ? 4096 : bytes;
+    w.p = nullptr;
+    w.bytes = 0;
+    if (hipMalloc(&w.p, nb) != hipSuccess) return (unsigned *)(w.p = nullptr);
+    if (hipMemset(w.p, 0, nb) != hipSuccess) {  // synchronous: never part of a captured graph
+        (void)hipFree(w.p);
+        w.p = nullptr;
+        return nullptr;
+    }
+    w.bytes = nb;
+    return (unsigned *)w.p;
+}
+
 jas_status release_workspace(hipStream_t s)
 {
     std::lock_guard<std::mutex> lk(g_ws_mu);
     auto it = g_ws.find(s);
-    if (it == g_ws.end()) return JAS_OK;
-    JAS_HIP(hipStreamSynchronize(s));  // queued kernels may still read the buffer
-    if (it->second.p) JAS_HIP(hipFree(it->second.p));
-    g_ws.erase(it);
+    auto ic = g_ctr.find(s);
+    if (it == g_ws.end() && ic == g_ctr.end()) return JAS_OK;
+    JAS_HIP(hipStreamSynchronize(s));  // queued kernels may still read the buffers
+    if (it != g_ws.end()) {
+        if (it->second.p) JAS_HIP(hipFree(it->second.p));
+        g_ws.erase(it);
+    }
+    if (ic != g_ctr.end()) {
+        if (ic->second.p) JAS_HIP(hipFree(ic->second.p));
+        g_ctr.erase(ic);
+    }
     return JAS_OK;
 }
 
