@@ -148,9 +148,66 @@ def cpu_baseline(B, ctx):
                "config3_note": "one head timed (scores, mask, hsoftmax, V P^T of mat_head_gen_t), x 96 heads",
                "config5_layer_s": round(t_layer, 3), "config5_lm_head_s": round(t_head, 3),
                "cores": 1, "host_cpu": model}
+        per.update(cpu_more_configs(ref, ctx))
     except Exception as e:  # pragma: no cover
         log("[bench] cpu config lines failed:", e)
     return head, per
+
+
+def cpu_more_configs(ref, ctx5):
+    """The remaining CPU lines: config 1 timed in full through the restatement (jasmine has
+    no GPT-2 block: pre-LN, GELU, learned positions), and sampled slices of configs 4 and 5
+    through the reference's own objects (oracle/_ref), extrapolated and labelled so.  About
+    15 s of one core."""
+    import ctypes as C
+    import numpy as np
+    from oracle_lib import orc, fp, ip, normal, randint, LmCfg, LmWeights, LM_WEIGHT_FIELDS
+    out = {}
+    # config 1: 2 layers, d 128, 4 heads, FFN 512, vocab 256, 32-token prompt, 32 greedy steps
+    L, d, H, F, V, P, S = 2, 128, 4, 512, 256, 32, 32
+    shp = {"wte": (V, d), "wpe": (P + S, d), "ln1_g": (L, d), "ln1_b": (L, d), "w_qkv": (L, 3 * d, d),
+           "b_qkv": (L, 3 * d), "w_o": (L, d, d), "b_o": (L, d), "ln2_g": (L, d), "ln2_b": (L, d),
+           "w_fc": (L, F, d), "b_fc": (L, F), "w_proj": (L, d, F), "b_proj": (L, d), "lnf_g": (d,), "lnf_b": (d,)}
+    w = {n: np.ascontiguousarray(normal(s, 0, k, 0.0, 0.02)) for k, (n, s) in enumerate(shp.items())}
+    ow = LmWeights(*[fp(w[n]) if n in w else None for n in LM_WEIGHT_FIELDS])
+    ids, prompt = np.zeros((1, S), np.int32), randint((1, P), V, 0)
+    t0 = time.perf_counter()
+    orc.orc_lm_generate(LmCfg(0, L, d, H, F, V, P + S, 1e-5, 1e4, 0), ow, 1, P, ip(prompt), S, None, ip(ids), None, 1)
+    t1 = time.perf_counter() - t0
+    out["config1_full_s"] = round(t1, 4)
+    out["config1_tok_s"] = round(S / t1, 1)
+    out["config1_note"] = ("timed in full (32-token prompt + 32 greedy steps, KV cache) through the C restatement "
+                           "oracle/oracle.c, 1 thread: kind 'port', jasmine has no GPT-2 block")
+    # config 4: GPT-2 small, batch 8, 512-token prompts, greedy decode at ~560 keys
+    a = C.c_double()
+    t_l4 = ref.ref_time_gpt2_layer(768, 12, 3072, 560, C.byref(a))
+    t_h4 = ref.ref_time_linear(50257, 768, 1, 1)
+    step4 = 8 * (12 * t_l4 + t_h4)
+    ap = C.c_double()
+    t_p4 = ref.ref_time_prefill_layer(0, 768, 12, 3072, 128, C.byref(ap))
+    pf4 = 8 * 12 * ((t_p4 - ap.value) * 512 / 128 + ap.value * (512 / 128) ** 2)
+    out.update(config4_layer_s=round(t_l4, 4), config4_layer_attention_s=round(a.value, 4),
+               config4_lm_head_s=round(t_h4, 4), config4_step_s_extrapolated=round(step4, 3),
+               config4_decode_tok_s_extrapolated=round(8 / step4, 3),
+               config4_prefill_slice_s=round(t_p4, 3), config4_prefill_slice_attention_s=round(ap.value, 3),
+               config4_prefill_s_extrapolated=round(pf4, 1),
+               config4_note=("reference objects (oracle/_ref, g++ -O2, 1 thread): one GPT-2-small decode layer of "
+                             "one sequence over 560 cached keys, the 50257 x 768 LM-head GEMV, and one layer of a "
+                             "128-token prefill slice; extrapolated to 8 sequences x 12 layers (decode) and to "
+                             "8 x 512-token prompts (projections x 4, attention x 16)"))
+    # config 5 prefill slice: one layer over 4 tokens (projections; jasmine's mat_dot_t streams
+    # the weights once per token column) and one causal head over 256 tokens (attention)
+    t_p5 = ref.ref_time_prefill_layer(1, 4096, 32, 11008, 4, C.byref(ap))
+    t_a5 = ref.ref_time_attention_head(128, 256)
+    pf5 = 16 * 32 * ((t_p5 - ap.value) * 2048 / 4 + 32 * t_a5 * (2048 / 256) ** 2)
+    out.update(config5_prefill_slice_s=round(t_p5, 3), config5_prefill_head256_s=round(t_a5, 4),
+               config5_prefill_s_extrapolated=round(pf5, 0),
+               config5_prefill_note=("reference objects: one LLaMA-7B layer's projections over a 4-token slice "
+                                     "(x 512 tokens) and one causal head over 256 tokens (x 32 heads x 64 for "
+                                     "2048 tokens), extrapolated to 16 x 2048-token prompts x 32 layers"))
+    log(f"[bench] cpu: config1 {t1:.3f} s in full; config4 step {step4:.1f} s, prefill {pf4:.0f} s (extrapolated); "
+        f"config5 prefill {pf5:.0f} s (extrapolated)")
+    return out
 
 
 def gpt2_decode_bytes(L, d, F, V, B, ctx):

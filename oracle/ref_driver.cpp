@@ -421,6 +421,105 @@ double ref_time_llama_layer(int d, int H, int F, int T, double *attn_s)
     return std::chrono::duration<double>(t1 - t0).count();
 }
 
+// ---- GPT-2-shaped decode step of one sequence, on jasmine's own objects ----
+// As ref_time_llama_layer, for the GPT-2 block (config 4): four projections with bias
+// through weight_net_t::forward (QKV as three d x d nets, O, FC d -> F, proj F -> d), the same
+// per-head attention over a T-key cache, and the O(d) glue (row LayerNorm, GELU, residual
+// adds) as plain loops.  Seconds for one layer; *attn_s gets the attention part.
+static void ln_rows(mat_t<float> &h, const mat_t<float> &x, int d)
+{
+    double m = 0, v = 0;
+    for (int i = 0; i < d; ++i) m += x(i, 0);
+    m /= d;
+    for (int i = 0; i < d; ++i) v += (x(i, 0) - m) * (x(i, 0) - m);
+    const float r = (float)(1.0 / std::sqrt(v / d + 1e-5));
+    for (int i = 0; i < d; ++i) h(i, 0) = (float)(x(i, 0) - m) * r;
+}
+
+double ref_time_gpt2_layer(int d, int H, int F, int T, double *attn_s)
+{
+    using M = mat_t<float>;
+    const int dh = d / H;
+    weight_net_t<M, upd_t> wq(d, d), wk(d, d), wv(d, d), wo(d, d), wf(d, F), wp(F, d);
+    std::vector<M> kc, vc;
+    for (int h = 0; h < H; ++h) {
+        kc.emplace_back(dh, T);
+        vc.emplace_back(dh, T);
+    }
+    M x(d, 1), hbuf(d, 1), att(d, 1);
+    for (int i = 0; i < d; ++i) x(i, 0) = 0.01f * (float)(i % 17);
+    volatile float sink = 0;
+    auto t0 = std::chrono::steady_clock::now();
+    ln_rows(hbuf, x, d);
+    M q = wq.forward(hbuf), k = wk.forward(hbuf), v = wv.forward(hbuf);
+    auto ta = std::chrono::steady_clock::now();
+    for (int h = 0; h < H; ++h) {
+        M qh = q.view(h * dh, 0, dh, 1);
+        auto scores = (qh.t().dot(kc[h]) / sqrt(dh)).clone();
+        auto p = hsoftmax(scores);
+        auto o = vc[h].dot(p.t()).clone();
+        for (int e = 0; e < dh; ++e) att(h * dh + e, 0) = o(e, 0);
+    }
+    auto tb = std::chrono::steady_clock::now();
+    M o = wo.forward(att);
+    for (int i = 0; i < d; ++i) x(i, 0) = x(i, 0) + o(i, 0);
+    ln_rows(hbuf, x, d);
+    M f = wf.forward(hbuf);
+    for (int i = 0; i < F; ++i) {
+        const float z = f(i, 0);
+        f(i, 0) = 0.5f * z * (1.0f + std::tanh(0.7978845608f * (z + 0.044715f * z * z * z)));
+    }
+    M pr = wp.forward(f);
+    for (int i = 0; i < d; ++i) x(i, 0) = x(i, 0) + pr(i, 0);
+    sink = sink + x(0, 0) + (float)k(0, 0) + (float)v(0, 0);
+    auto t1 = std::chrono::steady_clock::now();
+    if (attn_s) *attn_s = std::chrono::duration<double>(tb - ta).count();
+    return std::chrono::duration<double>(t1 - t0).count();
+}
+
+// ---- one layer of a T-token prefill slice, on jasmine's own objects ----
+// kind 0 (GPT-2 block: QKV, O, FC, proj) or 1 (LLaMA block: QKV, O, gate, up, down), every
+// projection through weight_net_t::forward on a [d, T] token matrix (mat_dot_t over the T
+// columns), causal attention per head as mat_head_gen_t computes it after its projections
+// (scores, mask, hsoftmax, V P^T; mat_mha_t.hpp:53-71); norms and activations are O(d T) and
+// left out.  Seconds for the layer; *attn_s gets the attention part, which grows with T^2
+// where the projections grow with T.
+double ref_time_prefill_layer(int kind, int d, int H, int F, int T, double *attn_s)
+{
+    using M = mat_t<float>;
+    const int dh = d / H;
+    weight_net_t<M, upd_t> wq(d, d), wk(d, d), wv(d, d), wo(d, d), w1(d, F), w2(F, d), w3(d, F);
+    M x(d, T);
+    init_matrix<hash_init_t>(x);
+    volatile float sink = 0;
+    auto t0 = std::chrono::steady_clock::now();
+    M q = wq.forward(x), k = wk.forward(x), v = wv.forward(x);
+    auto ta = std::chrono::steady_clock::now();
+    M att(d, T);
+    for (int h = 0; h < H; ++h) {
+        M qh = q.view(h * dh, 0, dh, T), kh = k.view(h * dh, 0, dh, T), vh = v.view(h * dh, 0, dh, T);
+        auto scores = (qh.t().dot(kh) / sqrt(dh)).clone();
+        for (int i = 0; i < T; ++i)
+            for (int j = i + 1; j < T; ++j) scores(i, j) = -std::numeric_limits<float>::infinity();
+        auto p = hsoftmax(scores);
+        auto o = vh.dot(p.t()).clone();
+        for (int e = 0; e < dh; ++e)
+            for (int t = 0; t < T; ++t) att(h * dh + e, t) = o(e, t);
+    }
+    auto tb = std::chrono::steady_clock::now();
+    M o = wo.forward(att);
+    M f = w1.forward(o);
+    if (kind == 1) {
+        M u = w3.forward(o);
+        sink = sink + u(0, 0);
+    }
+    M dn = w2.forward(f);
+    sink = sink + dn(0, 0);
+    auto t1 = std::chrono::steady_clock::now();
+    if (attn_s) *attn_s = std::chrono::duration<double>(tb - ta).count();
+    return std::chrono::duration<double>(t1 - t0).count();
+}
+
 // one causal attention head of S tokens at head dim dh without its projections (the
 // scores, mask, softmax and weighted sum of mat_head_gen_t::forward, mat_mha_t.hpp:53-71)
 double ref_time_attention_head(int dh, int S)

@@ -119,8 +119,11 @@ if ref is not None:
                  ("ref_time_attention_head", 2)):
         getattr(ref, n).restype = C.c_double
         getattr(ref, n).argtypes = [C.c_int] * k
-    ref.ref_time_llama_layer.restype = C.c_double
-    ref.ref_time_llama_layer.argtypes = [C.c_int] * 4 + [C.POINTER(C.c_double)]
+    for n in ("ref_time_llama_layer", "ref_time_gpt2_layer"):
+        getattr(ref, n).restype = C.c_double
+        getattr(ref, n).argtypes = [C.c_int] * 4 + [C.POINTER(C.c_double)]
+    ref.ref_time_prefill_layer.restype = C.c_double
+    ref.ref_time_prefill_layer.argtypes = [C.c_int] * 5 + [C.POINTER(C.c_double)]
 
 
 def normal(shape, seed, stream=0, mean=0.0, std=1.0):
