@@ -604,6 +604,39 @@ def test_attn_decode(jas, B, H, D, lens):
     close(do.numpy(), want[:, :, 0], atol=1e-5, rtol=1e-4)
 
 
+@pytest.mark.parametrize("B,H,D,lens,cap", [(2, 3, 64, (1, 37), 300), (3, 2, 128, (1000, 513, 64), 1100),
+                                            (8, 12, 64, (1024, 0, 5, 129, 1024, 700, 1, 64), 1024),
+                                            (2, 4, 32, (2049, 100), 2100)])
+def test_attn_decode_poisoned_tail(jas, B, H, D, lens, cap):
+    """Cache rows at and past each sequence's length hold NaN and Inf (the kernel's first
+    tile is requested before the length is known, bounded only by the cache's row count
+    max_len = cap): they must carry no weight.  Empty sequences (length 0) give zeros."""
+    K, V = normal((B, H, cap, D), 33, 0), normal((B, H, cap, D), 33, 1)
+    for b, L in enumerate(lens):
+        K[b, :, L:] = np.nan
+        V[b, :, L::2] = np.inf
+        V[b, :, L + 1::2] = np.nan
+    q = normal((B, H, 1, D), 33, 2)
+    sc = 1 / math.sqrt(D)
+    want = np.zeros((B, H, D), np.float32)
+    for b, L in enumerate(lens):
+        if L == 0:
+            continue
+        o = np.zeros((1, H, 1, D), np.float32)
+        orc.orc_attention(fp(np.ascontiguousarray(q[b:b + 1])), fp(np.ascontiguousarray(K[b:b + 1, :, :L])),
+                          fp(np.ascontiguousarray(V[b:b + 1, :, :L])), fp(o), 1, H, 1, L, D, sc, 1)
+        want[b] = o[0, :, 0]
+    dq, dk, dv, do = jas.to_device(q), jas.to_device(K), jas.to_device(V), jas.DeviceArray((B, H, D))
+    dl = jas.to_device(np.array(lens, np.int32))
+    ws = jas.DeviceArray(max(jas.lib.jas_attn_decode_workspace(B, H, D, cap) // 4, 1))
+    for _ in range(2):  # the split-arrival counters are left at zero for the next call
+        jas.check(jas.lib.jas_attn_decode(dq.p, dk.p, dv.p, do.p, dl.p, B, H, D, cap, H * cap * D, cap * D, sc,
+                                          ws.p, None))
+        got = do.numpy()
+        assert np.all(np.isfinite(got))
+        close(got, want, atol=1e-5, rtol=1e-4)
+
+
 # ---------------------------------------------------------------- RoPE / embed / argmax / rng
 def test_rope_jasmine(jas):
     for d, T in ((16, 6), (64, 33), (7, 5)):
