@@ -283,6 +283,18 @@ def run_kernel_legs(jas, reps=10):
     # device-to-device copy of one 8192^2 fp32 matrix (one read and one write per byte)
     ms = time_launches(lambda: chk(lib.jas_memcpy_d2d(D.p, A.p, mb, None)), reps)
     out["hbm_copy"] = line("device-to-device copy (HIP runtime), 268 MB: achievable-bandwidth reference", ms, 2 * mb)
+    # the achievable streaming-read rate (jas_hbm_read_probe: grid-stride nontemporal 16-byte
+    # reads, 8 in flight per thread) at two of the decode kernels' sizes: config 3's 50 MB
+    # K/V and a 201 MB LLaMA-7B QKV matrix, read from the 268 MB matrix A
+    big = A
+    sink = jas.DeviceArray((1,), np.uint32)
+    ceil = {}
+    for nb in (50331648, 201326592):
+        ms = time_launches(lambda: chk(lib.jas_hbm_read_probe(big.p, nb, 2048, 8, 1, sink.p, None)), reps * 3)
+        ceil[str(nb)] = round(nb / (ms * 1e-3) / 1e9, 1)
+    out["hbm_read_ceiling"] = {"kernel": "read_probe_kernel<8, nontemporal> (jas_hbm_read_probe), 2048 x 256 threads",
+                               "GB_s_by_bytes": ceil, "peak": HBM_PEAK_GBS,
+                               "note": "repeated reads of one buffer (the Infinity Cache may hold the 50 MB case)"}
     ms = time_launches(lambda: chk(lib.jas_ew_eval(pa, len(prog), la, len(leaves), D.p, 0, R, Cc, None)), reps)
     out["ew_cfg2"] = line("ew_eval_kernel: D = A*B + 0.5*C - tanh(A), 8192^2 fp32 (3 reads + 1 write)", ms, 4 * mb)
     ms = time_launches(lambda: chk(lib.jas_softmax(D.p, Y.p, R, Cc, Cc, Cc, 1, None)), reps)
@@ -663,7 +675,10 @@ def main():
         log("[bench] config 2/3 kernel lines")
         kernels = run_kernel_legs(jas)
         for k, v in kernels.items():
-            log(f"[bench]   {k}: {v['avg_launch_us']} us, {v['achieved']} {v['unit']} ({100 * v['frac']:.1f}% of peak)")
+            if "avg_launch_us" in v:
+                log(f"[bench]   {k}: {v['avg_launch_us']} us, {v['achieved']} {v['unit']} ({100 * v['frac']:.1f}% of peak)")
+            else:
+                log(f"[bench]   {k}: {v}")
     B, P = args.batch, args.prompt
     L, d, H, F, V = 32, 4096, 32, 11008, 32000
     dh = d // H

@@ -280,6 +280,13 @@ jas_status jas_argmax(const float *d_x, int n, int V, long ld, int32_t *d_out, j
 /* Seeded N(mean, std) fill, same counter-based generator as the host side. */
 jas_status jas_fill_normal(float *d_x, size_t n, uint64_t seed, uint64_t stream_id, float mean, float std,
                            jas_stream_t stream);
+/* Bandwidth calibration, no counterpart in the reference: a grid-stride streaming read of
+ * `bytes` (16-byte aligned, a multiple of 16) by `workgroups` 256-thread workgroups with 4 or
+ * 8 16-byte loads in flight per thread, nontemporal or plain.  d_sink (4 bytes) is written
+ * only in the unlikely case that the folded data equal a fixed constant.  bench.py uses it
+ * as the achievable-read ceiling next to the HBM-bound kernels. */
+jas_status jas_hbm_read_probe(const void *d_buf, size_t bytes, int workgroups, int loads_in_flight, int nontemporal,
+                              unsigned *d_sink, jas_stream_t stream);
 
 /* ------------------------------------------------------------------ decoder LM runner */
 /* Decoder-only language model (GPT-2 / LLaMA shapes).  The reference has no token

@@ -89,6 +89,7 @@ _sigs = {
     "jas_lm_project": [VP, C.c_char_p, I, I, VP, VP, VP],
     "jas_lm_proj_geometry": [VP, C.c_char_p, IP],
     "jas_stream_release_scratch": [VP],
+    "jas_hbm_read_probe": [VP, C.c_size_t, I, I, I, VP, VP],
 }
 for _n, _a in _sigs.items():
     getattr(lib, _n).argtypes = _a

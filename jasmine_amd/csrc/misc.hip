@@ -185,6 +185,28 @@ __global__ void fill_normal_kernel(float *x, size_t n, uint64_t key, float mean,
 
 using namespace jas;
 
+// Achievable streaming-read rate (bandwidth calibration, not a jasmine operation): every
+// thread reads 16-byte chunks grid-stride, U loads in flight, and folds them into one word
+// that is stored only if it equals a value no input makes likely, so the reads cannot be
+// removed.  NT: nontemporal loads, as the decode kernels issue them.
+template <int U, bool NT>
+__global__ void __launch_bounds__(256) read_probe_kernel(const u32x4 *__restrict__ a, long n16, unsigned *sink)
+{
+    const long stride = (long)gridDim.x * 256;
+    unsigned acc = 0;
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride * U) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const long j = min(i + u * stride, n16 - 1);
+            v[u] = NT ? __builtin_nontemporal_load(a + j) : a[j];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+    if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
 extern "C" {
 
 jas_status jas_rope_jasmine(const float *x, float *y, int d, int T, jas_stream_t stream)
@@ -240,6 +262,24 @@ jas_status jas_fill_normal(float *x, size_t n, uint64_t seed, uint64_t stream_id
     unsigned nb = (unsigned)std::min<size_t>((n + 255) / 256, 65536);
     hipLaunchKernelGGL(fill_normal_kernel, dim3(nb), dim3(256), 0, stream_or_default(stream), x, n,
                        stream_key(seed, stream_id), mean, std);
+    JAS_LAUNCH_CHECK();
+    return JAS_OK;
+}
+
+jas_status jas_hbm_read_probe(const void *d_buf, size_t bytes, int workgroups, int loads_in_flight, int nontemporal,
+                              unsigned *d_sink, jas_stream_t stream)
+{
+    JAS_CHECK(d_buf && d_sink && bytes >= 16 && bytes % 16 == 0 && (uintptr_t)d_buf % 16 == 0, JAS_ERR_INVALID,
+              "jas_hbm_read_probe: need a 16-byte aligned buffer of a multiple of 16 bytes");
+    JAS_CHECK(workgroups > 0 && (loads_in_flight == 4 || loads_in_flight == 8), JAS_ERR_INVALID,
+              "jas_hbm_read_probe: workgroups > 0, 4 or 8 loads in flight");
+    const long n16 = (long)(bytes / 16);
+    hipStream_t s = stream_or_default(stream);
+    const u32x4 *a = (const u32x4 *)d_buf;
+    if (loads_in_flight == 4 && nontemporal) hipLaunchKernelGGL((read_probe_kernel<4, true>), dim3(workgroups), dim3(256), 0, s, a, n16, d_sink);
+    else if (loads_in_flight == 4) hipLaunchKernelGGL((read_probe_kernel<4, false>), dim3(workgroups), dim3(256), 0, s, a, n16, d_sink);
+    else if (nontemporal) hipLaunchKernelGGL((read_probe_kernel<8, true>), dim3(workgroups), dim3(256), 0, s, a, n16, d_sink);
+    else hipLaunchKernelGGL((read_probe_kernel<8, false>), dim3(workgroups), dim3(256), 0, s, a, n16, d_sink);
     JAS_LAUNCH_CHECK();
     return JAS_OK;
 }

@@ -35,7 +35,7 @@ def load(path):
 
 def test_fixtures_present():
     names = {os.path.basename(p) for p in FIXTURES}
-    for c in ("config4_seq0", "config4_seq5"):
+    for c in ("config4_seq0", "config4_seq5", "config5_seq0", "config5_seq11"):
         assert f"lm_fixture_{c}.npz" in names, c
 
 
