@@ -246,6 +246,33 @@ def run_gpt2(jas, cfg_args, B, P, seed, steps, warmup, graph=True):
     return B * steps / dt, 1e3 * dt / steps, gpt2_decode_bytes(L, d, F, V, B, mean_ctx)
 
 
+def read_ceiling():
+    """Streaming-read rate of jas_hbm_read_probe (grid-stride nontemporal 16-byte loads, 8 in
+    flight per thread, 256-thread workgroups) by transfer size and workgroup count.  'fresh':
+    successive launches read successive ranges of a 1 GiB buffer, so a range is not re-read
+    while the Infinity Cache could still hold it; 'same': every launch re-reads one range."""
+    import ctypes as C
+    import numpy as np
+    import jasmine_amd as jas
+    from jasmine_amd.timing import time_launches
+    lib, chk = jas.lib, jas.check
+    chk(lib.jas_init(0))
+    n = 1 << 28
+    buf = jas.DeviceArray((n,))
+    chk(lib.jas_fill_normal(buf.p, n, 0, 0, 0.0, 1.0, None))
+    sink = jas.DeviceArray((1,), np.uint32)
+    out = {"unit": "GB/s (us per launch in brackets)", "fresh": {}, "same": {}}
+    for nb in (2359296, 9437184, 50331648, 201326592):
+        for wgs in (48, 96, 192, 256, 512, 2048):
+            offs = iter([((i * nb) % ((1 << 30) - nb)) // 256 * 256 for i in range(4000)])
+            ms = time_launches(lambda: chk(lib.jas_hbm_read_probe(C.c_void_p(buf.ptr + next(offs)), nb, wgs, 8, 1,
+                                                                  sink.p, None)), 30)
+            out["fresh"].setdefault(str(nb), {})[str(wgs)] = f"{nb / ms / 1e6:.0f} ({ms * 1e3:.2f})"
+            ms = time_launches(lambda: chk(lib.jas_hbm_read_probe(buf.p, nb, wgs, 8, 1, sink.p, None)), 30)
+            out["same"].setdefault(str(nb), {})[str(wgs)] = f"{nb / ms / 1e6:.0f} ({ms * 1e3:.2f})"
+    print(json.dumps({"hbm_read_ceiling": out}, indent=1), flush=True)
+
+
 def run_kernel_legs(jas, reps=10):
     """Configs 2 and 3 as per-kernel lines: HIP events on the library stream around `reps`
     back-to-back launches of each kernel at the config's full shape (inputs resident)."""
@@ -620,6 +647,9 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="decode with eager launches instead of graph replay (same kernels; for profilers)")
     ap.add_argument("--copy-calib", action="store_true", help="only run the copy used to calibrate PMC bytes")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="only the streaming-read sweep (jas_hbm_read_probe): sizes x workgroup counts, each "
+                         "launch at a fresh offset of a 1 GiB buffer, plus re-reads of one buffer")
     ap.add_argument("--traffic-kernels", action="store_true",
                     help="only run the dominant decode kernel at the profiled pass's shape (for rocprofv3 --pmc)")
     ap.add_argument("--traffic-bf16", action="store_true",
@@ -629,6 +659,9 @@ def main():
     args = ap.parse_args()
     if args.copy_calib:
         copy_calibration()
+        return
+    if args.read_ceiling:
+        read_ceiling()
         return
     if args.traffic_kernels:
         traffic_kernels(args)
