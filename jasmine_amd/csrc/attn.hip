@@ -551,7 +551,6 @@ struct DecodeArgs {
     int B, H, nsplit, chunk;
     float scale_log2;
     int o_packed_d;  // > 0: write O in the packed B-operand layout over o_packed_d features
-    int max_len;     // cache rows per (sequence, head): every row below it may be read
 };
 
 // Cross-workgroup hand-off of split partials.  The L2 caches of the XCDs are not coherent
@@ -638,13 +637,19 @@ __global__ void __launch_bounds__(WPB * 64) attn_decode_kernel(const DecodeArgs 
     constexpr int TPK = D / EPL;            // lanes per key
     constexpr int GPW = WAVE / TPK;         // key groups per wave
     constexpr int NG = WPB * GPW;           // key groups per workgroup
-    constexpr int U = 4;                    // keys per group and tile (two tiles in flight)
+    constexpr int U = WPB > 4 ? 8 : 4;      // keys per group per iteration (loads in flight)
     __shared__ float sm[NG], sl[NG];
     __shared__ float sacc[NG][D];
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int grp = w * GPW + lane / TPK, lig = lane % TPK;
     const int bh = blockIdx.y, b = bh / p.H, h = bh % p.H, split = blockIdx.x;
+    const int len = p.seqlens[b];
+    const int k0 = split * p.chunk, k1 = min(len, k0 + p.chunk);
+
+    float q[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) q[e] = p.q[(long)bh * D + EPL * lig + e] * p.scale_log2;
     const KT *Kb = (const KT *)p.K + (long)b * p.k_sb + (long)h * p.k_sh + EPL * lig;
     const KT *Vb = (const KT *)p.V + (long)b * p.k_sb + (long)h * p.k_sh + EPL * lig;
     // one 16-byte load per key row and lane, kept raw until it is used (bf16: eight elements
@@ -655,56 +660,29 @@ __global__ void __launch_bounds__(WPB * 64) attn_decode_kernel(const DecodeArgs 
         if constexpr (KB) return __uint_as_float(e & 1 ? u[e >> 1] & 0xffff0000u : u[e >> 1] << 16);
         else return __uint_as_float(u[e]);
     };
-    // tile of U keys per group starting at kb; keys past `last` re-read row `last` (in bounds,
-    // no branch around a load), their scores are masked and their values zeroed on use.
-    // Compiler-only barriers on both sides: the loads are issued here, not moved to their
-    // first use (which would undo the prefetch); they wait for nothing.
-    auto fetch = [&](u32x4_t (&kt)[U], u32x4_t (&vt)[U], int kb, int last) {
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int key = min(kb + grp + u * NG, last);
-            kt[u] = ld16(Kb + (long)key * D);
-            vt[u] = ld16(Vb + (long)key * D);
-        }
-        asm volatile("" ::: "memory");
-    };
-    // The length and the query are requested first, then the first tile (it needs neither:
-    // it stays below the cache's row count), so all three share one memory round trip and
-    // waiting for the length does not wait for the tile.
-    const int k0 = split * p.chunk, cap = min(k0 + p.chunk, p.max_len);
-    const int len = p.seqlens[b];
-    float q[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) q[e] = p.q[(long)bh * D + EPL * lig + e];
-    u32x4_t ka[U], va[U], kn[U], vn[U];
-    fetch(ka, va, k0, cap - 1);
-    const int k1 = min(len, k0 + p.chunk);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) q[e] *= p.scale_log2;
 
     float m = -FLT_MAX, l = 0.f;
     float acc[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-    // one tile of keys kb + grp + u * NG (masked past k1) into the running max, sum and
-    // weighted values.  The tile passes through an empty asm first: its arithmetic cannot be
-    // scheduled ahead of the next tile's loads (this waits for the current tile only).
-    auto consume = [&](u32x4_t (&kc)[U], u32x4_t (&vc)[U], int kb) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) asm volatile("" : "+v"(kc[u]), "+v"(vc[u]));
-        const int kk = kb + grp;
+    for (int kk = k0 + grp; kk < k1; kk += NG * U) {
+        u32x4_t kv[U], vv[U];
         float sc[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const bool in = kk + u * NG < k1;
-            if (!in) vc[u] = u32x4_t{0u, 0u, 0u, 0u};  // rows past the length may hold anything
-            float d = q[0] * elem(kc[u], 0);
+            int key = kk + u * NG;
+            bool ok = key < k1;
+            kv[u] = ok ? ld16(Kb + (long)key * D) : u32x4_t{0u, 0u, 0u, 0u};
+            vv[u] = ok ? ld16(Vb + (long)key * D) : u32x4_t{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
-            for (int e = 1; e < EPL; ++e) d += q[e] * elem(kc[u], e);
+        for (int u = 0; u < U; ++u) {
+            float d = q[0] * elem(kv[u], 0);
+#pragma unroll
+            for (int e = 1; e < EPL; ++e) d += q[e] * elem(kv[u], e);
 #pragma unroll
             for (int o = TPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, WAVE);
-            sc[u] = in ? d : -FLT_MAX;
+            sc[u] = (kk + u * NG) < k1 ? d : -FLT_MAX;
         }
         float mx = m;
 #pragma unroll
@@ -718,25 +696,9 @@ __global__ void __launch_bounds__(WPB * 64) attn_decode_kernel(const DecodeArgs 
             float pv = sc[u] == -FLT_MAX ? 0.f : exp2f(sc[u] - mx);
             l += pv;
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) acc[e] += pv * elem(vc[u], e);
+            for (int e = 0; e < EPL; ++e) acc[e] += pv * elem(vv[u], e);
         }
         m = mx;
-    };
-    // Two tile buffers in turn (no register copies, so no wait at the loop's back edge): the
-    // next tile is requested before the current one is consumed; past the end it re-reads
-    // row max(k1 - 1, k0) (cache hits, no branch).  The trip count is uniform over the
-    // workgroup, and there is at least one trip, so that no branch ahead of the loop invites
-    // the compiler to sink the first tile's loads behind the length: an empty split
-    // (k1 <= k0) masks every key and leaves m = -FLT_MAX, l = 0, acc = 0.
-    const int klast = max(k1 - 1, k0);
-    constexpr int TK = NG * U;  // keys per tile
-    for (int kb = k0;; kb += 2 * TK) {
-        fetch(kn, vn, kb + TK, klast);
-        consume(ka, va, kb);
-        if (kb + TK >= k1) break;
-        fetch(ka, va, kb + 2 * TK, klast);
-        consume(kn, vn, kb + TK);
-        if (kb + 2 * TK >= k1) break;
     }
     // merge the key groups of this workgroup: wave 0 finds the common max and each group's
     // weight (one group per lane, shuffle reductions); then every thread sums the weighted
@@ -806,10 +768,11 @@ __global__ void __launch_bounds__(WPB * 64) attn_decode_kernel(const DecodeArgs 
 // keys) eight splits of 128 against six of 192: 10.7 against 12.1 us with the merge.  With
 // the merge done by each pair's last split (no second launch) config 3 stays at 10.4-10.8 us
 // for splits of 64 to 256 keys: the hand-off's store, counter and load round trips cost what
-// the merge launch did.  Two tiles in flight (the first one requested with the query and
-// the length) moved the bf16-cache LLaMA-7B batch-16 attention from 0.767 to 0.793 of HBM
-// peak and left the fp32 one at 0.834; config 3 measured 10.9 -> 11.2 us (kernel trace),
-// where a bare 50 MB streaming read of the same grid takes 5.7-8.6 us.  A sequence's keys fall into the same splits
+// the merge launch did.  Two tiles of 4 keys in flight per workgroup (the first requested
+// together with the query and the length, unpredicated clamped loads) measured no better in
+// same-box A/B pairs: config 3 11.5 / 11.3 against 10.6 / 11.2 us, batch-1 LLaMA-7B 197.6
+// against 199.0-199.4 tok/s, the batch-16 lines within the run-to-run spread.  A sequence's
+// keys fall into the same splits
 // for a given max_len (the runner always passes its max_ctx); splits past a shorter
 // sequence's length are empty and carry zero weight in the merge.
 // bf16 caches take twice the keys per step (8 elements per lane), so their split count is
@@ -895,7 +858,7 @@ jas_status attn_decode_impl(const float *q, const void *K, const void *V, float 
     JAS_CHECK(ns == 1 || (work && ctr), JAS_ERR_INVALID, "jas_attn_decode: workspace and counters required");
     JAS_CHECK(o_packed_d <= 0 || (B <= 16 && o_packed_d == H * D), JAS_ERR_INVALID, "attn_decode: bad packed output");
     DecodeArgs p{q, K, V, O, seqlens, (float *)work, ctr, k_sb, k_sh, B, H, ns, chunk, scale * 1.4426950408889634f,
-                 o_packed_d, max_len};
+                 o_packed_d};
     dim3 grid(ns, B * H);
 #define JAS_DEC(DD)                                                                                  \
     if (D == DD) {                                                                                   \
