@@ -667,6 +667,23 @@ def test_rope_llama(jas):
     close(dx.numpy(), want, atol=1e-6, rtol=1e-6)
 
 
+def test_hbm_read_probe(jas):
+    """The bandwidth calibration reads its buffer and writes its 4-byte sink only when the
+    folded data equal a fixed constant (seeded normal data do not); bad arguments are
+    rejected before any launch."""
+    n = 1 << 20
+    buf = jas.DeviceArray((n,))
+    jas.check(jas.lib.jas_fill_normal(buf.p, n, 7, 0, 0.0, 1.0, None))
+    sink = jas.to_device(np.array([12345], np.uint32))
+    for wgs, u, nt in ((1, 4, 1), (300, 8, 0), (2048, 8, 1)):
+        jas.check(jas.lib.jas_hbm_read_probe(buf.p, 4 * n, wgs, u, nt, sink.p, None))
+    jas.check(jas.lib.jas_synchronize(None))
+    assert int(sink.numpy()[0]) == 12345
+    for args in ((buf.p, 4 * n + 4, 64, 8, 1), (buf.p, 4 * n, 0, 8, 1), (buf.p, 4 * n, 64, 5, 1), (None, 4 * n, 64, 8, 1)):
+        with pytest.raises(jas.JasError):
+            jas.check(jas.lib.jas_hbm_read_probe(*args, sink.p, None))
+
+
 def test_embed_argmax_fill(jas):
     V, d, n = 50, 16, 7
     wte, wpe = normal((V, d), 42, 0), normal((20, d), 42, 1)
