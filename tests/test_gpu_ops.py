@@ -272,11 +272,14 @@ def test_column_layernorm_jasmine(jas):
 
 
 @pytest.mark.parametrize("mode", ["ln", "rms", "softmax"])
-@pytest.mark.parametrize("R,Cc", [(512, 100), (130, 37), (1000, 64), (3, 5), (4096, 130)])
+@pytest.mark.parametrize("R,Cc", [(512, 100), (130, 37), (1000, 64), (3, 5), (4096, 130), (5000, 64), (1000, 1024),
+                                  (3000, 2048), (7, 1028)])
 def test_column_row_ops(jas, mode, R, Cc):
     """Vectors down the columns of a row-major [R, Cc] matrix (element stride Cc): the
-    column kernels (64 vectors per workgroup, rows split over waves) against the oracle's
-    row functions on the transposed matrix."""
+    column kernels against the oracle's row functions on the transposed matrix.  Column
+    counts that are multiples of 4 take the 16-byte column-group kernel (8 vectors per
+    workgroup below 1024 columns, 16 from 1024; elements held in registers up to 4096 / 2048
+    rows, streamed past that: (5000, 64) and (3000, 2048)); the others the one-float form."""
     x = normal((R, Cc), 34, 0)
     xt = np.ascontiguousarray(x.T)
     gam, bet = normal(R, 34, 1), normal(R, 34, 2)
