@@ -16,6 +16,7 @@
 #include <cfloat>
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 #include <unordered_map>
 
 namespace jas {
@@ -586,6 +587,29 @@ __device__ __forceinline__ long decode_out_index(const DecodeArgs &p, int bh, in
     return ((long)(k >> 4) * 64 + b + 16 * ((k & 15) >> 2)) * 4 + (k & 3);
 }
 
+// Sum over the TPK lanes of a key group (TPK = 4, 8, 16 or 32 adjacent lanes), every lane
+// receiving the sum, in registers: DPP quad permutes (lane ^ 1, lane ^ 2), then the 8- and
+// 16-lane mirrors within a row (each quad, then each half row, meets its partner), then the
+// 16-lane row swap across a 32-lane group -- instead of a chain of LDS permutes.  Each step
+// adds two values in either order, so all lanes of a group hold the same bits.
+template <int TPK>
+__device__ __forceinline__ float group_sum(float v)
+{
+    static_assert(TPK == 4 || TPK == 8 || TPK == 16 || TPK == 32, "key group width");
+    auto dpp = [](float x, auto ctrl) {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value, 0xf, 0xf, false));
+    };
+    v += dpp(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1, 0, 3, 2]
+    v += dpp(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2, 3, 0, 1]
+    if constexpr (TPK >= 8) v += dpp(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
+    if constexpr (TPK >= 16) v += dpp(v, std::integral_constant<int, 0x140>{});  // row_mirror
+    if constexpr (TPK >= 32) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    return v;
+}
+
 // Merges the nsplit partials (max, sum, weighted values) of pair bh into its output element
 // tid.  Eight splits' triples are requested at a time; with at most eight splits the whole
 // merge is one memory round trip.  The sums keep split order.
@@ -680,8 +704,7 @@ __global__ void __launch_bounds__(WPB * 64) attn_decode_kernel(const DecodeArgs 
             float d = q[0] * elem(kv[u], 0);
 #pragma unroll
             for (int e = 1; e < EPL; ++e) d += q[e] * elem(kv[u], e);
-#pragma unroll
-            for (int o = TPK / 2; o > 0; o >>= 1) d += __shfl_xor(d, o, WAVE);
+            d = group_sum<TPK>(d);
             sc[u] = (kk + u * NG) < k1 ? d : -FLT_MAX;
         }
         float mx = m;
