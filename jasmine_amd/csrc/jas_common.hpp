@@ -79,18 +79,35 @@ __device__ __forceinline__ floatx4 widen_bf16x4(u32x2 u)
                    __uint_as_float(u.y & 0xffff0000u)};
 }
 
-// ---- wave64 reductions (DPP/permute lowered by the compiler from shfl_xor) ----
+// ---- wave64 reductions in registers ----
+// Partners meet through DPP within a 16-lane row (quad permutes lane ^ 1 and lane ^ 2, then
+// the half-row and row mirrors) and through the gfx950 row swaps across rows
+// (v_permlane16_swap, v_permlane32_swap) -- no LDS permutes.  Every step combines two values
+// in either order, so all 64 lanes end with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+template <typename Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op)
+{
+    v = op(v, dpp_f32<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+    v = op(v, dpp_f32<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+    v = op(v, dpp_f32<0x141>(v));  // row_half_mirror
+    v = op(v, dpp_f32<0x140>(v));  // row_mirror
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
 __device__ __forceinline__ float wave_sum(float v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
-    return v;
+    return wave_reduce(v, [](float a, float b) { return a + b; });
 }
 __device__ __forceinline__ float wave_max(float v)
 {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
-    return v;
+    return wave_reduce(v, [](float a, float b) { return fmaxf(a, b); });
 }
 __device__ __forceinline__ double wave_sum_d(double v)
 {
