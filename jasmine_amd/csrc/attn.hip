@@ -735,13 +735,9 @@ __global__ void __launch_bounds__(WPB * 64) attn_decode_kernel(const DecodeArgs 
     __shared__ float sf[NG], sML[2];
     if (w == 0) {
         const float mg = lane < NG ? sm[lane] : -FLT_MAX;
-        float M = mg;
-#pragma unroll
-        for (int o = WAVE / 2; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, WAVE));
+        const float M = wave_max(mg);
         const float f = (lane < NG && mg != -FLT_MAX) ? exp2f(mg - M) : 0.f;
-        float L = lane < NG ? sl[lane] * f : 0.f;
-#pragma unroll
-        for (int o = WAVE / 2; o > 0; o >>= 1) L += __shfl_xor(L, o, WAVE);
+        const float L = wave_sum(lane < NG ? sl[lane] * f : 0.f);
         if (lane < NG) sf[lane] = f;
         if (lane == 0) { sML[0] = M; sML[1] = L; }
     }
