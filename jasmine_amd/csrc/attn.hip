@@ -130,7 +130,7 @@ __device__ __forceinline__ bool fa_work_item(int nqb, int BH, int nsplit, int fo
 // the rescale needs no cross-lane traffic; the reduction index of each product is permuted
 // identically in both operands so that S lands in the P operand's registers with no shuffle.
 template <int D, bool BF16, int BK, int NW = FA_WAVES>
-__global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArgs p)
+__global__ void __launch_bounds__(64 * NW, (NW == 8 && D <= 64) ? 4 : 1) flash_prefill_kernel(const PrefillArgs p)
 {
     constexpr int FA_NW = NW, FA_BQ = 16 * FA_NW;
     constexpr int NT = 64 * FA_NW;
@@ -232,7 +232,15 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
         const int idx = tid + it * NT, key = idx / CPR, ch = idx % CPR;                    \
         if (NCH % NT != 0 && idx >= NCH) break;                                            \
         *(u32x4 *)(&Ks[BUF][key * KLD + ch * EPC]) = KR[it];                               \
-        *(u32x4 *)(&Vt[BUF][key * KLDV + ch * EPC]) = VR[it];                              \
+        if constexpr (BF16) {                                                                   \
+            *(u32x4 *)(&Vt[BUF][key * KLDV + ch * EPC]) = VR[it];                              \
+        } else { /* fp32 V rows interleaved: element d at (d % 16) * NC + d / 16 */            \
+            _Pragma("unroll") for (int e = 0; e < 4; ++e)                                      \
+            {                                                                                  \
+                const int d = ch * EPC + e;                                                    \
+                Vt[BUF][key * KLDV + (d % 16) * NC + d / 16] = __uint_as_float(VR[it][e]);    \
+            }                                                                                  \
+        }                                                                                      \
     }
 
     // Pipeline: tile t is computed from LDS buffer t%2 while tile t+1 waits in registers
@@ -414,14 +422,30 @@ __global__ void __launch_bounds__(64 * NW) flash_prefill_kernel(const PrefillArg
             }
             // O[q][d = 16c + n] += sum_key P[q][key] V[key][d]: in product t of key block j the
             // lanes of group g contribute key 16j + 4g + t -- their own score s[j][t] as A and
-            // V[16j + 4g + t][16c + n] (one float, consecutive across n) as B
+            // V[16j + 4g + t][16c + n] as B.  The staged V rows are interleaved (element d at
+            // (d % 16) * NC + d / 16), so a lane's NC values for c = 0..NC-1 are adjacent: one
+            // 16-byte LDS read per four of them instead of one read per value
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    const float *vrow = Vc + (16 * j + 4 * g + t) * KLDV + r16;
+                    const float *vrow = Vc + (16 * j + 4 * g + t) * KLDV + r16 * NC;
+                    float vv[NC];
+                    if constexpr (NC % 4 == 0) {
 #pragma unroll
-                    for (int c = 0; c < NC; ++c) oacc[c] = mfma4(s[j][t], vrow[16 * c], oacc[c]);
+                        for (int c = 0; c < NC; c += 4) {
+                            const float4 f = *(const float4 *)(vrow + c);
+                            vv[c] = f.x, vv[c + 1] = f.y, vv[c + 2] = f.z, vv[c + 3] = f.w;
+                        }
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < NC; c += 2) {
+                            const float2 f = *(const float2 *)(vrow + c);
+                            vv[c] = f.x, vv[c + 1] = f.y;
+                        }
+                    }
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) oacc[c] = mfma4(s[j][t], vv[c], oacc[c]);
                 }
         }
     };
